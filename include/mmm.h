@@ -1,0 +1,132 @@
+/*
+ * mmm.h -- C ABI of the MI355X (gfx950) FP16->FP32 GEMM and 5-D tensor contraction.
+ *
+ * Drop-in boundary for the hot path of thrasos-g/RDNA4-GEMM-WMMA.  The reference has no
+ * library or FFI layer: its boundary is the kernel entry
+ *     template<int WAVE_M,int WAVE_N,int WAVES_I,int WAVES_J>
+ *     __global__ void WMMA_Swizzled_Full(_Float16* A, _Float16* B, float* C)   (mmm.cpp:1214-1215)
+ * launched as <<<dim3(ceil(DIM_J/BLOCK_N), ceil(DIM_I/BLOCK_M)), dim3(32, WAVES_I*WAVES_J)>>>
+ * on the null stream (mmm.cpp:1471-1472, 1488, 1496), with the problem size in the
+ * compile-time globals DIM_I/DIM_J/DIM_K (mmm.cpp:13-15).  The entry points below keep that
+ * shape -- device pointers, M/N/K and the tile template parameters -- and add what a real
+ * boundary needs: run-time sizes and leading dimensions, a stream, and an error code.
+ *
+ * Conventions (all entry points):
+ *  - fp16 tensors are passed as pointers to IEEE binary16 bit patterns (mmm_half).
+ *  - Pointers are device pointers owned by the caller.  No entry point allocates device
+ *    memory, synchronises the host, or exits the process.
+ *  - C is overwritten (alpha = 1, beta = 0, as mmm.cpp:1512-1513 and the kernel's store at
+ *    mmm.cpp:1370); C is never read.
+ *  - Errors: hipErrorInvalidValue for null pointers, negative sizes or leading dimensions
+ *    smaller than the row length; a launch error is returned as the runtime reports it.
+ *    M == 0 or N == 0 is a no-op; K == 0 writes zeros to C.
+ *  - Work is enqueued on `stream` (0 = the null stream, as the reference) and is
+ *    asynchronous, as the reference's launches are (the caller synchronises, mmm.cpp:1491).
+ *  - Thread safety: the library keeps no mutable global state.
+ */
+#ifndef MMM_H
+#define MMM_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t mmm_half; /* IEEE binary16 bit pattern */
+
+/*
+ * C[M][N] (fp32, row-major, ldc) = A[M][K] (fp16, row-major, lda) * B[K][N] (fp16, row-major, ldb).
+ * fp32 accumulation.  Leading dimensions are in elements.
+ * Replaces: WMMA_Swizzled_Full<2,2,4,4><<<..>>>(dA, dB, dC) with DIM_I = M, DIM_J = N,
+ * DIM_K = K (mmm.cpp:1461-1472, 1496) -- the templated lineage mmm.cpp:694-1374.  Unlike
+ * the reference's unmasked kernel, any M, N, K and any leading dimensions are accepted
+ * (the ragged shapes the tensor variant masks at mmmTensor.cpp:135-178, 246).
+ */
+hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                           int64_t ldb, int64_t ldc, hipStream_t stream);
+
+/*
+ * As mmm_gemm_f16f32, with the tile shape chosen by the caller through the reference's
+ * template parameters (mmm.cpp:694-695, 1462-1465), reinterpreted for wave64 MFMA:
+ *   WAVE_M, WAVE_N   -- 32x32 MFMA tiles per wave along M and N (the reference counts
+ *                       16x16 WMMA tiles);
+ *   WAVES_I, WAVES_J -- waves per workgroup along M and N.
+ * Block tile = (WAVES_I*WAVE_M*32) x (WAVES_J*WAVE_N*32), K step 64.
+ * Instantiated shapes (WAVE_M,WAVE_N,WAVES_I,WAVES_J): (4,4,2,2) 256x256, (2,4,2,2) 128x256,
+ * (4,2,2,2) 256x128, (2,2,2,2) 128x128.  Others return hipErrorInvalidValue.
+ */
+hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
+                                 int64_t lda, int64_t ldb, int64_t ldc, int wave_m, int wave_n, int waves_i,
+                                 int waves_j, hipStream_t stream);
+
+/*
+ * 5-D tensor contraction descriptor.  Each GEMM axis (m, n, k) is a pair of sub-indices
+ * (hi, lo), folded as  m = m_hi * m_ext[1] + m_lo  (same for n and k), and each operand
+ * gives an element stride for every sub-index it carries:
+ *   A(m, k) = A[m_hi*a_m_stride[0] + m_lo*a_m_stride[1] + k_hi*a_k_stride[0] + k_lo*a_k_stride[1]]
+ *   B(k, n) = B[k_hi*b_k_stride[0] + k_lo*b_k_stride[1] + n_hi*b_n_stride[0] + n_lo*b_n_stride[1]]
+ *   C(m, n) = C[m_hi*c_m_stride[0] + m_lo*c_m_stride[1] + n_hi*c_n_stride[0] + n_lo*c_n_stride[1]]
+ *   C(m, n) = sum_k A(m, k) * B(k, n)   (fp32 accumulate, overwrite)
+ * The fold and any index permutation are applied in the kernels' address generation; no
+ * operand is repacked or transposed in memory.
+ */
+typedef struct mmm_contract_desc {
+    int64_t m_ext[2], n_ext[2], k_ext[2];
+    int64_t a_m_stride[2], a_k_stride[2];
+    int64_t b_k_stride[2], b_n_stride[2];
+    int64_t c_m_stride[2], c_n_stride[2];
+} mmm_contract_desc;
+
+/*
+ * Descriptor for C[b,i,j] = sum_{k,l} A[b,i,k,l] * B[k,l,j], all dense in the listed index
+ * order: m = (b, i), k = (k, l), n = j.  This is the contraction of the benchmark
+ * configuration; the reference has no such preset (its only contraction is the one below).
+ */
+hipError_t mmm_contract_desc_baseline(mmm_contract_desc* d, int b, int i, int k, int l, int j);
+
+/*
+ * Descriptor for the reference's contraction (mmmTensor.cpp:20-28):
+ *   Out[m][b][r] = sum_{n,l} G[r][n][m][l] * Input[b][n][l]
+ * with G [rt][nt][mt][rt_l], Input [bt][nt][rt_l], Out [mt][bt][rt]:  GEMM m = (m, r),
+ * k = (n, l), n = b.  This replaces the reference's host pack of G (mmmTensor.cpp:329-340),
+ * its TN read of Input (mmmTensor.cpp:168) and its output remap (mmmTensor.cpp:246-252).
+ */
+hipError_t mmm_contract_desc_reference(mmm_contract_desc* d, int mt, int bt, int rt, int nt, int rt_l);
+
+/*
+ * Runs the contraction described by d.  Replaces the tensor variant
+ * WMMA_Swizzled_Full<2,2,4,4><<<..>>>(dA, d_Input, d_Output) (mmmTensor.cpp:44-257, launch
+ * mmmTensor.cpp:354-371) together with the host pack it needs (mmmTensor.cpp:329-343).
+ */
+hipError_t mmm_contract5d_f16f32(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
+                                 hipStream_t stream);
+
+/*
+ * Seeded synthetic inputs, generated on the device (the reference fills with unseeded
+ * rand()/RAND_MAX on the host, mmm.cpp:1409-1414; these are reproducible instead):
+ *   key = splitmix64(seed * 0x9E3779B97F4A7C15 + tensor_id + 1), x_i = splitmix64(key + i)
+ *   uniform: (x_i >> 40) * 2^-23 - 1  in [-1, 1), rounded to fp16 (RNE)
+ *   normal:  Box-Muller on x_{2i}, x_{2i+1} in fp64, times scale, rounded to fp16 (RNE)
+ */
+hipError_t mmm_fill_uniform_f16(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream);
+hipError_t mmm_fill_normal_f16(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, double scale,
+                               hipStream_t stream);
+
+/*
+ * Host-side query of the tile scheduler: the output tile (tm, tn) computed by workgroup
+ * `block` of a launch with tiles_m x tiles_n tiles.  Lets callers and tests check that every
+ * tile is computed exactly once (the reference's remap, mmm.cpp:1219-1236, is not a
+ * bijection for every grid).  Returns hipErrorInvalidValue for out-of-range arguments.
+ */
+hipError_t mmm_tile_of_block(int block, int tiles_m, int tiles_n, int* tm, int* tn);
+
+/* Library version string. */
+const char* mmm_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MMM_H */

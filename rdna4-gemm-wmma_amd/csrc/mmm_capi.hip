@@ -1,0 +1,307 @@
+// C ABI of the MI355X GEMM / contraction library (declarations and reference citations in
+// include/mmm.h): argument validation, kernel selection, contraction descriptors, and the
+// seeded on-device input generator.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mmm.h"
+#include "mmm_kernels.h"
+#include "mmm_tile_map.h"
+
+namespace mmm {
+
+// ---------------------------------------------------------------- seeded input generator
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__host__ __device__ inline uint64_t stream_key(uint64_t seed, uint32_t tensor_id) {
+  uint64_t z = seed * 0x9E3779B97F4A7C15ull + (uint64_t)tensor_id + 1ull;
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// fp64 -> fp16 with a single round-to-nearest-even (integer arithmetic, no fp32 detour).
+__device__ __forceinline__ uint16_t f64_to_f16_rne(double d) {
+  const uint64_t x = __builtin_bit_cast(uint64_t, d);
+  const uint16_t sign = (uint16_t)((x >> 48) & 0x8000u);
+  const uint64_t ax = x & 0x7fffffffffffffffull;
+  if (ax >= 0x7ff0000000000000ull) return sign | (ax == 0x7ff0000000000000ull ? 0x7c00u : 0x7e00u);
+  if (ax >= 0x40effe0000000000ull) return sign | 0x7c00u;  // >= 65520 rounds to inf
+  const int e = (int)(ax >> 52) - 1023;
+  if (e >= -14) {
+    const uint64_t mant = ax & 0xfffffffffffffull;
+    uint64_t h = ((uint64_t)(e + 15) << 10) | (mant >> 42);
+    const uint64_t rem = mant & ((1ull << 42) - 1ull);
+    if (rem > (1ull << 41) || (rem == (1ull << 41) && (h & 1ull))) h++;
+    return sign | (uint16_t)h;
+  }
+  if (e < -1022) return sign;
+  const uint64_t mant = (ax & 0xfffffffffffffull) | (1ull << 52);
+  const int shift = 28 - e;
+  if (shift > 53) return sign;
+  uint64_t h = mant >> shift;
+  const uint64_t rem = mant & ((1ull << shift) - 1ull);
+  const uint64_t half = 1ull << (shift - 1);
+  if (rem > half || (rem == half && (h & 1ull))) h++;
+  return sign | (uint16_t)h;
+}
+
+__global__ void fill_uniform_kernel(mmm_half* out, int64_t n, uint64_t key) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint64_t x = splitmix64(key + (uint64_t)i);
+    const float v = (float)(uint32_t)(x >> 40) * 1.1920928955078125e-07f - 1.0f;  // exact
+    out[i] = __builtin_bit_cast(uint16_t, (_Float16)v);                            // v_cvt_f16_f32, RNE
+  }
+}
+
+__global__ void fill_normal_kernel(mmm_half* out, int64_t n, uint64_t key, double scale) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint64_t x1 = splitmix64(key + 2ull * (uint64_t)i);
+    const uint64_t x2 = splitmix64(key + 2ull * (uint64_t)i + 1ull);
+    const double u1 = (double)((x1 >> 11) + 1ull) * 1.1102230246251565e-16;
+    const double u2 = (double)(x2 >> 11) * 1.1102230246251565e-16;
+    const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+    out[i] = f64_to_f16_rne(z * scale);
+  }
+}
+
+static unsigned fill_blocks(int64_t n) {
+  int64_t b = (n + 255) / 256;
+  if (b > 65536) b = 65536;
+  return (unsigned)(b < 1 ? 1 : b);
+}
+
+hipError_t launch_fill_uniform(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream) {
+  hipLaunchKernelGGL(fill_uniform_kernel, dim3(fill_blocks(n)), dim3(256), 0, stream, out, n,
+                     stream_key(seed, tensor_id));
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, double scale,
+                              hipStream_t stream) {
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(fill_blocks(n)), dim3(256), 0, stream, out, n,
+                     stream_key(seed, tensor_id), scale);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- zero fill (K == 0)
+__global__ void zero_kernel(float* C, int M, int N, int64_t ldc) {
+  const int64_t total = (int64_t)M * N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride)
+    C[(i / N) * ldc + (i % N)] = 0.0f;
+}
+
+__global__ void zero_fold_kernel(FoldProblem p) {
+  const int64_t total = (int64_t)p.M * p.N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int m = (int)(i / p.N), n = (int)(i % p.N);
+    const int64_t off = (int64_t)(m / p.m_lo) * p.cm[0] + (int64_t)(m % p.m_lo) * p.cm[1] +
+                        (int64_t)(n / p.n_lo) * p.cn[0] + (int64_t)(n % p.n_lo) * p.cn[1];
+    p.C[off] = 0.0f;
+  }
+}
+
+hipError_t launch_zero_f32(float* C, int M, int N, int64_t ldc, hipStream_t stream) {
+  hipLaunchKernelGGL(zero_kernel, dim3(fill_blocks((int64_t)M * N)), dim3(256), 0, stream, C, M, N, ldc);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream) {
+  hipLaunchKernelGGL(zero_fold_kernel, dim3(fill_blocks((int64_t)p.M * p.N)), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- tile selection
+// Estimated cost of a tile shape: rounds of 256 concurrent workgroups (one per CU) times
+// the work per tile over the tile's relative MFMA efficiency (larger wave tiles read less
+// LDS per MAC).
+static int pick_tile(int M, int N) {
+  struct Cand {
+    int id, bm, bn;
+    double eff;
+  };
+  const Cand cands[] = {{kTile256x256, 256, 256, 1.0},
+                        {kTile256x128, 256, 128, 0.85},
+                        {kTile128x256, 128, 256, 0.85},
+                        {kTile128x128, 128, 128, 0.70}};
+  int best = kTile256x256;
+  double best_cost = 1e300;
+  for (const Cand& c : cands) {
+    const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const int64_t rounds = (tiles + 255) / 256;
+    const double cost = (double)rounds * c.bm * c.bn / c.eff;
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = c.id;
+    }
+  }
+  return best;
+}
+
+static hipError_t check_gemm(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                             int64_t ldb, int64_t ldc) {
+  if (M < 0 || N < 0 || K < 0) return hipErrorInvalidValue;
+  if (M == 0 || N == 0) return hipSuccess;
+  if (!C) return hipErrorInvalidValue;
+  if (K > 0 && (!A || !B)) return hipErrorInvalidValue;
+  if (lda < K || ldb < N || ldc < N) return hipErrorInvalidValue;
+  return hipSuccess;
+}
+
+static int tile_from_params(int wave_m, int wave_n, int waves_i, int waves_j) {
+  if (waves_i != 2 || waves_j != 2) return -1;
+  if (wave_m == 4 && wave_n == 4) return kTile256x256;
+  if (wave_m == 2 && wave_n == 4) return kTile128x256;
+  if (wave_m == 4 && wave_n == 2) return kTile256x128;
+  if (wave_m == 2 && wave_n == 2) return kTile128x128;
+  return -1;
+}
+
+static bool collapse(int64_t ext_hi, int64_t ext_lo, int64_t s_hi, int64_t s_lo, int64_t* stride) {
+  if (ext_hi <= 1) {
+    *stride = s_lo;
+    return true;
+  }
+  if (ext_lo <= 1) {
+    *stride = s_hi;
+    return true;
+  }
+  if (s_hi == ext_lo * s_lo) {
+    *stride = s_lo;
+    return true;
+  }
+  return false;
+}
+
+}  // namespace mmm
+
+using namespace mmm;
+
+extern "C" {
+
+hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                           int64_t ldb, int64_t ldc, hipStream_t stream) {
+  hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
+  if (e != hipSuccess || M == 0 || N == 0) return e;
+  if (K == 0) return launch_zero_f32(C, M, N, ldc, stream);
+  GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false};
+  return launch_gemm_nn(p, pick_tile(M, N), stream);
+}
+
+hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
+                                 int64_t lda, int64_t ldb, int64_t ldc, int wave_m, int wave_n, int waves_i,
+                                 int waves_j, hipStream_t stream) {
+  const int tile = tile_from_params(wave_m, wave_n, waves_i, waves_j);
+  if (tile < 0) return hipErrorInvalidValue;
+  hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
+  if (e != hipSuccess || M == 0 || N == 0) return e;
+  if (K == 0) return launch_zero_f32(C, M, N, ldc, stream);
+  GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false};
+  return launch_gemm_nn(p, tile, stream);
+}
+
+hipError_t mmm_contract_desc_baseline(mmm_contract_desc* d, int b, int i, int k, int l, int j) {
+  if (!d || b < 0 || i < 0 || k < 0 || l < 0 || j < 0) return hipErrorInvalidValue;
+  // A[b,i,k,l]: m = (b, i), k = (k, l).  B[k,l,j]: n = (1, j).  C[b,i,j].
+  *d = mmm_contract_desc{};
+  d->m_ext[0] = b, d->m_ext[1] = i;
+  d->k_ext[0] = k, d->k_ext[1] = l;
+  d->n_ext[0] = 1, d->n_ext[1] = j;
+  d->a_m_stride[0] = (int64_t)i * k * l, d->a_m_stride[1] = (int64_t)k * l;
+  d->a_k_stride[0] = l, d->a_k_stride[1] = 1;
+  d->b_k_stride[0] = (int64_t)l * j, d->b_k_stride[1] = j;
+  d->b_n_stride[0] = j, d->b_n_stride[1] = 1;
+  d->c_m_stride[0] = (int64_t)i * j, d->c_m_stride[1] = j;
+  d->c_n_stride[0] = j, d->c_n_stride[1] = 1;
+  return hipSuccess;
+}
+
+hipError_t mmm_contract_desc_reference(mmm_contract_desc* d, int mt, int bt, int rt, int nt, int rt_l) {
+  if (!d || mt < 0 || bt < 0 || rt < 0 || nt < 0 || rt_l < 0) return hipErrorInvalidValue;
+  // G[r][n][m][l] as A(m', k') with m' = (m, r), k' = (n, l)          (mmmTensor.cpp:329-340)
+  // Input[b][n][l] as B(k', b): k' = (n, l) contiguous, n = b          (mmmTensor.cpp:168)
+  // Out[m][b][r] as C(m', b)                                           (mmmTensor.cpp:251)
+  *d = mmm_contract_desc{};
+  d->m_ext[0] = mt, d->m_ext[1] = rt;
+  d->k_ext[0] = nt, d->k_ext[1] = rt_l;
+  d->n_ext[0] = 1, d->n_ext[1] = bt;
+  d->a_m_stride[0] = rt_l, d->a_m_stride[1] = (int64_t)nt * mt * rt_l;
+  d->a_k_stride[0] = (int64_t)mt * rt_l, d->a_k_stride[1] = 1;
+  d->b_k_stride[0] = rt_l, d->b_k_stride[1] = 1;
+  d->b_n_stride[0] = (int64_t)bt * nt * rt_l, d->b_n_stride[1] = (int64_t)nt * rt_l;
+  d->c_m_stride[0] = (int64_t)bt * rt, d->c_m_stride[1] = 1;
+  d->c_n_stride[0] = (int64_t)bt * rt, d->c_n_stride[1] = rt;
+  return hipSuccess;
+}
+
+hipError_t mmm_contract5d_f16f32(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
+                                 hipStream_t stream) {
+  if (!d) return hipErrorInvalidValue;
+  for (int q = 0; q < 2; ++q)
+    if (d->m_ext[q] < 0 || d->n_ext[q] < 0 || d->k_ext[q] < 0) return hipErrorInvalidValue;
+  const int64_t M = d->m_ext[0] * d->m_ext[1], N = d->n_ext[0] * d->n_ext[1], K = d->k_ext[0] * d->k_ext[1];
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return hipErrorInvalidValue;
+  if (M == 0 || N == 0) return hipSuccess;
+  if (!C || (K > 0 && (!A || !B))) return hipErrorInvalidValue;
+
+  // A fold that is a plain row-major GEMM runs on the GEMM kernels (the benchmark's
+  // A[b,i,k,l] x B[k,l,j] -> C[b,i,j] is one: M = b*i, K = k*l, N = j).
+  int64_t am, ak, bk, bn, cm, cn;
+  const bool plain = collapse(d->m_ext[0], d->m_ext[1], d->a_m_stride[0], d->a_m_stride[1], &am) &&
+                     collapse(d->k_ext[0], d->k_ext[1], d->a_k_stride[0], d->a_k_stride[1], &ak) && ak == 1 &&
+                     collapse(d->k_ext[0], d->k_ext[1], d->b_k_stride[0], d->b_k_stride[1], &bk) &&
+                     collapse(d->n_ext[0], d->n_ext[1], d->b_n_stride[0], d->b_n_stride[1], &bn) && bn == 1 &&
+                     collapse(d->m_ext[0], d->m_ext[1], d->c_m_stride[0], d->c_m_stride[1], &cm) &&
+                     collapse(d->n_ext[0], d->n_ext[1], d->c_n_stride[0], d->c_n_stride[1], &cn) && cn == 1 &&
+                     am >= K && bk >= N && cm >= N;
+  if (plain) return mmm_gemm_f16f32(A, B, C, (int)M, (int)N, (int)K, am, bk, cm, stream);
+
+  FoldProblem p{};
+  p.A = A, p.B = B, p.C = C;
+  p.M = (int)M, p.N = (int)N, p.K = (int)K;
+  p.m_lo = (int)(d->m_ext[1] > 0 ? d->m_ext[1] : 1);
+  p.n_lo = (int)(d->n_ext[1] > 0 ? d->n_ext[1] : 1);
+  p.k_lo = (int)(d->k_ext[1] > 0 ? d->k_ext[1] : 1);
+  for (int q = 0; q < 2; ++q) {
+    p.am[q] = d->a_m_stride[q], p.ak[q] = d->a_k_stride[q];
+    p.bk[q] = d->b_k_stride[q], p.bn[q] = d->b_n_stride[q];
+    p.cm[q] = d->c_m_stride[q], p.cn[q] = d->c_n_stride[q];
+  }
+  if (K == 0) return launch_zero_fold(p, stream);
+  return launch_gemm_fold(p, stream);
+}
+
+hipError_t mmm_fill_uniform_f16(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream) {
+  if (n < 0 || (n > 0 && !out)) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  return launch_fill_uniform(out, n, seed, tensor_id, stream);
+}
+
+hipError_t mmm_fill_normal_f16(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, double scale,
+                               hipStream_t stream) {
+  if (n < 0 || (n > 0 && !out)) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  return launch_fill_normal(out, n, seed, tensor_id, scale, stream);
+}
+
+hipError_t mmm_tile_of_block(int block, int tiles_m, int tiles_n, int* tm, int* tn) {
+  if (!tm || !tn || tiles_m <= 0 || tiles_n <= 0) return hipErrorInvalidValue;
+  if ((int64_t)tiles_m * tiles_n > 0x7fffffff) return hipErrorInvalidValue;
+  if (block < 0 || block >= tiles_m * tiles_n) return hipErrorInvalidValue;
+  tile_of_block(block, tiles_m, tiles_n, 4, tm, tn);
+  return hipSuccess;
+}
+
+const char* mmm_version(void) { return "mmm-gfx950 0.1.0"; }
+
+}  // extern "C"

@@ -1,0 +1,559 @@
+// MI355X (gfx950, CDNA4, wave64) FP16->FP32 GEMM kernels.
+//
+// Computes C[M][N] = A[M][K] * B[K][N] (fp16 in, fp32 accumulate and out, row-major), the
+// operation of the reference's templated WMMA lineage (mmm.cpp:694-1374; definition at
+// mmm.cpp:52-62).  The design is CDNA4's own, not a translation of the RDNA4 kernel:
+//
+//  * Math: v_mfma_f32_32x32x16_f16 (one wave, 32x32 outputs, K 16 per instruction).  The
+//    MFMA operands are issued swapped (B fragment as src A, A fragment as src B), so the
+//    accumulator holds C^T: lane l owns row m = l%32 and, for accumulator v, column
+//    n = 8*(v/4) + 4*(l/32) + v%4 -- four consecutive columns per lane, stored as float4.
+//  * Block tile BM x BN with K step 64, WGM x WGN waves, each wave (BM/WGM) x (BN/WGN).
+//    The default 256x256 tile with 2x2 waves gives every wave 4x4 MFMA tiles (256 fp32
+//    accumulators, held in AGPRs), i.e. 32 MACs per LDS byte read -- twice what the
+//    MFMA rate needs from LDS.
+//  * Operand staging: HBM -> LDS by buffer_load_dwordx4 ... lds (direct to LDS, no VGPR
+//    round trip), double-buffered (2 x 64 KB of the 160 KB LDS).  Out-of-range rows and
+//    the K tail read as zero through the buffer descriptor's range check.
+//  * LDS layouts and swizzles (16-byte chunks, chosen for CDNA4's 64-bank LDS):
+//      A stage [BM][64] fp16, row = 8 chunks, chunk c of row m at c ^ fA(m),
+//          fA(m) = (m & 7) ^ ((m >> 3) & 3): 16 consecutive rows at one chunk hit 16
+//          distinct 16-byte bank groups (ds_read_b128 conflict-free).
+//      B stage [64][BN] fp16 (N contiguous, as in HBM), chunk c of row k at c ^ gB(k & 3),
+//          gB = {0, 6, 10, 12}: the 4 rows x 4 chunks that 32 lanes of one
+//          ds_read_b64_tr_b16 touch land in 16 distinct bank groups.
+//    The A fragment is one ds_read_b128 (8 consecutive k of one row).  The B fragment needs
+//    8 consecutive k of one column of an N-contiguous tile: two ds_read_b64_tr_b16, which
+//    transpose 4x16 blocks across each 16-lane group (lane i receives column i of the 4
+//    rows that lanes 4e + i/4 address).
+//  * Workgroup -> tile: XCD-aware, L2-grouped bijection (mmm_tile_map.h).
+//
+// A second instantiation of the same kernel ("generic") stages through VGPRs with
+// element-wise masked loads; it serves leading dimensions or pointers that are not
+// 16-byte aligned (e.g. the ragged 4097 x 4095 x 4111 configuration) and arbitrary K.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mmm.h"
+#include "mmm_kernels.h"
+#include "mmm_tile_map.h"
+
+namespace mmm {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define LDS_AS __attribute__((address_space(3)))
+
+// Buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format, no swizzle).
+constexpr int kRsrcWord3 = 0x00020000;
+// Byte offset used for masked-off chunks; every descriptor's range is clipped below it.
+constexpr uint32_t kOobOffset = 0x7ffffff0u;
+
+template <int BM_, int BN_, int WGM_, int WGN_>
+struct Tile {
+  static constexpr int BM = BM_, BN = BN_, BK = 64, WGM = WGM_, WGN = WGN_;
+  static constexpr int NT = 64 * WGM * WGN;
+  static constexpr int TM = BM / WGM, TN = BN / WGN;
+  static constexpr int FM = TM / 32, FN = TN / 32;
+  static constexpr int CA = BK / 8;  // 16-byte chunks per A row (8)
+  static constexpr int CB = BN / 8;  // 16-byte chunks per B row
+  static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int RA = BM * CA / NT;  // A chunks per thread per stage
+  static constexpr int RB = BK * CB / NT;  // B chunks per thread per stage
+  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32x32");
+  static_assert(CB >= 16, "B swizzle needs rows of at least 16 chunks (BN >= 128)");
+  static_assert((BM * CA) % NT == 0 && (BK * CB) % NT == 0, "chunks must divide evenly over threads");
+  static_assert(2 * STAGE <= 160 * 1024, "double-buffered stages must fit the 160 KB LDS");
+};
+
+__device__ __forceinline__ int swz_a(int m) { return (m & 7) ^ ((m >> 3) & 3); }
+__device__ __forceinline__ int swz_b(int k) { return (0xCA60 >> (4 * (k & 3))) & 15; }  // {0,6,10,12}
+
+__device__ __forceinline__ half8 lds_read_a(const char LDS_AS* p) { return *(const half8 LDS_AS*)p; }
+
+__device__ __forceinline__ half8 lds_read_b_tr(const char LDS_AS* p_lo, const char LDS_AS* p_hi) {
+  fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)p_lo);
+  fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)p_hi);
+  half4 l4 = __builtin_bit_cast(half4, lo);
+  half4 h4 = __builtin_bit_cast(half4, hi);
+  return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor (base, num_records bytes, word 3) built from uniform values.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t num_records) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)b), __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
+               __builtin_amdgcn_readfirstlane((int)num_records), kRsrcWord3};
+}
+
+// 16 bytes per lane from the buffer at byte offset voff straight into LDS at
+// lds_addr + 16 * lane (buffer_load_dwordx4 ... lds; m0 holds the wave's LDS base).
+// Issued as inline asm so the compiler does not treat every later LDS read as dependent on
+// it: completion is awaited explicitly (vmcnt(0)) before the barrier that publishes the
+// stage.  Out-of-range offsets (>= num_records) write zeros.  DS instructions on gfx9-family
+// targets do not read m0, so overwriting it here is safe.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_b128(uint32_t lds_addr, i32x4 rsrc, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr_of(const char LDS_AS* p) { return (uint32_t)(uintptr_t)p; }
+
+__device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
+  if (bytes <= 0) return 0u;
+  return bytes > (int64_t)kOobOffset ? kOobOffset : (uint32_t)bytes;
+}
+
+// One pass over a 64-deep LDS stage: 4 K-steps of FM x FN MFMAs.
+// BKM = false: B stage is [64][BN] (N contiguous), fragments by two transposing reads;
+//              b_off[nb] addresses fragment nb, K-steps add whole rows.
+// BKM = true : B stage is [BN][64] (K contiguous, swizzled like A), fragments by one
+//              ds_read_b128; b_off[kk] addresses K-step kk, fragments add 32 rows.
+template <class T, bool BKM>
+__device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const char LDS_AS* b_st,
+                                              const uint32_t (&a_off)[4], const uint32_t (&b_off)[4],
+                                              f32x16 (&acc)[T::FM][T::FN]) {
+#pragma unroll
+  for (int kk = 0; kk < T::BK / 16; ++kk) {
+    half8 af[T::FM], bf[T::FN];
+#pragma unroll
+    for (int mb = 0; mb < T::FM; ++mb) af[mb] = lds_read_a(a_st + a_off[kk] + mb * 32 * T::BK * 2);
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb) {
+      if constexpr (BKM)
+        bf[nb] = lds_read_a(b_st + b_off[kk] + nb * 32 * T::BK * 2);
+      else
+        bf[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * 16) * T::BN * 2, b_st + b_off[nb] + (kk * 16 + 4) * T::BN * 2);
+    }
+#pragma unroll
+    for (int mb = 0; mb < T::FM; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < T::FN; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[nb], af[mb], acc[mb][nb], 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void block_sync() { __syncthreads(); }
+
+// GENERIC = false: direct-to-LDS buffer loads; needs lda, ldb, K, N multiples of 8 and
+//                  16-byte-aligned A and B (checked by the host).
+// GENERIC = true : element-wise masked loads through VGPRs; any shape and alignment.
+template <class T, bool GENERIC>
+__global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * T::STAGE];
+
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, 4, &tm, &tn);
+  // The tile origin is uniform; readfirstlane keeps it (and everything derived from it, such
+  // as the buffer descriptors) in SGPRs -- the integer divisions above are expanded on the VALU.
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * T::BM), n0 = __builtin_amdgcn_readfirstlane(tn * T::BN);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / T::WGN, wn = w % T::WGN;
+  const int M = p.M, N = p.N, K = p.K;
+  const int64_t lda = p.lda, ldb = p.ldb;
+
+  // ---- staging map.  Thread (w, lane) moves chunk slot s = r*NT + w*64 + lane of a stage
+  // (r = 0..RA-1 for A, 0..RB-1 for B).  A round of NT slots covers RPA = NT/CA rows of A
+  // and RPB = NT/CB rows of B, so slot rows are row0 + r*RP and the logical chunk (the
+  // swizzle only sees row bits below 5, and RP is a multiple of 4) is the same every round.
+  constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
+  static_assert(RPA % 32 == 0 && RPB % 4 == 0, "round strides must preserve the swizzle");
+  const int a_row0 = w * (64 / T::CA) + lane / T::CA;
+  const int a_kc = 8 * ((lane % T::CA) ^ swz_a(a_row0));
+  const int b_row0 = w * (64 / T::CB) + lane / T::CB;
+  const int b_nc = 8 * ((lane % T::CB) ^ swz_b(b_row0));
+
+  // ---- fragment read offsets (bytes within a stage)
+  uint32_t a_off[4];
+  {
+    const int m = wm * T::TM + (lane & 31);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ swz_a(m)) * 16;
+  }
+  static_assert(T::FN <= 4, "b_off holds at most 4 fragments");
+  uint32_t b_off[4] = {0, 0, 0, 0};
+  {
+    const int k = 8 * (lane >> 5) + ((lane >> 2) & 3);
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb) {
+      const int n = wn * T::TN + 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      b_off[nb] = k * T::BN * 2 + (((n >> 3) ^ swz_b(k)) * 16) + (n & 7) * 2;
+    }
+  }
+
+  f32x16 acc[T::FM][T::FN];
+#pragma unroll
+  for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x16{};
+
+  const int KT = (K + T::BK - 1) / T::BK;
+  char LDS_AS* lds_base = (char LDS_AS*)lds;
+
+  if constexpr (!GENERIC) {
+    const uint32_t a_goff = (uint32_t)((a_row0 * lda + a_kc) * 2);
+    const uint32_t b_goff = (uint32_t)((b_row0 * ldb + b_nc) * 2);
+    const uint32_t a_rstep = (uint32_t)(RPA * lda * 2), b_rstep = (uint32_t)(RPB * ldb * 2);
+
+    // Loads of K tile t into stage `stage`: RA + RB buffer_load_dwordx4 ... lds per thread.
+    auto issue = [&](int t, int stage) {
+      const int k0 = t * T::BK;
+      // Each range ends at the operand's last element (row M-1, column K-1 of A; row K-1,
+      // column N-1 of B), so nothing past the caller's data is ever fetched; rows past the
+      // end read as zero.  With N, K multiples of 8 no chunk straddles a range end.
+      const i32x4 ra =
+          make_rsrc(p.A + (int64_t)m0 * lda + k0, clip_records(((int64_t)(M - 1 - m0) * lda + K - k0) * 2));
+      const i32x4 rb =
+          make_rsrc(p.B + (int64_t)k0 * ldb + n0, clip_records(((int64_t)(K - 1 - k0) * ldb + N - n0) * 2));
+      const uint32_t a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
+      const uint32_t b_dst = a_dst + T::A_BYTES;
+      // K tail: a chunk at or past K gets kOobOffset added, which puts it beyond the
+      // descriptor's range so it reads as zero (no select: keeps the loads branch-free).
+      const uint32_t a_dead = (uint32_t)(K - 1 - (k0 + a_kc)) >> 31;
+      const uint32_t a_base = a_goff + a_dead * kOobOffset;
+#pragma unroll
+      for (int r = 0; r < T::RA; ++r) dma_b128(a_dst + r * T::NT * 16, ra, a_base + r * a_rstep);
+#pragma unroll
+      for (int r = 0; r < T::RB; ++r) dma_b128(b_dst + r * T::NT * 16, rb, b_goff + r * b_rstep);
+    };
+
+    issue(0, 0);
+    wait_dma();
+    block_sync();
+    for (int t = 0; t + 1 < KT; ++t) {
+      const int cur = t & 1;
+      issue(t + 1, cur ^ 1);
+      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc);
+      wait_dma();
+      block_sync();
+    }
+    {
+      const int cur = (KT - 1) & 1;
+      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc);
+    }
+  } else {
+    u32x4 ra[T::RA], rb[T::RB];
+    const _Float16* A = (const _Float16*)p.A;
+    const _Float16* B = (const _Float16*)p.B;
+    auto load = [&](int t) {
+      const int k0 = t * T::BK;
+#pragma unroll
+      for (int r = 0; r < T::RA; ++r) {
+        const int m = m0 + a_row0 + r * RPA, k = k0 + a_kc;
+        half8 v = {};
+        if (m < M) {
+          const _Float16* src = A + (int64_t)m * lda + k;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k + e < K) v[e] = src[e];
+        }
+        ra[r] = __builtin_bit_cast(u32x4, v);
+      }
+#pragma unroll
+      for (int r = 0; r < T::RB; ++r) {
+        const int k = k0 + b_row0 + r * RPB, n = n0 + b_nc;
+        half8 v = {};
+        if (k < K) {
+          const _Float16* src = B + (int64_t)k * ldb + n;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < N) v[e] = src[e];
+        }
+        rb[r] = __builtin_bit_cast(u32x4, v);
+      }
+    };
+    auto store = [&](int stage) {
+      char LDS_AS* a_dst = lds_base + stage * T::STAGE + (w * 64 + lane) * 16;
+      char LDS_AS* b_dst = lds_base + stage * T::STAGE + T::A_BYTES + (w * 64 + lane) * 16;
+#pragma unroll
+      for (int r = 0; r < T::RA; ++r) *(u32x4 LDS_AS*)(a_dst + r * T::NT * 16) = ra[r];
+#pragma unroll
+      for (int r = 0; r < T::RB; ++r) *(u32x4 LDS_AS*)(b_dst + r * T::NT * 16) = rb[r];
+    };
+
+    load(0);
+    store(0);
+    block_sync();
+    for (int t = 0; t + 1 < KT; ++t) {
+      const int cur = t & 1;
+      load(t + 1);
+      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc);
+      store(cur ^ 1);
+      block_sync();
+    }
+    {
+      const int cur = (KT - 1) & 1;
+      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc);
+    }
+  }
+
+  // ---- epilogue: lane owns row m, columns n..n+3 for each (mb, nb, q).
+  float* C = p.C;
+  const int64_t ldc = p.ldc;
+  const bool vec_ok = p.c_vec4;
+#pragma unroll
+  for (int mb = 0; mb < T::FM; ++mb) {
+    const int m = m0 + wm * T::TM + 32 * mb + (lane & 31);
+    if (m >= M) continue;
+    float* crow = C + (int64_t)m * ldc;
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * T::TN + 32 * nb + 8 * q + 4 * (lane >> 5);
+        f32x4 v = {acc[mb][nb][4 * q + 0], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2], acc[mb][nb][4 * q + 3]};
+        if (vec_ok && n + 3 < N) {
+          *(f32x4*)(crow + n) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) crow[n + e] = v[e];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Folded (5-D contraction) kernel: each GEMM axis is a (hi, lo) pair of sub-indices with
+// its own strides per operand (mmm.h, mmm_contract_desc).  Operands are gathered element by
+// element into the same swizzled LDS stages and multiplied by the same MFMA core; the
+// output is scattered through the C strides.  A lane owns 32 consecutive m across the wave,
+// so an output whose low m sub-index is contiguous (the reference's Out[m][b][r], r
+// contiguous, mmmTensor.cpp:251) is written in 128-byte runs.
+// BKM = true stages B as [BN][64] (for operands whose k_lo stride is 1, e.g. the
+// reference's TN Input[b][n][l]); BKM = false stages B as [64][BN].
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ int64_t fold_off(int i, int lo, int64_t s_hi, int64_t s_lo) {
+  return (int64_t)(i / lo) * s_hi + (int64_t)(i % lo) * s_lo;
+}
+
+template <class T, bool BKM>
+__global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int tiles_m, int tiles_n) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * T::STAGE];
+  static_assert(!BKM || T::BN * 8 % T::NT == 0, "K-major B chunks must divide over threads");
+  constexpr int RBK = BKM ? T::BN * 8 / T::NT : T::RB;
+
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, 4, &tm, &tn);
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * T::BM), n0 = __builtin_amdgcn_readfirstlane(tn * T::BN);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / T::WGN, wn = w % T::WGN;
+  const int M = p.M, N = p.N, K = p.K;
+
+  int a_row[T::RA], a_kc[T::RA];
+  int64_t a_base[T::RA];
+#pragma unroll
+  for (int r = 0; r < T::RA; ++r) {
+    const int s = r * T::NT + w * 64 + lane;
+    const int m = s / T::CA;
+    a_row[r] = m;
+    a_kc[r] = 8 * ((s % T::CA) ^ swz_a(m));
+    a_base[r] = (m0 + m < M) ? fold_off(m0 + m, p.m_lo, p.am[0], p.am[1]) : 0;
+  }
+  int b_row[RBK], b_c[RBK];
+  int64_t b_base[RBK];
+#pragma unroll
+  for (int r = 0; r < RBK; ++r) {
+    const int s = r * T::NT + w * 64 + lane;
+    if constexpr (BKM) {
+      const int n = s / 8;
+      b_row[r] = n;  // tile column n; chunk holds 8 consecutive k
+      b_c[r] = 8 * ((s % 8) ^ swz_a(n));
+      b_base[r] = (n0 + n < N) ? fold_off(n0 + n, p.n_lo, p.bn[0], p.bn[1]) : 0;
+    } else {
+      const int k = s / T::CB;
+      b_row[r] = k;  // tile row k; chunk holds 8 consecutive n
+      b_c[r] = 8 * ((s % T::CB) ^ swz_b(k));
+      b_base[r] = 0;
+    }
+  }
+
+  uint32_t a_off[4];
+  {
+    const int m = wm * T::TM + (lane & 31);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ swz_a(m)) * 16;
+  }
+  uint32_t b_off[4] = {0, 0, 0, 0};
+  if constexpr (BKM) {
+    const int n = wn * T::TN + (lane & 31);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) b_off[kk] = n * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ swz_a(n)) * 16;
+  } else {
+    static_assert(BKM || T::FN <= 4, "b_off holds at most 4 fragments");
+    const int k = 8 * (lane >> 5) + ((lane >> 2) & 3);
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb) {
+      const int n = wn * T::TN + 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+      b_off[nb] = k * T::BN * 2 + (((n >> 3) ^ swz_b(k)) * 16) + (n & 7) * 2;
+    }
+  }
+
+  f32x16 acc[T::FM][T::FN];
+#pragma unroll
+  for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x16{};
+
+  const _Float16* A = (const _Float16*)p.A;
+  const _Float16* B = (const _Float16*)p.B;
+  u32x4 ra[T::RA], rb[RBK];
+  auto load = [&](int t) {
+    const int k0 = t * T::BK;
+#pragma unroll
+    for (int r = 0; r < T::RA; ++r) {
+      const int k = k0 + a_kc[r];
+      half8 v = {};
+      if (m0 + a_row[r] < M) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (k + e < K) v[e] = A[a_base[r] + fold_off(k + e, p.k_lo, p.ak[0], p.ak[1])];
+      }
+      ra[r] = __builtin_bit_cast(u32x4, v);
+    }
+#pragma unroll
+    for (int r = 0; r < RBK; ++r) {
+      half8 v = {};
+      if constexpr (BKM) {
+        const int k = k0 + b_c[r];
+        if (n0 + b_row[r] < N) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k + e < K) v[e] = B[b_base[r] + fold_off(k + e, p.k_lo, p.bk[0], p.bk[1])];
+        }
+      } else {
+        const int k = k0 + b_row[r], n = n0 + b_c[r];
+        if (k < K) {
+          const int64_t kb = fold_off(k, p.k_lo, p.bk[0], p.bk[1]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < N) v[e] = B[kb + fold_off(n + e, p.n_lo, p.bn[0], p.bn[1])];
+        }
+      }
+      rb[r] = __builtin_bit_cast(u32x4, v);
+    }
+  };
+  char LDS_AS* lds_base = (char LDS_AS*)lds;
+  auto store = [&](int stage) {
+    char LDS_AS* a_dst = lds_base + stage * T::STAGE + (w * 64 + lane) * 16;
+    char LDS_AS* b_dst = lds_base + stage * T::STAGE + T::A_BYTES + (w * 64 + lane) * 16;
+#pragma unroll
+    for (int r = 0; r < T::RA; ++r) *(u32x4 LDS_AS*)(a_dst + r * T::NT * 16) = ra[r];
+#pragma unroll
+    for (int r = 0; r < RBK; ++r) *(u32x4 LDS_AS*)(b_dst + r * T::NT * 16) = rb[r];
+  };
+
+  const int KT = (K + T::BK - 1) / T::BK;
+  load(0);
+  store(0);
+  block_sync();
+  for (int t = 0; t < KT; t += 2) {
+    if (t + 1 < KT) load(t + 1);
+    compute_stage<T, BKM>(lds_base, lds_base + T::A_BYTES, a_off, b_off, acc);
+    if (t + 1 < KT) store(1);
+    block_sync();
+    if (t + 1 < KT) {
+      if (t + 2 < KT) load(t + 2);
+      compute_stage<T, BKM>(lds_base + T::STAGE, lds_base + T::STAGE + T::A_BYTES, a_off, b_off, acc);
+      if (t + 2 < KT) store(0);
+      block_sync();
+    }
+  }
+
+  float* C = p.C;
+#pragma unroll
+  for (int mb = 0; mb < T::FM; ++mb) {
+    const int m = m0 + wm * T::TM + 32 * mb + (lane & 31);
+    if (m >= M) continue;
+    const int64_t crow = fold_off(m, p.m_lo, p.cm[0], p.cm[1]);
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int n = n0 + wn * T::TN + 32 * nb + 8 * q + 4 * (lane >> 5) + e;
+          if (n < N) C[crow + fold_off(n, p.n_lo, p.cn[0], p.cn[1])] = acc[mb][nb][4 * q + e];
+        }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Host-side launch
+// ------------------------------------------------------------------------------------
+template <class T, bool GENERIC>
+static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
+  const int tiles_m = (p.M + T::BM - 1) / T::BM;
+  const int tiles_n = (p.N + T::BN - 1) / T::BN;
+  const int64_t blocks = (int64_t)tiles_m * tiles_n;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_nn_kernel<T, GENERIC>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+using Tile256x256 = Tile<256, 256, 2, 2>;
+using Tile128x256 = Tile<128, 256, 2, 2>;
+using Tile256x128 = Tile<256, 128, 2, 2>;
+using Tile128x128 = Tile<128, 128, 2, 2>;
+
+// True when the direct-to-LDS path's preconditions hold for this problem and tile.
+static bool dma_ok(const GemmProblem& p, int bm) {
+  const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
+  if ((a & 15) || (b & 15)) return false;
+  if (p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8) return false;
+  // per-tile byte offsets must fit the 32-bit buffer offsets
+  if ((int64_t)bm * p.lda * 2 >= (int64_t)kOobOffset) return false;
+  if ((int64_t)64 * p.ldb * 2 >= (int64_t)kOobOffset) return false;
+  return true;
+}
+
+hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream) {
+  GemmProblem p = p0;
+  p.c_vec4 = ((uintptr_t)p.C % 16 == 0) && (p.ldc % 4 == 0);
+  switch (tile_id) {
+    case kTile256x256:
+      return dma_ok(p, 256) ? launch_nn<Tile256x256, false>(p, stream) : launch_nn<Tile256x256, true>(p, stream);
+    case kTile128x256:
+      return dma_ok(p, 128) ? launch_nn<Tile128x256, false>(p, stream) : launch_nn<Tile128x256, true>(p, stream);
+    case kTile256x128:
+      return dma_ok(p, 256) ? launch_nn<Tile256x128, false>(p, stream) : launch_nn<Tile256x128, true>(p, stream);
+    case kTile128x128:
+      return dma_ok(p, 128) ? launch_nn<Tile128x128, false>(p, stream) : launch_nn<Tile128x128, true>(p, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream) {
+  using T = Tile128x128;
+  const int tiles_m = (p.M + T::BM - 1) / T::BM;
+  const int tiles_n = (p.N + T::BN - 1) / T::BN;
+  const int64_t blocks = (int64_t)tiles_m * tiles_n;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  const bool bkm = (p.bk[1] == 1) || (p.k_lo == 1 && p.bk[0] == 1);
+  if (bkm)
+    hipLaunchKernelGGL((gemm_fold_kernel<T, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m, tiles_n);
+  else
+    hipLaunchKernelGGL((gemm_fold_kernel<T, false>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m, tiles_n);
+  return hipGetLastError();
+}
+
+}  // namespace mmm

@@ -1,0 +1,44 @@
+// Internal launch interface shared by the kernel sources and the C ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mmm.h"
+
+namespace mmm {
+
+// Plain row-major problem: C[M][N] (ldc) = A[M][K] (lda) * B[K][N] (ldb).
+struct GemmProblem {
+  const mmm_half* A;
+  const mmm_half* B;
+  float* C;
+  int M, N, K;
+  int64_t lda, ldb, ldc;
+  bool c_vec4;  // set by the launcher: C 16-byte aligned and ldc % 4 == 0
+};
+
+// Folded problem (the 5-D contraction descriptor, see mmm.h), with int32 extents.
+struct FoldProblem {
+  const mmm_half* A;
+  const mmm_half* B;
+  float* C;
+  int M, N, K;
+  int m_lo, n_lo, k_lo;  // extents of the low sub-index of each axis
+  int64_t am[2], ak[2];  // A strides for (m_hi, m_lo), (k_hi, k_lo)
+  int64_t bk[2], bn[2];  // B strides for (k_hi, k_lo), (n_hi, n_lo)
+  int64_t cm[2], cn[2];  // C strides for (m_hi, m_lo), (n_hi, n_lo)
+};
+
+enum TileId { kTile256x256 = 0, kTile128x256 = 1, kTile256x128 = 2, kTile128x128 = 3 };
+
+hipError_t launch_gemm_nn(const GemmProblem& p, int tile_id, hipStream_t stream);
+hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
+hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);
+hipError_t launch_fill_uniform(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream);
+hipError_t launch_fill_normal(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, double scale,
+                              hipStream_t stream);
+hipError_t launch_zero_f32(float* C, int M, int N, int64_t ldc, hipStream_t stream);
+hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream);
+
+}  // namespace mmm

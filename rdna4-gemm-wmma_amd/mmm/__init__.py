@@ -1,0 +1,229 @@
+"""Python binding of the MI355X GEMM / contraction library (ctypes over lib/libmmm.so).
+
+The library's C ABI is declared in ``include/mmm.h``; this module mirrors it one to one
+for Python callers (tests, bench).  Device buffers are torch tensors (torch is only the
+allocator and stream provider here); every call goes through the HIP kernels in
+``lib/libmmm.so``.  There is no CPU fallback: if the library is missing, loading fails.
+
+The entry points mirror the reference's kernel entry (thrasos-g/RDNA4-GEMM-WMMA,
+``WMMA_Swizzled_Full<WAVE_M,WAVE_N,WAVES_I,WAVES_J>(A, B, C)``, mmm.cpp:1214-1215, and the
+tensor variant mmmTensor.cpp:44-45): device pointers, M/N/K, tile parameters.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.dirname(_HERE)
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libmmm.so")
+HEADER_PATH = os.path.join(REPO_ROOT, "include", "mmm.h")
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+
+_lib = None
+
+
+class MMMError(RuntimeError):
+    """A library call returned a hipError_t other than hipSuccess."""
+
+    def __init__(self, func: str, code: int):
+        self.code = code
+        super().__init__(f"{func} failed: hipError_t {code} ({_error_name(code)})")
+
+
+def _error_name(code: int) -> str:
+    try:
+        hip = C.CDLL("libamdhip64.so")
+        hip.hipGetErrorName.restype = C.c_char_p
+        hip.hipGetErrorName.argtypes = [C.c_int]
+        return hip.hipGetErrorName(code).decode()
+    except OSError:
+        return "unknown"
+
+
+class ContractDesc(C.Structure):
+    """mmm_contract_desc (include/mmm.h)."""
+
+    _fields_ = [(name, C.c_int64 * 2) for name in (
+        "m_ext", "n_ext", "k_ext", "a_m_stride", "a_k_stride", "b_k_stride", "b_n_stride", "c_m_stride",
+        "c_n_stride")]
+
+    def as_dict(self):
+        return {name: tuple(getattr(self, name)) for name, _ in self._fields_}
+
+    @property
+    def M(self) -> int:
+        return self.m_ext[0] * self.m_ext[1]
+
+    @property
+    def N(self) -> int:
+        return self.n_ext[0] * self.n_ext[1]
+
+    @property
+    def K(self) -> int:
+        return self.k_ext[0] * self.k_ext[1]
+
+
+def declared_symbols(header: str = HEADER_PATH):
+    """Names of the functions include/mmm.h declares."""
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mmm_[a-z0-9_]+)\s*\(", text)))
+
+
+def build() -> None:
+    """Compile the gfx950 library in-tree (make -C rdna4-gemm-wmma_amd)."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-j4", "-C", PKG_ROOT], check=True)
+
+
+def lib() -> C.CDLL:
+    """Load lib/libmmm.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C {PKG_ROOT}` (or __graft_entry__.build())")
+    # torch wheels carry their own HIP runtime under the same soname (libamdhip64.so.7).
+    # Loading torch first makes this library bind to that runtime; loading it first would
+    # put a second HIP runtime into the process, and torch's device memory would not be
+    # visible to it (hipErrorNoDevice).
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    L = C.CDLL(LIB_PATH)
+    p, i, i64, s = C.c_void_p, C.c_int, C.c_int64, C.c_void_p
+    L.mmm_gemm_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, s]
+    L.mmm_gemm_f16f32_tiled.argtypes = [p, p, p, i, i, i, i64, i64, i64, i, i, i, i, s]
+    L.mmm_contract_desc_baseline.argtypes = [C.POINTER(ContractDesc), i, i, i, i, i]
+    L.mmm_contract_desc_reference.argtypes = [C.POINTER(ContractDesc), i, i, i, i, i]
+    L.mmm_contract5d_f16f32.argtypes = [C.POINTER(ContractDesc), p, p, p, s]
+    L.mmm_fill_uniform_f16.argtypes = [p, i64, C.c_uint64, C.c_uint32, s]
+    L.mmm_fill_normal_f16.argtypes = [p, i64, C.c_uint64, C.c_uint32, C.c_double, s]
+    L.mmm_tile_of_block.argtypes = [i, i, i, C.POINTER(i), C.POINTER(i)]
+    for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_tiled", "mmm_contract_desc_baseline",
+                 "mmm_contract_desc_reference", "mmm_contract5d_f16f32", "mmm_fill_uniform_f16",
+                 "mmm_fill_normal_f16", "mmm_tile_of_block"):
+        getattr(L, name).restype = C.c_int
+    L.mmm_version.restype = C.c_char_p
+    L.mmm_version.argtypes = []
+    _lib = L
+    return L
+
+
+def _check(func: str, code: int) -> None:
+    if code != HIP_SUCCESS:
+        raise MMMError(func, code)
+
+
+def _stream(stream):
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return C.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
+
+
+def _ptr(t) -> C.c_void_p:
+    return C.c_void_p(t.data_ptr())
+
+
+def _check_f16(name: str, t) -> None:
+    import torch
+
+    if t.dtype != torch.float16 or not t.is_cuda:
+        raise TypeError(f"{name} must be a CUDA float16 tensor")
+
+
+# Tile parameters (WAVE_M, WAVE_N, WAVES_I, WAVES_J) of the instantiated block tiles.
+TILES = {"256x256": (4, 4, 2, 2), "128x256": (2, 4, 2, 2), "256x128": (4, 2, 2, 2), "128x128": (2, 2, 2, 2)}
+
+
+def gemm(A, B, C_out=None, tile=None, stream=None):
+    """C = A @ B for fp16 A [M,K] and B [K,N] (row-major, any leading dimension via strides).
+
+    Returns the fp32 C [M,N].  ``tile`` is None (library heuristic), a key of TILES, or a
+    (WAVE_M, WAVE_N, WAVES_I, WAVES_J) tuple.
+    """
+    import torch
+
+    _check_f16("A", A)
+    _check_f16("B", B)
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[0]:
+        raise ValueError("A must be [M,K] and B [K,N]")
+    if A.stride(1) != 1 or B.stride(1) != 1:
+        raise ValueError("A and B must be row-major (unit stride along the last dimension)")
+    M, K = A.shape
+    N = B.shape[1]
+    if C_out is None:
+        C_out = torch.empty((M, N), dtype=torch.float32, device=A.device)
+    if C_out.dtype != torch.float32 or C_out.stride(1) != 1 or tuple(C_out.shape) != (M, N):
+        raise ValueError("C must be a row-major float32 [M,N] tensor")
+    lda = A.stride(0) if M > 1 else max(K, 1)
+    ldb = B.stride(0) if K > 1 else max(N, 1)
+    ldc = C_out.stride(0) if M > 1 else max(N, 1)
+    st = _stream(stream)
+    L = lib()
+    if tile is None:
+        _check("mmm_gemm_f16f32", L.mmm_gemm_f16f32(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, st))
+    else:
+        params = TILES[tile] if isinstance(tile, str) else tuple(tile)
+        _check("mmm_gemm_f16f32_tiled",
+               L.mmm_gemm_f16f32_tiled(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, *params, st))
+    return C_out
+
+
+def contract_desc_baseline(b: int, i: int, k: int, l: int, j: int) -> ContractDesc:
+    d = ContractDesc()
+    _check("mmm_contract_desc_baseline", lib().mmm_contract_desc_baseline(C.byref(d), b, i, k, l, j))
+    return d
+
+
+def contract_desc_reference(mt: int, bt: int, rt: int, nt: int, rt_l: int) -> ContractDesc:
+    d = ContractDesc()
+    _check("mmm_contract_desc_reference", lib().mmm_contract_desc_reference(C.byref(d), mt, bt, rt, nt, rt_l))
+    return d
+
+
+def contract(desc: ContractDesc, A, B, C_out, stream=None):
+    """Runs the 5-D contraction described by desc (A, B fp16; C fp32; caller-shaped tensors)."""
+    import torch
+
+    _check_f16("A", A)
+    _check_f16("B", B)
+    if C_out.dtype != torch.float32 or not C_out.is_cuda:
+        raise TypeError("C must be a CUDA float32 tensor")
+    _check("mmm_contract5d_f16f32",
+           lib().mmm_contract5d_f16f32(C.byref(desc), _ptr(A), _ptr(B), _ptr(C_out), _stream(stream)))
+    return C_out
+
+
+def fill_uniform(t, seed: int, tensor_id: int, stream=None):
+    """Fill fp16 tensor t with the seeded uniform[-1,1) stream (seed, tensor_id)."""
+    _check_f16("t", t)
+    _check("mmm_fill_uniform_f16", lib().mmm_fill_uniform_f16(_ptr(t), t.numel(), seed, tensor_id, _stream(stream)))
+    return t
+
+
+def fill_normal(t, seed: int, tensor_id: int, scale: float = 0.1, stream=None):
+    """Fill fp16 tensor t with the seeded N(0,1)*scale stream (seed, tensor_id)."""
+    _check_f16("t", t)
+    _check("mmm_fill_normal_f16",
+           lib().mmm_fill_normal_f16(_ptr(t), t.numel(), seed, tensor_id, scale, _stream(stream)))
+    return t
+
+
+def tile_of_block(block: int, tiles_m: int, tiles_n: int):
+    tm, tn = C.c_int(), C.c_int()
+    _check("mmm_tile_of_block", lib().mmm_tile_of_block(block, tiles_m, tiles_n, C.byref(tm), C.byref(tn)))
+    return tm.value, tn.value
+
+
+def version() -> str:
+    return lib().mmm_version().decode()

@@ -1,0 +1,297 @@
+"""GPU parity tests: the HIP library (through its C ABI) against the CPU oracle.
+
+Tolerance (BASELINE): |C - C_ref| <= 1e-3 * S elementwise, S = sum_k |a_ik * b_kj|,
+against the fp64 truth and against the CPU restatement of the reference kernel's fp32
+arithmetic.  Integer-valued inputs (|a|, |b| <= 4, 16*K < 2^24) make every fp32 partial
+sum exact in any order, so those cases must match an int64 product bit for bit.
+At full size, outputs are checked on sampled rows/columns plus row and column checksums
+(C 1 = A (B 1), 1^T C = (1^T A) B, each within the summed tolerance).
+"""
+import numpy as np
+import pytest
+
+from conftest import to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _int_inputs(rng, M, N, K):
+    A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
+    truth = A.astype(np.int64) @ B.astype(np.int64)
+    return A, B, truth.astype(np.float32)
+
+
+def _check_sampled(orc, A, B, C, rows, cols, label):
+    T, S = orc.gemm_f64(A, B, rows=rows)
+    bad, worst = orc.check_tol(np.ascontiguousarray(C[rows]), T, S, TOL)
+    assert bad == 0, f"{label}: {bad} row-sample violations (worst |d|/S = {worst:.3g})"
+    T, S = orc.gemm_f64(A, B, cols=cols)
+    bad2, worst2 = orc.check_tol(np.ascontiguousarray(C[:, cols]), T, S, TOL)
+    assert bad2 == 0, f"{label}: {bad2} column-sample violations (worst |d|/S = {worst2:.3g})"
+    return max(worst, worst2)
+
+
+def _check_checksums(A, B, C, label):
+    A64 = A.astype(np.float64)
+    B64 = B.astype(np.float64)
+    C64 = C.astype(np.float64)
+    r_true = A64 @ B64.sum(axis=1)
+    r_bound = np.abs(A64) @ np.abs(B64).sum(axis=1)
+    r_err = np.abs(C64.sum(axis=1) - r_true)
+    assert np.all(r_err <= TOL * r_bound), f"{label}: row checksum off by {np.max(r_err / r_bound):.3g} of bound"
+    c_true = A64.sum(axis=0) @ B64
+    c_bound = np.abs(A64).sum(axis=0) @ np.abs(B64)
+    c_err = np.abs(C64.sum(axis=0) - c_true)
+    assert np.all(c_err <= TOL * c_bound), f"{label}: column checksum off by {np.max(c_err / c_bound):.3g} of bound"
+
+
+def _sample(n, k, rng, must=()):
+    s = set(int(x) for x in rng.choice(n, size=min(k, n), replace=False))
+    s.update(int(m) % n for m in must)
+    return np.array(sorted(s), dtype=np.int64)
+
+
+# ------------------------------------------------------------------------------ configs
+def test_config1_256_full(orc, mm, cuda):
+    """C1: 256^3, U[-1,1], seed 0; every output vs fp64 and vs the reference-kernel restatement."""
+    A = orc.uniform_f16((256, 256), 0, 0)
+    B = orc.uniform_f16((256, 256), 0, 1)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B)).cpu().numpy()
+    T, S = orc.gemm_f64(A, B)
+    bad, worst = orc.check_tol(C, T, S, TOL)
+    assert bad == 0, f"{bad} violations vs fp64 (worst {worst:.3g})"
+    R = orc.gemm_refkernel_f32(A, B)
+    assert np.all(np.abs(C.astype(np.float64) - R) <= TOL * S), "violations vs the reference kernel's fp32 math"
+    N32 = orc.gemm_naive_f32(A, B)
+    assert np.all(np.abs(C.astype(np.float64) - N32) <= TOL * S), "violations vs GEMM_Naive's fp32 math"
+
+
+def test_config2_8192_sampled(orc, mm, cuda):
+    """C2: 8192^3, U[-1,1], seed 1; sampled rows/cols vs fp64, plus row/column checksums."""
+    n = 8192
+    A = orc.uniform_f16((n, n), 1, 0)
+    B = orc.uniform_f16((n, n), 1, 1)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B))
+    cuda.cuda.synchronize()
+    C = C.cpu().numpy()
+    rng = np.random.default_rng(11)
+    rows = _sample(n, 24, rng, must=(0, 255, 256, n - 1))
+    cols = _sample(n, 8, rng, must=(0, n - 1))
+    _check_sampled(orc, A, B, C, rows, cols, "8192^3")
+    R = orc.gemm_refkernel_f32(A, B, rows=rows[:4])
+    T, S = orc.gemm_f64(A, B, rows=rows[:4])
+    assert np.all(np.abs(C[rows[:4]].astype(np.float64) - R) <= TOL * S)
+    _check_checksums(A, B, C, "8192^3")
+
+
+def test_config3_ragged(orc, mm, cuda):
+    """C3: 4097 x 4095 x 4111 (no dimension a tile multiple, rows only 2-byte aligned), seed 2."""
+    M, N, K = 4097, 4095, 4111
+    A = orc.uniform_f16((M, K), 2, 0)
+    B = orc.uniform_f16((K, N), 2, 1)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)
+    C = Cd.cpu().numpy()
+    assert not np.isnan(C).any(), "unwritten outputs remain"
+    rng = np.random.default_rng(12)
+    rows = _sample(M, 20, rng, must=(0, 127, 128, 255, 256, M - 2, M - 1))
+    cols = _sample(N, 12, rng, must=(0, 127, 128, N - 2, N - 1))
+    _check_sampled(orc, A, B, C, rows, cols, "ragged")
+    _check_checksums(A, B, C, "ragged")
+
+
+def test_config4_contraction_baseline(orc, mm, cuda):
+    """C4: C[b,i,j] = sum_{k,l} A[b,i,k,l] B[k,l,j], b=8 i=1024 k=32 l=64 j=2048, N(0,1)*0.1, seed 3."""
+    b, i, k, l, j = 8, 1024, 32, 64, 2048
+    A = orc.normal_f16((b, i, k, l), 3, 0, 0.1)
+    B = orc.normal_f16((k, l, j), 3, 1, 0.1)
+    desc = mm.contract_desc_baseline(b, i, k, l, j)
+    Cd = cuda.full((b, i, j), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(desc, to_dev(cuda, A), to_dev(cuda, B), Cd)
+    C = Cd.cpu().numpy()
+    rng = np.random.default_rng(13)
+    bi = _sample(b * i, 24, rng, must=(0, i - 1, i, b * i - 1))
+    T, S = orc.contract_baseline_f64(A, B, bi)  # 5-D loop nest, no fold
+    Cs = np.ascontiguousarray(C.reshape(b * i, j)[bi])
+    bad, worst = orc.check_tol(Cs, T, S, TOL)
+    assert bad == 0, f"{bad} violations vs the 5-D loop nest (worst {worst:.3g})"
+    _check_checksums(A.reshape(b * i, k * l), B.reshape(k * l, j), C.reshape(b * i, j), "contraction")
+
+
+def test_config5_skinny_full(orc, mm, cuda):
+    """C5: 16 x 8192 x 8192, U[-1,1], seed 4; every output vs fp64."""
+    M, N, K = 16, 8192, 8192
+    A = orc.uniform_f16((M, K), 4, 0)
+    B = orc.uniform_f16((K, N), 4, 1)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B)).cpu().numpy()
+    T, S = orc.gemm_f64(A, B)
+    bad, worst = orc.check_tol(C, T, S, TOL)
+    assert bad == 0, f"{bad} violations vs fp64 (worst {worst:.3g})"
+    R = orc.gemm_refkernel_f32(A, B, cols=np.arange(0, N, 64))
+    assert np.all(np.abs(C[:, ::64].astype(np.float64) - R) <= TOL * S[:, ::64])
+
+
+# ------------------------------------------------------------------------------ exact / edges
+EXACT_SHAPES = [
+    (256, 256, 256),   # aligned, direct-to-LDS path, one tile
+    (300, 264, 200),   # direct-to-LDS path with M/N edge tiles, K tail of 8
+    (257, 129, 77),    # generic path (odd K and N)
+    (513, 1000, 1032), # several tiles, K tail 8
+    (33, 40, 16),      # smaller than one tile
+    (1, 1, 1),
+]
+
+
+@pytest.mark.parametrize("shape", EXACT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_exact_integer(mm, cuda, shape):
+    M, N, K = shape
+    rng = np.random.default_rng(M * 7919 + N * 31 + K)
+    A, B, truth = _int_inputs(rng, M, N, K)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B)).cpu().numpy()
+    assert np.array_equal(C, truth), f"max |diff| {np.abs(C - truth).max()}"
+
+
+@pytest.mark.parametrize("tile", ["256x256", "128x256", "256x128", "128x128"])
+@pytest.mark.parametrize("K", [264, 263])
+def test_exact_every_tile(mm, cuda, tile, K):
+    """Every instantiated tile, on both the direct-to-LDS (K=264) and generic (K=263) paths."""
+    M, N = 333, (520 if K % 8 == 0 else 517)
+    rng = np.random.default_rng(K)
+    A, B, truth = _int_inputs(rng, M, N, K)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B), tile=tile).cpu().numpy()
+    assert np.array_equal(C, truth)
+
+
+def test_identity(mm, cuda, orc):
+    """A = I gives C = float(B) exactly."""
+    n = 384
+    A = np.eye(n, dtype=np.float16)
+    B = orc.uniform_f16((n, 640), 5, 1)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B)).cpu().numpy()
+    assert np.array_equal(C, B.astype(np.float32))
+
+
+def test_all_ones(mm, cuda):
+    """All-ones inputs give C = K exactly."""
+    M, N, K = 200, 300, 4100
+    A = np.ones((M, K), dtype=np.float16)
+    B = np.ones((K, N), dtype=np.float16)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B)).cpu().numpy()
+    assert np.all(C == K)
+
+
+def test_leading_dimensions(mm, cuda):
+    """Sub-matrix views: padded lda/ldb/ldc (aligned and unaligned) and a misaligned base."""
+    rng = np.random.default_rng(5)
+    M, N, K = 190, 270, 136
+    A, B, truth = _int_inputs(rng, M, N, K)
+    for pad_a, pad_b, off in [(8, 10, 0), (3, 5, 0), (8, 10, 1)]:
+        Abig = np.zeros((M, K + pad_a + off), dtype=np.float16)
+        Abig[:, off:off + K] = A
+        Bbig = np.zeros((K, N + pad_b), dtype=np.float16)
+        Bbig[:, :N] = B
+        Ad = to_dev(cuda, Abig)[:, off:off + K]
+        Bd = to_dev(cuda, Bbig)[:, :N]
+        Cbig = cuda.full((M, N + 7), -1.0, dtype=cuda.float32, device="cuda")
+        mm.gemm(Ad, Bd, Cbig[:, :N])
+        C = Cbig.cpu().numpy()
+        assert np.array_equal(C[:, :N], truth), f"pads {pad_a},{pad_b} offset {off}"
+        assert np.all(C[:, N:] == -1.0), "wrote outside the C view"
+
+
+def test_degenerate_sizes(mm, cuda):
+    A = cuda.zeros((5, 0), dtype=cuda.float16, device="cuda")
+    B = cuda.zeros((0, 7), dtype=cuda.float16, device="cuda")
+    C = cuda.full((5, 7), 3.0, dtype=cuda.float32, device="cuda")
+    mm.gemm(A, B, C)
+    assert (C.cpu() == 0).all(), "K == 0 must write zeros"
+    A = cuda.zeros((0, 9), dtype=cuda.float16, device="cuda")
+    B = cuda.zeros((9, 4), dtype=cuda.float16, device="cuda")
+    C = mm.gemm(A, B)
+    assert C.shape == (0, 4)
+
+
+def test_invalid_arguments(mm, cuda):
+    import ctypes as C
+
+    L = mm.lib()
+    null = C.c_void_p(0)
+    assert L.mmm_gemm_f16f32(null, null, null, 4, 4, 4, 4, 4, 4, null) == mm.HIP_ERROR_INVALID_VALUE
+    A = cuda.zeros((4, 4), dtype=cuda.float16, device="cuda")
+    Cd = cuda.zeros((4, 4), dtype=cuda.float32, device="cuda")
+    p = C.c_void_p(A.data_ptr())
+    assert L.mmm_gemm_f16f32(p, p, C.c_void_p(Cd.data_ptr()), 4, 4, 4, 3, 4, 4, null) == mm.HIP_ERROR_INVALID_VALUE
+    assert L.mmm_gemm_f16f32(p, p, C.c_void_p(Cd.data_ptr()), -1, 4, 4, 4, 4, 4, null) == mm.HIP_ERROR_INVALID_VALUE
+    assert L.mmm_gemm_f16f32_tiled(p, p, C.c_void_p(Cd.data_ptr()), 4, 4, 4, 4, 4, 4, 2, 2, 4, 4, null) == \
+        mm.HIP_ERROR_INVALID_VALUE
+
+
+# ------------------------------------------------------------------------------ contractions
+def test_contraction_baseline_exact(mm, cuda):
+    b, i, k, l, j = 2, 33, 3, 40, 70
+    rng = np.random.default_rng(21)
+    A = rng.integers(-4, 5, size=(b, i, k, l)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(k, l, j)).astype(np.float16)
+    truth = np.einsum("bikl,klj->bij", A.astype(np.int64), B.astype(np.int64)).astype(np.float32)
+    C = cuda.full((b, i, j), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(mm.contract_desc_baseline(b, i, k, l, j), to_dev(cuda, A), to_dev(cuda, B), C)
+    assert np.array_equal(C.cpu().numpy(), truth)
+
+
+@pytest.mark.parametrize("dims", [(4, 40, 8, 3, 24), (3, 130, 32, 5, 16)], ids=lambda d: "x".join(map(str, d)))
+def test_contraction_reference_layout_exact(mm, cuda, orc, dims):
+    """Reference layout Out[m][b][r] = sum_{n,l} G[r][n][m][l] In[b][n][l] (mmmTensor.cpp)."""
+    mt, bt, rt, nt, rt_l = dims
+    rng = np.random.default_rng(sum(dims))
+    G = rng.integers(-4, 5, size=(rt, nt, mt, rt_l)).astype(np.float16)
+    In = rng.integers(-4, 5, size=(bt, nt, rt_l)).astype(np.float16)
+    truth = np.einsum("rnml,bnl->mbr", G.astype(np.int64), In.astype(np.int64)).astype(np.float32)
+    Out = cuda.full((mt, bt, rt), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), to_dev(cuda, G), to_dev(cuda, In), Out)
+    got = Out.cpu().numpy()
+    assert np.array_equal(got, truth)
+    # the same numbers as the reference's own route: host pack + TN GEMM + remap
+    hA = orc.pack_reference_G(G).astype(np.int64)
+    gemm = hA @ In.reshape(bt, nt * rt_l).astype(np.int64).T  # [(m*rt+r)][b]
+    assert np.array_equal(got, gemm.reshape(mt, rt, bt).transpose(0, 2, 1).astype(np.float32))
+
+
+def test_contraction_reference_layout_tolerance(mm, cuda, orc):
+    mt, bt, rt, nt, rt_l = 16, 512, 64, 8, 128
+    G = orc.normal_f16((rt, nt, mt, rt_l), 6, 0, 0.1)
+    In = orc.normal_f16((bt, nt, rt_l), 6, 1, 0.1)
+    Out = cuda.full((mt, bt, rt), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), to_dev(cuda, G), to_dev(cuda, In), Out)
+    got = Out.cpu().numpy()
+    rng = np.random.default_rng(14)
+    mr = _sample(mt * rt, 32, rng, must=(0, mt * rt - 1))
+    T, S = orc.contract_reference_f64(G, In, mr)
+    Cs = np.ascontiguousarray(got.transpose(0, 2, 1).reshape(mt * rt, bt)[mr])
+    bad, worst = orc.check_tol(Cs, T, S, TOL)
+    assert bad == 0, f"{bad} violations (worst {worst:.3g})"
+
+
+# ------------------------------------------------------------------------------ input generator
+def test_fill_uniform_matches_oracle(mm, cuda, orc):
+    n = 1_000_003
+    t = cuda.empty(n, dtype=cuda.float16, device="cuda")
+    mm.fill_uniform(t, 7, 1)
+    assert np.array_equal(t.cpu().numpy().view(np.uint16), orc.uniform_f16((n,), 7, 1).view(np.uint16))
+
+
+def test_fill_normal_matches_oracle(mm, cuda, orc):
+    n = 1_000_003
+    t = cuda.empty(n, dtype=cuda.float16, device="cuda")
+    mm.fill_normal(t, 3, 0, 0.1)
+    got = t.cpu().numpy()
+    ref = orc.normal_f16((n,), 3, 0, 0.1)
+    diff = got.view(np.uint16) != ref.view(np.uint16)
+    # device and host libm (log, cos) may differ in the last fp64 bit; after the single
+    # rounding to fp16 that can flip at most a rare halfway case by one ulp.
+    assert diff.mean() < 1e-4
+    if diff.any():
+        ulps = np.abs(got[diff].view(np.uint16).astype(np.int32) - ref[diff].view(np.uint16).astype(np.int32))
+        assert ulps.max() <= 1
