@@ -1,0 +1,301 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X FP16->FP32 GEMM / 5-D contraction (one GPU).
+
+Driver contract: ``python bench.py --gpus N --steps K --warmup W`` prints ONE JSON line.
+A step is one launch of the hot path over one batch of synthetic input already resident
+in HBM.  The default workload is BASELINE configs[1]: the 8192^3 row-major GEMM with
+inputs uniform in [-1, 1) from seed 1 (generated on the device by the library's seeded
+generator).  ``value`` is TFLOP/s (2*M*N*K per step over the timed region).
+
+Extra objects on the line:
+  roofline     -- the dominant kernel's achieved rate (algorithmic flops, or bytes for the
+                  HBM-bound skinny shape, per launch over the average launch duration measured
+                  with HIP events on the launch stream) against MI355X's published peak
+                  (dense FP16 MFMA 2516.6 TFLOP/s = 256 CU x 4096 flop/clk x 2.4 GHz; HBM3E
+                  8 TB/s); `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE +
+                  WRITE_SIZE (read from profiles/, null when not measured for the workload).
+  cpu_baseline -- the oracle's multithreaded CPU FP16->FP32 GEMM on a bounded sample of the
+                  same workload, on this host's cores (reported only).
+  hipblaslt    -- hipBLASLt on the same inputs and problem (FP16 in, FP32 out).
+
+Other workloads (parity configs, reported with --workload or --report, never the default):
+gemm256, ragged, contraction, skinny.  One GPU only: --gpus above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "rdna4-gemm-wmma_amd")
+for p in (REPO, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "FP16→FP32 GEMM TFLOP/s at 8192³; % of MI355X dense FP16 MFMA peak"
+PEAK_TFLOPS = 2516.6  # 256 CU x 4096 flop/clk x 2.4 GHz, dense FP16 MFMA
+PEAK_GBS = 8000.0     # HBM3E
+
+WORKLOADS = {
+    # name: (M, N, K, kind, seed, dist)
+    "gemm256": (256, 256, 256, "gemm", 0, "uniform"),
+    "gemm8192": (8192, 8192, 8192, "gemm", 1, "uniform"),
+    "ragged": (4097, 4095, 4111, "gemm", 2, "uniform"),
+    "contraction": (8192, 2048, 2048, "contraction", 3, "normal"),
+    "skinny": (16, 8192, 8192, "gemm", 4, "uniform"),
+    # known-size reference for the HBM byte counters: a 256 MiB fp32 device-to-device copy
+    "copy": (8192, 8192, 1, "copy", 0, "uniform"),
+}
+DESCRIPTIONS = {
+    "gemm256": "gemm_nn 256x256x256 fp16 row-major, U[-1,1) seed 0",
+    "gemm8192": "gemm_nn 8192x8192x8192 fp16 row-major, U[-1,1) seed 1",
+    "ragged": "gemm_nn 4097x4095x4111 fp16 row-major, U[-1,1) seed 2",
+    "contraction": "contract5d C[b,i,j]=sum_kl A[b,i,k,l] B[k,l,j], b=8 i=1024 k=32 l=64 j=2048, N(0,1)*0.1 seed 3",
+    "skinny": "gemm_nn 16x8192x8192 fp16 row-major, U[-1,1) seed 4, 3 rotating B buffers",
+    "copy": "copy 256 MiB fp32 device-to-device (counter scaling reference), zeros",
+}
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_workload(name, torch, mmm):
+    """Device inputs and a launch closure for one step of the named workload."""
+    M, N, K, kind, seed, dist = WORKLOADS[name]
+    dev = "cuda"
+    fill = mmm.fill_uniform if dist == "uniform" else (lambda t, s, i: mmm.fill_normal(t, s, i, 0.1))
+    if kind == "copy":
+        src = torch.zeros((M, N), dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        return {"launch": lambda: dst.copy_(src), "witness": None, "host_inputs": None, "M": M, "N": N, "K": K,
+                "bytes": 2.0 * src.numel() * 4}
+    if kind == "contraction":
+        b, i, k, l, j = 8, 1024, 32, 64, 2048
+        A = torch.empty((b, i, k, l), dtype=torch.float16, device=dev)
+        B = torch.empty((k, l, j), dtype=torch.float16, device=dev)
+        fill(A, seed, 0)
+        fill(B, seed, 1)
+        Cd = torch.empty((b, i, j), dtype=torch.float32, device=dev)
+        desc = mmm.contract_desc_baseline(b, i, k, l, j)
+        A2, B2, C2 = A.view(M, K), B.view(K, N), Cd.view(M, N)
+        return {
+            "launch": lambda: mmm.contract(desc, A, B, Cd),
+            "witness": lambda: mmm.witness_hipblaslt(A2, B2, C2),
+            "host_inputs": lambda: (A2.cpu().numpy(), B2.cpu().numpy()),
+            "M": M, "N": N, "K": K,
+        }
+    A = torch.empty((M, K), dtype=torch.float16, device=dev)
+    fill(A, seed, 0)
+    nb = 3 if name == "skinny" else 1  # rotate B past the 256 MB Infinity Cache
+    Bs = []
+    for r in range(nb):
+        Bt = torch.empty((K, N), dtype=torch.float16, device=dev)
+        fill(Bt, seed, 1 + r)
+        Bs.append(Bt)
+    Cd = torch.empty((M, N), dtype=torch.float32, device=dev)
+    state = {"i": 0}
+
+    def launch():
+        mmm.gemm(A, Bs[state["i"] % nb], Cd)
+        state["i"] += 1
+
+    def witness():
+        mmm.witness_hipblaslt(A, Bs[state["i"] % nb], Cd)
+        state["i"] += 1
+
+    return {"launch": launch, "witness": witness, "host_inputs": lambda: (A.cpu().numpy(), Bs[0].cpu().numpy()),
+            "M": M, "N": N, "K": K}
+
+
+def time_launches(torch, fn, steps: int, warmup: int):
+    """W untimed launches, then exactly `steps` launches between synchronizations.
+
+    Returns (ms per step over the whole timed region, list of per-launch ms from HIP events
+    recorded on the launch stream, wall seconds)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t_begin = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_begin.record(stream)
+    for s in range(steps):
+        starts[s].record(stream)
+        fn()
+        ends[s].record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_begin.elapsed_time(t_end)
+    per = [starts[s].elapsed_time(ends[s]) for s in range(steps)]
+    return total_ms / steps, per, wall
+
+
+def read_traffic(workload: str):
+    """HBM bytes per launch for the workload, from the committed rocprofv3 PMC summary."""
+    path = os.path.join(REPO, "profiles", f"traffic_{workload}.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(W, budget_s: float = 12.0):
+    """Oracle CPU GEMM on a bounded sample of the workload's inputs (about budget_s of work).
+
+    If one pass over the whole workload fits the budget, whole passes are repeated until the
+    budget is spent (the best pass is reported); otherwise a leading row block of A is used."""
+    import numpy as np
+    import oracle
+
+    A, B = W["host_inputs"]()
+    M, N, K = W["M"], W["N"], W["K"]
+    threads = oracle.max_threads()
+    probe_rows = min(M, 192)
+    t0 = time.perf_counter()
+    oracle.cpu_gemm_f16f32(np.ascontiguousarray(A[:probe_rows]), B, threads)  # warm-up
+    t_probe = time.perf_counter() - t0
+    rate = 2.0 * probe_rows * N * K / max(t_probe, 1e-6)
+    rows = int(min(M, max(probe_rows, budget_s * rate / (2.0 * N * K))))
+    rows = max(6, rows - rows % 6) if rows < M else M
+    As = np.ascontiguousarray(A[:rows])
+    times = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        oracle.cpu_gemm_f16f32(As, B, threads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all >= budget_s or len(times) >= 50:
+            break
+    best = min(times)
+    return {
+        "value": round(2.0 * rows * N * K / best / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{rows}x{N}x{K} (rows 0..{rows - 1} of the {M}x{N}x{K} workload, same seeded inputs), "
+                  f"best of {len(times)} passes in {sum(times):.1f} s after a {probe_rows}-row warm-up",
+    }
+
+
+def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness):
+    W = make_workload(name, torch, mmm)
+    M, N, K = W["M"], W["N"], W["K"]
+    flops = 2.0 * M * N * K
+    algo_bytes = W.get("bytes", 2.0 * M * K + 2.0 * K * N + 4.0 * M * N)
+    ms, per, wall = time_launches(torch, W["launch"], steps, warmup)
+    avg_launch = statistics.fmean(per)
+    hbm = name in ("skinny", "copy")
+    with_witness = with_witness and W["witness"] is not None
+    with_cpu = with_cpu and W["host_inputs"] is not None
+    res = {
+        "workload": name,
+        "ms_per_step": ms,
+        "tflops": flops / (ms * 1e-3) / 1e12,
+        "gbs": algo_bytes / (ms * 1e-3) / 1e9,
+        "launch_ms": {"avg": avg_launch, "min": min(per), "median": statistics.median(per)},
+        "wall_s": wall,
+    }
+    if hbm:
+        achieved = algo_bytes / (avg_launch * 1e-3) / 1e9
+        res["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                           "frac": round(achieved / PEAK_GBS, 4), "traffic": read_traffic(name)}
+    else:
+        achieved = flops / (avg_launch * 1e-3) / 1e12
+        res["roofline"] = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(name)}
+    if with_witness:
+        try:
+            wms, wper, _ = time_launches(torch, W["witness"], steps, warmup)
+            res["hipblaslt"] = {"ms_per_step": wms, "tflops": flops / (wms * 1e-3) / 1e12,
+                                "gbs": algo_bytes / (wms * 1e-3) / 1e9}
+        except Exception as e:  # the comparison point must not hide the measurement
+            res["hipblaslt"] = {"error": str(e)}
+    if with_cpu:
+        res["cpu_baseline"] = cpu_baseline(W)
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="gemm8192")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-witness", action="store_true", help="skip the hipBLASLt comparison")
+    ap.add_argument("--report", metavar="PATH", help="measure every workload and write a JSON report to PATH")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not implemented)"}))
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        ap.error("--steps must be >= 1 and --warmup >= 0")
+
+    import torch
+    import mmm
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    mmm.lib()
+
+    if args.report:
+        report = []
+        for name in ["gemm8192", "contraction", "ragged", "skinny", "gemm256"]:
+            _log(f"[bench] {name}")
+            r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=False,
+                             with_witness=not args.no_witness)
+            _log(f"[bench] {name}: {r['tflops']:.1f} TFLOP/s ({r['gbs']:.0f} GB/s); "
+                 f"hipBLASLt {r.get('hipblaslt', {}).get('tflops', float('nan')):.1f} TFLOP/s")
+            report.append(r)
+            torch.cuda.empty_cache()
+        with open(args.report, "w") as f:
+            json.dump({"device": torch.cuda.get_device_name(0), "results": report}, f, indent=1)
+
+    name = args.workload
+    r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=not args.no_cpu,
+                     with_witness=not args.no_witness)
+    M, N, K = WORKLOADS[name][:3]
+    skinny = name in ("skinny", "copy")
+    line = {
+        "metric": METRIC if name == "gemm8192" else f"{name} {'GB/s' if skinny else 'TFLOP/s'}",
+        "value": round(r["gbs"] if skinny else r["tflops"], 2),
+        "unit": "GB/s" if skinny else "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (f32 accumulate)",
+        "data": f"synthetic: seeded on-device generator, {DESCRIPTIONS[name].split(', ', 1)[1]}",
+        "config": {"workload": DESCRIPTIONS[name], "M": M, "N": N, "K": K},
+        "pct_peak": round(100.0 * r["tflops"] / PEAK_TFLOPS, 2),
+        "launch_ms": {k: round(v, 5) for k, v in r["launch_ms"].items()},
+        "roofline": r["roofline"],
+    }
+    if "cpu_baseline" in r:
+        line["cpu_baseline"] = r["cpu_baseline"]
+    if "hipblaslt" in r:
+        line["hipblaslt"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r["hipblaslt"].items()}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -54,26 +54,40 @@ constexpr int kRsrcWord3 = 0x00020000;
 // Byte offset used for masked-off chunks; every descriptor's range is clipped below it.
 constexpr uint32_t kOobOffset = 0x7ffffff0u;
 
-template <int BM_, int BN_, int WGM_, int WGN_>
+// Block tile BM x BN, K step BK (32 or 64), WGM x WGN waves, STAGES-deep LDS ring.
+template <int BM_, int BN_, int WGM_, int WGN_, int BK_, int STAGES_>
 struct Tile {
-  static constexpr int BM = BM_, BN = BN_, BK = 64, WGM = WGM_, WGN = WGN_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
   static constexpr int NT = 64 * WGM * WGN;
   static constexpr int TM = BM / WGM, TN = BN / WGN;
   static constexpr int FM = TM / 32, FN = TN / 32;
-  static constexpr int CA = BK / 8;  // 16-byte chunks per A row (8)
-  static constexpr int CB = BN / 8;  // 16-byte chunks per B row
+  static constexpr int KSTEPS = BK / 16;  // MFMA K-steps per stage
+  static constexpr int CA = BK / 8;       // 16-byte chunks per A row
+  static constexpr int CB = BN / 8;       // 16-byte chunks per B row
   static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int RA = BM * CA / NT;  // A chunks per thread per stage
   static constexpr int RB = BK * CB / NT;  // B chunks per thread per stage
+  // A-row swizzle (chunk c of row m stored at c ^ swz_a(m)).  Rows of 128 B (BK = 64):
+  // 8 consecutive rows take 8 distinct chunk slots and 16 consecutive rows 16 distinct
+  // 16-byte bank groups of the 256-byte bank window.  Rows of 64 B (BK = 32): four rows share
+  // a 256-byte window, so the swizzle uses row bits 1..3.  Both are conflict-free for
+  // ds_read_b128 whether the LDS serves 8 or 16 lanes per cycle.
+  static __device__ __forceinline__ int swz_a(int m) {
+    if constexpr (BK == 64) return (m & 7) ^ ((m >> 3) & 3);
+    else return ((m >> 1) & 3) ^ ((m >> 3) & 1);
+  }
+  static constexpr int SWZ_A_ROWS = BK == 64 ? 32 : 16;  // swz_a depends on m % SWZ_A_ROWS
+  static_assert(BK == 32 || BK == 64, "K step must be 32 or 64");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32x32");
+  static_assert(FN <= 4, "at most 4 B fragments per wave");
   static_assert(CB >= 16, "B swizzle needs rows of at least 16 chunks (BN >= 128)");
   static_assert((BM * CA) % NT == 0 && (BK * CB) % NT == 0, "chunks must divide evenly over threads");
-  static_assert(2 * STAGE <= 160 * 1024, "double-buffered stages must fit the 160 KB LDS");
+  static_assert(STAGES >= 2 && STAGES * STAGE <= 160 * 1024, "LDS ring must fit the 160 KB LDS");
 };
 
-__device__ __forceinline__ int swz_a(int m) { return (m & 7) ^ ((m >> 3) & 3); }
-__device__ __forceinline__ int swz_b(int k) { return (0xCA60 >> (4 * (k & 3))) & 15; }  // {0,6,10,12}
+// B-row swizzle (chunk c of row k stored at c ^ swz_b(k)), {0, 6, 10, 12} by k % 4.
+__device__ __forceinline__ int swz_b(int k) { return (0xCA60 >> (4 * (k & 3))) & 15; }
 
 __device__ __forceinline__ half8 lds_read_a(const char LDS_AS* p) { return *(const half8 LDS_AS*)p; }
 
@@ -110,7 +124,14 @@ __device__ __forceinline__ void dma_b128(uint32_t lds_addr, i32x4 rsrc, uint32_t
 }
 #pragma clang diagnostic pop
 
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Wait until at most N of this wave's vector-memory operations are outstanding (they
+// complete in issue order), i.e. all but the N most recent DMA loads have landed in LDS.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"I"(N) : "memory");
+}
+__device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
 
 __device__ __forceinline__ uint32_t lds_addr_of(const char LDS_AS* p) { return (uint32_t)(uintptr_t)p; }
 
@@ -119,17 +140,19 @@ __device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
   return bytes > (int64_t)kOobOffset ? kOobOffset : (uint32_t)bytes;
 }
 
-// One pass over a 64-deep LDS stage: 4 K-steps of FM x FN MFMAs.
-// BKM = false: B stage is [64][BN] (N contiguous), fragments by two transposing reads;
+// One pass over an LDS stage: KSTEPS K-steps of FM x FN MFMAs.  `after_first_reads` runs
+// once the first K-step's fragment reads are issued (the DMA of a later stage goes there,
+// so the MFMA pipe is fed before the loads are queued).
+// BKM = false: B stage is [BK][BN] (N contiguous), fragments by two transposing reads;
 //              b_off[nb] addresses fragment nb, K-steps add whole rows.
-// BKM = true : B stage is [BN][64] (K contiguous, swizzled like A), fragments by one
+// BKM = true : B stage is [BN][BK] (K contiguous, swizzled like A), fragments by one
 //              ds_read_b128; b_off[kk] addresses K-step kk, fragments add 32 rows.
-template <class T, bool BKM>
+template <class T, bool BKM, class Hook>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const char LDS_AS* b_st,
-                                              const uint32_t (&a_off)[4], const uint32_t (&b_off)[4],
-                                              f32x16 (&acc)[T::FM][T::FN]) {
+                                              const uint32_t (&a_off)[T::KSTEPS], const uint32_t (&b_off)[4],
+                                              f32x16 (&acc)[T::FM][T::FN], Hook&& after_first_reads) {
 #pragma unroll
-  for (int kk = 0; kk < T::BK / 16; ++kk) {
+  for (int kk = 0; kk < T::KSTEPS; ++kk) {
     half8 af[T::FM], bf[T::FN];
 #pragma unroll
     for (int mb = 0; mb < T::FM; ++mb) af[mb] = lds_read_a(a_st + a_off[kk] + mb * 32 * T::BK * 2);
@@ -140,6 +163,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
       else
         bf[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * 16) * T::BN * 2, b_st + b_off[nb] + (kk * 16 + 4) * T::BN * 2);
     }
+    if (kk == 0) after_first_reads();
 #pragma unroll
     for (int mb = 0; mb < T::FM; ++mb)
 #pragma unroll
@@ -148,6 +172,10 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
   }
 }
 
+struct NoHook {
+  __device__ __forceinline__ void operator()() const {}
+};
+
 __device__ __forceinline__ void block_sync() { __syncthreads(); }
 
 // GENERIC = false: direct-to-LDS buffer loads; needs lda, ldb, K, N multiples of 8 and
@@ -155,7 +183,7 @@ __device__ __forceinline__ void block_sync() { __syncthreads(); }
 // GENERIC = true : element-wise masked loads through VGPRs; any shape and alignment.
 template <class T, bool GENERIC>
 __global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
-  __shared__ __attribute__((aligned(1024))) char lds[2 * T::STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
 
   int tm, tn;
   tile_of_block(blockIdx.x, tiles_m, tiles_n, 4, &tm, &tn);
@@ -170,23 +198,22 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int ti
 
   // ---- staging map.  Thread (w, lane) moves chunk slot s = r*NT + w*64 + lane of a stage
   // (r = 0..RA-1 for A, 0..RB-1 for B).  A round of NT slots covers RPA = NT/CA rows of A
-  // and RPB = NT/CB rows of B, so slot rows are row0 + r*RP and the logical chunk (the
-  // swizzle only sees row bits below 5, and RP is a multiple of 4) is the same every round.
+  // and RPB = NT/CB rows of B, so slot rows are row0 + r*RP; RPA is a multiple of the rows
+  // the A swizzle depends on and RPB of 4, so the logical chunk is the same every round.
   constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
-  static_assert(RPA % 32 == 0 && RPB % 4 == 0, "round strides must preserve the swizzle");
+  static_assert(RPA % T::SWZ_A_ROWS == 0 && RPB % 4 == 0, "round strides must preserve the swizzle");
   const int a_row0 = w * (64 / T::CA) + lane / T::CA;
-  const int a_kc = 8 * ((lane % T::CA) ^ swz_a(a_row0));
+  const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
   const int b_row0 = w * (64 / T::CB) + lane / T::CB;
   const int b_nc = 8 * ((lane % T::CB) ^ swz_b(b_row0));
 
   // ---- fragment read offsets (bytes within a stage)
-  uint32_t a_off[4];
+  uint32_t a_off[T::KSTEPS];
   {
     const int m = wm * T::TM + (lane & 31);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ swz_a(m)) * 16;
+    for (int kk = 0; kk < T::KSTEPS; ++kk) a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(m)) * 16;
   }
-  static_assert(T::FN <= 4, "b_off holds at most 4 fragments");
   uint32_t b_off[4] = {0, 0, 0, 0};
   {
     const int k = 8 * (lane >> 5) + ((lane >> 2) & 3);
@@ -211,7 +238,7 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int ti
     const uint32_t b_goff = (uint32_t)((b_row0 * ldb + b_nc) * 2);
     const uint32_t a_rstep = (uint32_t)(RPA * lda * 2), b_rstep = (uint32_t)(RPB * ldb * 2);
 
-    // Loads of K tile t into stage `stage`: RA + RB buffer_load_dwordx4 ... lds per thread.
+    // DMA of K tile t into ring slot `stage`: RA + RB buffer_load_dwordx4 ... lds per thread.
     auto issue = [&](int t, int stage) {
       const int k0 = t * T::BK;
       // Each range ends at the operand's last element (row M-1, column K-1 of A; row K-1,
@@ -233,21 +260,34 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int ti
       for (int r = 0; r < T::RB; ++r) dma_b128(b_dst + r * T::NT * 16, rb, b_goff + r * b_rstep);
     };
 
-    issue(0, 0);
-    wait_dma();
-    block_sync();
-    for (int t = 0; t + 1 < KT; ++t) {
-      const int cur = t & 1;
-      issue(t + 1, cur ^ 1);
-      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc);
+    // Ring of STAGES slots, P = STAGES-1 tiles in flight ahead of the one computed.  At the
+    // top of iteration t: wait until tile t has landed (this wave's loads complete in order,
+    // so at most (P-1) tiles' loads may stay outstanding), barrier (every wave's part of tile
+    // t is in LDS, and every wave has finished reading slot (t-1) % STAGES), then refill that
+    // slot with tile t+P while computing tile t.
+    constexpr int P = T::STAGES - 1;
+    constexpr int LPT = T::RA + T::RB;
+    for (int s = 0; s < P; ++s)
+      if (s < KT) issue(s, s);
+    int cur = 0, nxt = P;  // ring slots of tile t and tile t+P
+    int t = 0;
+    for (; t + P < KT; ++t) {
+      wait_vmcnt<(P - 1) * LPT>();
+      block_sync();
+      const char LDS_AS* st = lds_base + cur * T::STAGE;
+      compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue(t + P, nxt); });
+      cur = cur + 1 == T::STAGES ? 0 : cur + 1;
+      nxt = nxt + 1 == T::STAGES ? 0 : nxt + 1;
+    }
+    for (; t < KT; ++t) {
       wait_dma();
       block_sync();
-    }
-    {
-      const int cur = (KT - 1) & 1;
-      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc);
+      const char LDS_AS* st = lds_base + cur * T::STAGE;
+      compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, NoHook{});
+      cur = cur + 1 == T::STAGES ? 0 : cur + 1;
     }
   } else {
+    static_assert(!GENERIC || T::STAGES == 2, "the register-staged path double-buffers");
     u32x4 ra[T::RA], rb[T::RB];
     const _Float16* A = (const _Float16*)p.A;
     const _Float16* B = (const _Float16*)p.B;
@@ -293,13 +333,15 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int ti
     for (int t = 0; t + 1 < KT; ++t) {
       const int cur = t & 1;
       load(t + 1);
-      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc);
+      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc,
+                              NoHook{});
       store(cur ^ 1);
       block_sync();
     }
     {
       const int cur = (KT - 1) & 1;
-      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc);
+      compute_stage<T, false>(lds_base + cur * T::STAGE, lds_base + cur * T::STAGE + T::A_BYTES, a_off, b_off, acc,
+                              NoHook{});
     }
   }
 
@@ -347,6 +389,7 @@ __device__ __forceinline__ int64_t fold_off(int i, int lo, int64_t s_hi, int64_t
 template <class T, bool BKM>
 __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[2 * T::STAGE];
+  static_assert(T::STAGES == 2 && T::BK == 64, "the folded path double-buffers 64-deep stages");
   static_assert(!BKM || T::BN * 8 % T::NT == 0, "K-major B chunks must divide over threads");
   constexpr int RBK = BKM ? T::BN * 8 / T::NT : T::RB;
 
@@ -365,7 +408,7 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
     const int s = r * T::NT + w * 64 + lane;
     const int m = s / T::CA;
     a_row[r] = m;
-    a_kc[r] = 8 * ((s % T::CA) ^ swz_a(m));
+    a_kc[r] = 8 * ((s % T::CA) ^ T::swz_a(m));
     a_base[r] = (m0 + m < M) ? fold_off(m0 + m, p.m_lo, p.am[0], p.am[1]) : 0;
   }
   int b_row[RBK], b_c[RBK];
@@ -376,7 +419,7 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
     if constexpr (BKM) {
       const int n = s / 8;
       b_row[r] = n;  // tile column n; chunk holds 8 consecutive k
-      b_c[r] = 8 * ((s % 8) ^ swz_a(n));
+      b_c[r] = 8 * ((s % 8) ^ T::swz_a(n));
       b_base[r] = (n0 + n < N) ? fold_off(n0 + n, p.n_lo, p.bn[0], p.bn[1]) : 0;
     } else {
       const int k = s / T::CB;
@@ -386,19 +429,18 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
     }
   }
 
-  uint32_t a_off[4];
+  uint32_t a_off[T::KSTEPS];
   {
     const int m = wm * T::TM + (lane & 31);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ swz_a(m)) * 16;
+    for (int kk = 0; kk < T::KSTEPS; ++kk) a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(m)) * 16;
   }
   uint32_t b_off[4] = {0, 0, 0, 0};
   if constexpr (BKM) {
     const int n = wn * T::TN + (lane & 31);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) b_off[kk] = n * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ swz_a(n)) * 16;
+    for (int kk = 0; kk < T::KSTEPS; ++kk) b_off[kk] = n * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(n)) * 16;
   } else {
-    static_assert(BKM || T::FN <= 4, "b_off holds at most 4 fragments");
     const int k = 8 * (lane >> 5) + ((lane >> 2) & 3);
 #pragma unroll
     for (int nb = 0; nb < T::FN; ++nb) {
@@ -467,12 +509,12 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
   block_sync();
   for (int t = 0; t < KT; t += 2) {
     if (t + 1 < KT) load(t + 1);
-    compute_stage<T, BKM>(lds_base, lds_base + T::A_BYTES, a_off, b_off, acc);
+    compute_stage<T, BKM>(lds_base, lds_base + T::A_BYTES, a_off, b_off, acc, NoHook{});
     if (t + 1 < KT) store(1);
     block_sync();
     if (t + 1 < KT) {
       if (t + 2 < KT) load(t + 2);
-      compute_stage<T, BKM>(lds_base + T::STAGE, lds_base + T::STAGE + T::A_BYTES, a_off, b_off, acc);
+      compute_stage<T, BKM>(lds_base + T::STAGE, lds_base + T::STAGE + T::A_BYTES, a_off, b_off, acc, NoHook{});
       if (t + 2 < KT) store(0);
       block_sync();
     }
@@ -509,10 +551,29 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-using Tile256x256 = Tile<256, 256, 2, 2>;
-using Tile128x256 = Tile<128, 256, 2, 2>;
-using Tile256x128 = Tile<256, 128, 2, 2>;
-using Tile128x128 = Tile<128, 128, 2, 2>;
+// Direct-to-LDS path: K step, ring depth and wave grid (compile-time).  Measured on MI355X
+// at 8192^3 (median TFLOP/s): 64 x 2 stages with 2 x 4 waves (two waves per SIMD, so one
+// wave's MFMAs cover the other's barrier and LDS waits) 1126; the same with 2 x 2 waves
+// 1077; 32 x 4 or 32 x 5 stages 1055-1106 -- deeper prefetch does not pay, latency of the
+// operand fetch is not the limiter.
+#ifndef MMM_DMA_BK
+#define MMM_DMA_BK 64
+#endif
+#ifndef MMM_DMA_STAGES
+#define MMM_DMA_STAGES 2
+#endif
+#ifndef MMM_DMA_WGM
+#define MMM_DMA_WGM 2
+#endif
+#ifndef MMM_DMA_WGN
+#define MMM_DMA_WGN 4
+#endif
+template <int BM, int BN>
+using DmaTile = Tile<BM, BN, (BM == 256 && BN == 256 ? MMM_DMA_WGM : 2), (BM == 256 && BN == 256 ? MMM_DMA_WGN : 2),
+                     MMM_DMA_BK, MMM_DMA_STAGES>;
+// Register-staged path: 64-deep stages, double-buffered.
+template <int BM, int BN>
+using RegTile = Tile<BM, BN, 2, 2, 64, 2>;
 
 // True when the direct-to-LDS path's preconditions hold for this problem and tile.
 static bool dma_ok(const GemmProblem& p, int bm) {
@@ -521,7 +582,7 @@ static bool dma_ok(const GemmProblem& p, int bm) {
   if (p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8) return false;
   // per-tile byte offsets must fit the 32-bit buffer offsets
   if ((int64_t)bm * p.lda * 2 >= (int64_t)kOobOffset) return false;
-  if ((int64_t)64 * p.ldb * 2 >= (int64_t)kOobOffset) return false;
+  if ((int64_t)MMM_DMA_BK * p.ldb * 2 >= (int64_t)kOobOffset) return false;
   return true;
 }
 
@@ -530,20 +591,24 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
   p.c_vec4 = ((uintptr_t)p.C % 16 == 0) && (p.ldc % 4 == 0);
   switch (tile_id) {
     case kTile256x256:
-      return dma_ok(p, 256) ? launch_nn<Tile256x256, false>(p, stream) : launch_nn<Tile256x256, true>(p, stream);
+      return dma_ok(p, 256) ? launch_nn<DmaTile<256, 256>, false>(p, stream)
+                            : launch_nn<RegTile<256, 256>, true>(p, stream);
     case kTile128x256:
-      return dma_ok(p, 128) ? launch_nn<Tile128x256, false>(p, stream) : launch_nn<Tile128x256, true>(p, stream);
+      return dma_ok(p, 128) ? launch_nn<DmaTile<128, 256>, false>(p, stream)
+                            : launch_nn<RegTile<128, 256>, true>(p, stream);
     case kTile256x128:
-      return dma_ok(p, 256) ? launch_nn<Tile256x128, false>(p, stream) : launch_nn<Tile256x128, true>(p, stream);
+      return dma_ok(p, 256) ? launch_nn<DmaTile<256, 128>, false>(p, stream)
+                            : launch_nn<RegTile<256, 128>, true>(p, stream);
     case kTile128x128:
-      return dma_ok(p, 128) ? launch_nn<Tile128x128, false>(p, stream) : launch_nn<Tile128x128, true>(p, stream);
+      return dma_ok(p, 128) ? launch_nn<DmaTile<128, 128>, false>(p, stream)
+                            : launch_nn<RegTile<128, 128>, true>(p, stream);
     default:
       return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream) {
-  using T = Tile128x128;
+  using T = RegTile<128, 128>;
   const int tiles_m = (p.M + T::BM - 1) / T::BM;
   const int tiles_n = (p.N + T::BN - 1) / T::BN;
   const int64_t blocks = (int64_t)tiles_m * tiles_n;

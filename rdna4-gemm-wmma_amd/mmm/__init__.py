@@ -227,3 +227,34 @@ def tile_of_block(block: int, tiles_m: int, tiles_n: int):
 
 def version() -> str:
     return lib().mmm_version().decode()
+
+
+# ------------------------------------------------------------------------------ vendor witness
+WITNESS_PATH = os.path.join(PKG_ROOT, "lib", "libmmm_witness.so")
+_witness = None
+_witness_ws = None
+
+
+def witness_hipblaslt(A, B, C_out=None, stream=None):
+    """hipBLASLt on the same FP16->FP32 row-major problem (comparison point only)."""
+    import torch
+
+    global _witness, _witness_ws
+    if _witness is None:
+        lib()  # torch first, then this library, so both bind to torch's HIP runtime
+        W = C.CDLL(WITNESS_PATH)
+        W.mmm_witness_hipblaslt_gemm.restype = C.c_int
+        W.mmm_witness_hipblaslt_gemm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
+                                                 C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_size_t, C.c_void_p]
+        _witness = W
+    if _witness_ws is None:
+        _witness_ws = torch.empty(64 << 20, dtype=torch.uint8, device=A.device)
+    M, K = A.shape
+    N = B.shape[1]
+    if C_out is None:
+        C_out = torch.empty((M, N), dtype=torch.float32, device=A.device)
+    rc = _witness.mmm_witness_hipblaslt_gemm(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, A.stride(0), B.stride(0),
+                                             C_out.stride(0), _ptr(_witness_ws), _witness_ws.numel(), _stream(stream))
+    if rc != 0:
+        raise MMMError("mmm_witness_hipblaslt_gemm", rc)
+    return C_out

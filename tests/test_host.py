@@ -1,0 +1,126 @@
+"""Host-side tests (no GPU): the C ABI library loads and exports what include/mmm.h declares,
+the descriptor presets encode the reference's layouts, the tile scheduler is a bijection,
+and argument validation fails before any device work."""
+import ctypes as C
+import json
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_declared_symbol(mm):
+    declared = mm.declared_symbols()
+    assert len(declared) >= 9
+    L = mm.lib()
+    for name in declared:
+        assert hasattr(L, name), f"{name} declared in include/mmm.h but not exported"
+    out = subprocess.run(["nm", "-D", "--defined-only", mm.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(declared) <= exported
+    assert mm.version().startswith("mmm-gfx950")
+
+
+def test_library_is_built_for_gfx950(mm):
+    """The library (built here from this repository's sources) embeds a gfx950 code object."""
+    data = open(mm.LIB_PATH, "rb").read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+
+
+def test_contract_desc_baseline(mm):
+    d = mm.contract_desc_baseline(8, 1024, 32, 64, 2048)
+    assert (d.M, d.N, d.K) == (8192, 2048, 2048)
+    A = np.zeros((8, 1024, 32, 64))
+    B = np.zeros((32, 64, 2048))
+    Cz = np.zeros((8, 1024, 2048))
+    # strides (elements) of A[b,i,k,l], B[k,l,j], C[b,i,j]
+    sa = [s // 8 for s in A.strides]
+    sb = [s // 8 for s in B.strides]
+    sc = [s // 8 for s in Cz.strides]
+    assert tuple(d.a_m_stride) == (sa[0], sa[1]) and tuple(d.a_k_stride) == (sa[2], sa[3])
+    assert tuple(d.b_k_stride) == (sb[0], sb[1]) and d.b_n_stride[1] == sb[2]
+    assert tuple(d.c_m_stride) == (sc[0], sc[1]) and d.c_n_stride[1] == sc[2]
+
+
+def test_contract_desc_reference(mm):
+    """mmmTensor.cpp:20-28: G[r][n][m][l], Input[b][n][l], Out[m][b][r]; m' = m*rt + r, k' = n*rt_l + l."""
+    mt, bt, rt, nt, rt_l = 128, 8192, 64, 64, 128
+    d = mm.contract_desc_reference(mt, bt, rt, nt, rt_l)
+    assert (d.M, d.N, d.K) == (mt * rt, bt, nt * rt_l)
+    assert tuple(d.m_ext) == (mt, rt) and tuple(d.k_ext) == (nt, rt_l) and d.n_ext[1] == bt
+    # pack index (mmmTensor.cpp:336): g_idx = r*nt*mt*rt_l + n*mt*rt_l + m*rt_l + l
+    for (m, r, n, l) in [(3, 5, 7, 11), (127, 63, 63, 127)]:
+        a_off = m * d.a_m_stride[0] + r * d.a_m_stride[1] + n * d.a_k_stride[0] + l * d.a_k_stride[1]
+        assert a_off == r * nt * mt * rt_l + n * mt * rt_l + m * rt_l + l
+    # TN read (mmmTensor.cpp:168): Input[b*DIM_K + k]
+    for (b, n, l) in [(5, 2, 9), (8191, 63, 127)]:
+        assert b * d.b_n_stride[1] + n * d.b_k_stride[0] + l * d.b_k_stride[1] == b * (nt * rt_l) + n * rt_l + l
+    # output remap (mmmTensor.cpp:251): Out[m*bt*rt + b*rt + r]
+    for (m, r, b) in [(2, 3, 4), (127, 63, 8191)]:
+        assert m * d.c_m_stride[0] + r * d.c_m_stride[1] + b * d.c_n_stride[1] == m * bt * rt + b * rt + r
+
+
+@pytest.mark.parametrize("tm,tn", [(t1, t2) for t1 in range(1, 41, 3) for t2 in range(1, 41, 5)] +
+                         [(32, 32), (17, 16), (17, 32), (33, 16), (32, 8), (1, 64), (64, 1), (129, 3)])
+def test_tile_map_bijection(mm, tm, tn):
+    seen = np.zeros((tm, tn), dtype=np.int32)
+    for b in range(tm * tn):
+        i, j = mm.tile_of_block(b, tm, tn)
+        assert 0 <= i < tm and 0 <= j < tn
+        seen[i, j] += 1
+    assert np.all(seen == 1)
+
+
+def test_tile_map_xcd_locality(mm):
+    """At 8192^3 (32 x 32 tiles of 256), the 32 workgroups one XCD runs first (ids x, x+8, ...)
+    form a 4 x 8 tile patch: they share 4 A panels and 8 B panels in that XCD's L2."""
+    for x in range(8):
+        tiles = [mm.tile_of_block(x + 8 * s, 32, 32) for s in range(32)]
+        rows = {t[0] for t in tiles}
+        cols = {t[1] for t in tiles}
+        assert len(rows) == 4 and len(cols) == 8
+
+
+def test_argument_validation_without_gpu(mm):
+    L = mm.lib()
+    null = C.c_void_p(0)
+    HIP_INVALID = mm.HIP_ERROR_INVALID_VALUE
+    assert L.mmm_gemm_f16f32(null, null, null, 8, 8, 8, 8, 8, 8, null) == HIP_INVALID
+    assert L.mmm_gemm_f16f32(null, null, null, -1, 8, 8, 8, 8, 8, null) == HIP_INVALID
+    assert L.mmm_gemm_f16f32(null, null, null, 0, 8, 8, 8, 8, 8, null) == 0  # M == 0: no-op
+    assert L.mmm_gemm_f16f32(null, null, null, 8, 0, 8, 8, 8, 8, null) == 0
+    dummy = C.c_void_p(0x1000)
+    assert L.mmm_gemm_f16f32(dummy, dummy, dummy, 8, 8, 8, 7, 8, 8, null) == HIP_INVALID  # lda < K
+    assert L.mmm_gemm_f16f32(dummy, dummy, dummy, 8, 8, 8, 8, 7, 8, null) == HIP_INVALID  # ldb < N
+    assert L.mmm_gemm_f16f32(dummy, dummy, dummy, 8, 8, 8, 8, 8, 7, null) == HIP_INVALID  # ldc < N
+    assert L.mmm_gemm_f16f32_tiled(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, 2, 2, 4, 4, null) == HIP_INVALID
+    assert L.mmm_gemm_f16f32_tiled(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, 3, 4, 2, 2, null) == HIP_INVALID
+    d = mm.contract_desc_baseline(2, 3, 4, 5, 6)
+    assert L.mmm_contract5d_f16f32(C.byref(d), null, null, null, null) == HIP_INVALID
+    assert L.mmm_contract5d_f16f32(None, dummy, dummy, dummy, null) == HIP_INVALID
+    assert L.mmm_fill_uniform_f16(null, 10, 0, 0, null) == HIP_INVALID
+    assert L.mmm_fill_uniform_f16(null, 0, 0, 0, null) == 0
+    assert L.mmm_contract_desc_baseline(None, 1, 1, 1, 1, 1) == HIP_INVALID
+    tm, tn = C.c_int(), C.c_int()
+    assert L.mmm_tile_of_block(4, 2, 2, C.byref(tm), C.byref(tn)) == HIP_INVALID
+    assert L.mmm_tile_of_block(0, 0, 2, C.byref(tm), C.byref(tn)) == HIP_INVALID
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_header_is_plain_c():
+    """include/mmm.h compiles as C (no torch or C++ types at the boundary)."""
+    src = "#include \"mmm.h\"\nint main(void) { mmm_contract_desc d; (void)d; return 0; }\n"
+    r = subprocess.run(["gcc", "-std=c99", "-x", "c", "-fsyntax-only", "-I", os.path.join(REPO, "include"),
+                        "-I", "/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", "-"], input=src, capture_output=True,
+                       text=True)
+    assert r.returncode == 0, r.stderr
