@@ -194,7 +194,8 @@ hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M
   hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
   if (e != hipSuccess || M == 0 || N == 0) return e;
   if (K == 0) return launch_zero_f32(C, M, N, ldc, stream);
-  GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false};
+  GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
+  if (skinny_ok(p)) return launch_gemm_skinny(p, stream);  // M <= 16: HBM-bound streaming kernel
   return launch_gemm_nn(p, pick_tile(M, N), stream);
 }
 
@@ -206,7 +207,7 @@ hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C,
   hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
   if (e != hipSuccess || M == 0 || N == 0) return e;
   if (K == 0) return launch_zero_f32(C, M, N, ldc, stream);
-  GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false};
+  GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
   return launch_gemm_nn(p, tile, stream);
 }
 

@@ -260,6 +260,49 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int ti
       for (int r = 0; r < T::RB; ++r) dma_b128(b_dst + r * T::NT * 16, rb, b_goff + r * b_rstep);
     };
 
+    // The last K tile of an unaligned problem (K or N not a multiple of 8, or rows not
+    // 16-byte aligned) is gathered element by element through VGPRs into the same slot
+    // layout: its chunks may straddle K, N or the end of an operand, which the descriptor's
+    // range check cannot mask exactly.  Every earlier tile lies wholly inside both operands.
+    const _Float16* Ah = (const _Float16*)p.A;
+    const _Float16* Bh = (const _Float16*)p.B;
+    auto fill_regs = [&](int t, int stage) {
+      const int k0 = t * T::BK;
+      char LDS_AS* a_dst = lds_base + stage * T::STAGE + (w * 64 + lane) * 16;
+      char LDS_AS* b_dst = a_dst + T::A_BYTES;
+#pragma unroll
+      for (int r = 0; r < T::RA; ++r) {
+        const int m = m0 + a_row0 + r * RPA, k = k0 + a_kc;
+        half8 v = {};
+        if (m < M) {
+          const _Float16* src = Ah + (int64_t)m * lda + k;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k + e < K) v[e] = src[e];
+        }
+        *(half8 LDS_AS*)(a_dst + r * T::NT * 16) = v;
+      }
+#pragma unroll
+      for (int r = 0; r < T::RB; ++r) {
+        const int k = k0 + b_row0 + r * RPB, n = n0 + b_nc;
+        half8 v = {};
+        if (k < K) {
+          const _Float16* src = Bh + (int64_t)k * ldb + n;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < N) v[e] = src[e];
+        }
+        *(half8 LDS_AS*)(b_dst + r * T::NT * 16) = v;
+      }
+    };
+    const bool tail_regs = p.tail_regs;
+    auto issue_tile = [&](int t, int stage) {
+      if (tail_regs && t == KT - 1)
+        fill_regs(t, stage);
+      else
+        issue(t, stage);
+    };
+
     // Ring of STAGES slots, P = STAGES-1 tiles in flight ahead of the one computed.  At the
     // top of iteration t: wait until tile t has landed (this wave's loads complete in order,
     // so at most (P-1) tiles' loads may stay outstanding), barrier (every wave's part of tile
@@ -268,14 +311,14 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int ti
     constexpr int P = T::STAGES - 1;
     constexpr int LPT = T::RA + T::RB;
     for (int s = 0; s < P; ++s)
-      if (s < KT) issue(s, s);
+      if (s < KT) issue_tile(s, s);
     int cur = 0, nxt = P;  // ring slots of tile t and tile t+P
     int t = 0;
     for (; t + P < KT; ++t) {
       wait_vmcnt<(P - 1) * LPT>();
       block_sync();
       const char LDS_AS* st = lds_base + cur * T::STAGE;
-      compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue(t + P, nxt); });
+      compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue_tile(t + P, nxt); });
       cur = cur + 1 == T::STAGES ? 0 : cur + 1;
       nxt = nxt + 1 == T::STAGES ? 0 : nxt + 1;
     }
@@ -575,20 +618,29 @@ using DmaTile = Tile<BM, BN, (BM == 256 && BN == 256 ? MMM_DMA_WGM : 2), (BM == 
 template <int BM, int BN>
 using RegTile = Tile<BM, BN, 2, 2, 64, 2>;
 
-// True when the direct-to-LDS path's preconditions hold for this problem and tile.
+// True when the direct-to-LDS path can serve the problem: fp16 operands (2-byte aligned;
+// rows that are not 16-byte aligned are read by unaligned buffer loads, which gfx9-family
+// hardware serves under ROCm's unaligned memory mode), and per-tile byte offsets that fit
+// the 32-bit buffer offsets.
 static bool dma_ok(const GemmProblem& p, int bm) {
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
-  if ((a & 15) || (b & 15)) return false;
-  if (p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8) return false;
-  // per-tile byte offsets must fit the 32-bit buffer offsets
+  if ((a & 1) || (b & 1)) return false;
   if ((int64_t)bm * p.lda * 2 >= (int64_t)kOobOffset) return false;
   if ((int64_t)MMM_DMA_BK * p.ldb * 2 >= (int64_t)kOobOffset) return false;
   return true;
 }
 
+// True when every DMA chunk of the last K tile also lies wholly inside the operands (K and
+// N multiples of 8, 16-byte aligned rows); otherwise that tile is gathered through VGPRs.
+static bool tail_aligned(const GemmProblem& p) {
+  const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
+  return !((a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8);
+}
+
 hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream) {
   GemmProblem p = p0;
   p.c_vec4 = ((uintptr_t)p.C % 16 == 0) && (p.ldc % 4 == 0);
+  p.tail_regs = !tail_aligned(p);
   switch (tile_id) {
     case kTile256x256:
       return dma_ok(p, 256) ? launch_nn<DmaTile<256, 256>, false>(p, stream)

@@ -15,7 +15,8 @@ struct GemmProblem {
   float* C;
   int M, N, K;
   int64_t lda, ldb, ldc;
-  bool c_vec4;  // set by the launcher: C 16-byte aligned and ldc % 4 == 0
+  bool c_vec4;     // set by the launcher: C 16-byte aligned and ldc % 4 == 0
+  bool tail_regs;  // set by the launcher: gather the last K tile through VGPRs
 };
 
 // Folded problem (the 5-D contraction descriptor, see mmm.h), with int32 extents.
@@ -34,6 +35,7 @@ enum TileId { kTile256x256 = 0, kTile128x256 = 1, kTile256x128 = 2, kTile128x128
 
 hipError_t launch_gemm_nn(const GemmProblem& p, int tile_id, hipStream_t stream);
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
+bool skinny_ok(const GemmProblem& p);  // M <= 16 and aligned operands
 hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);
 hipError_t launch_fill_uniform(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream);
 hipError_t launch_fill_normal(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, double scale,

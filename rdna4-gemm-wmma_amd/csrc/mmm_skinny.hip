@@ -1,0 +1,204 @@
+// Skinny GEMM for M <= 16 (decode-shaped, e.g. 16 x 8192 x 8192): HBM-bound, so the design
+// goal is to stream B once at full bandwidth with the MFMA work hidden underneath.
+//
+//  * One 256-thread workgroup per 32-column strip of C (= of B).  Strips are ordered so each
+//    XCD owns a contiguous range of them: neighbouring strips share 128-byte lines of B, and
+//    those lines are then fetched into one L2 only.
+//  * The four waves split K into contiguous ranges.  Each wave streams its range through its
+//    own 6-slot LDS ring (36 KB per wave) with direct-to-LDS buffer loads, and only reads
+//    what it loaded itself, so the loop has no workgroup barrier: a wave waits on its own
+//    vmcnt only.  Five slots in flight per wave (80 KB of B per CU) cover ~2.5 us of memory
+//    latency at 8 TB/s / 256 CUs.
+//  * A slot holds a 64-deep K step: A [16][64] (2 KB, rows swizzled by chunk ^ ((row>>1)&7)
+//    so 16 rows at one chunk hit 16 bank groups) and B [64][32] (4 KB, N contiguous).
+//  * Math: v_mfma_f32_16x16x32_f16, A fragment by ds_read_b128, B fragment by two
+//    ds_read_b64_tr_b16 (transposing 4x16 blocks into the K-contiguous operand layout).
+//  * The four K-partial 16x32 tiles are summed through LDS in a fixed order (deterministic).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mmm.h"
+#include "mmm_kernels.h"
+#include "mmm_tile_map.h"
+
+namespace mmm {
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+#define LDS_AS __attribute__((address_space(3)))
+
+constexpr int kNS = 32;             // columns per workgroup
+constexpr int kKS = 64;             // K rows per ring slot
+constexpr int kSlots = 6;           // ring slots per wave
+constexpr int kWaves = 4;
+constexpr int kABytes = 16 * kKS * 2;   // 2 KB
+constexpr int kBBytes = kKS * kNS * 2;  // 4 KB
+constexpr int kSlot = kABytes + kBBytes;
+constexpr int kLoadsPerSlot = kABytes / 1024 + kBBytes / 1024;  // 1 KB per wave-wide DMA
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr uint32_t kOobOffset = 0x7ffffff0u;
+static_assert(kWaves * kSlots * kSlot <= 160 * 1024, "rings must fit the LDS");
+
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t num_records) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)b), __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
+               __builtin_amdgcn_readfirstlane((int)num_records), kRsrcWord3};
+}
+
+__device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
+  if (bytes <= 0) return 0u;
+  return bytes > (int64_t)kOobOffset ? kOobOffset : (uint32_t)bytes;
+}
+
+// buffer_load_dwordx4 ... lds: 16 bytes per lane into LDS at lds_addr + 16*lane.  Issued as
+// inline asm so the compiler does not serialise later LDS reads behind it; completion is
+// awaited explicitly.  DS instructions on gfx9-family targets do not read m0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_b128(uint32_t lds_addr, i32x4 rsrc, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"I"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ int swz16(int row) { return (row >> 1) & 7; }
+
+}  // namespace
+
+__global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int strips) {
+  __shared__ __attribute__((aligned(1024))) char lds[kWaves * kSlots * kSlot];
+  const int strip = __builtin_amdgcn_readfirstlane(xcd_compact(blockIdx.x, strips));
+  const int n0 = strip * kNS;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = p.M, N = p.N, K = p.K;
+  const int64_t lda = p.lda, ldb = p.ldb;
+
+  // this wave's K steps
+  const int nst_all = (K + kKS - 1) / kKS;
+  const int s_begin = __builtin_amdgcn_readfirstlane((w * nst_all) / kWaves);
+  const int s_end = __builtin_amdgcn_readfirstlane(((w + 1) * nst_all) / kWaves);
+  const int nst = s_end - s_begin;
+
+  char LDS_AS* ring = (char LDS_AS*)lds + w * kSlots * kSlot;
+  const uint32_t ring_addr = (uint32_t)(uintptr_t)ring;
+
+  // DMA map.  A: instruction i covers rows 8i..8i+7, lane -> row 8i + lane/8, slot chunk
+  // lane%8 holding logical chunk (lane%8) ^ swz16(row).  B: instruction i covers rows
+  // 16i..16i+15, lane -> row 16i + lane/4, chunk lane%4 (natural layout).
+  const int a_row = lane >> 3;  // + 8i
+  const uint32_t a_goff0 = (uint32_t)((a_row * lda + 8 * ((lane & 7) ^ swz16(a_row))) * 2);
+  const uint32_t a_goff1 = (uint32_t)(((a_row + 8) * lda + 8 * ((lane & 7) ^ swz16(a_row + 8))) * 2);
+  const int a_kc0 = 8 * ((lane & 7) ^ swz16(a_row)), a_kc1 = 8 * ((lane & 7) ^ swz16(a_row + 8));
+  const uint32_t b_goff = (uint32_t)(((lane >> 2) * ldb + 8 * (lane & 3)) * 2);
+  const uint32_t b_rstep = (uint32_t)(16 * ldb * 2);
+  const i32x4 rb_full = make_rsrc(p.B + n0, clip_records(((int64_t)(K - 1) * ldb + N - n0) * 2));
+
+  auto issue = [&](int s, int slot) {
+    const int k0 = (s_begin + s) * kKS;
+    const i32x4 ra = make_rsrc(p.A + k0, clip_records(((int64_t)(M - 1) * lda + K - k0) * 2));
+    const uint32_t dst = ring_addr + slot * kSlot;
+    // K tail: chunks at or past K are pushed out of the descriptor's range (read as zero)
+    const uint32_t dead0 = (uint32_t)(K - 1 - (k0 + a_kc0)) >> 31;
+    const uint32_t dead1 = (uint32_t)(K - 1 - (k0 + a_kc1)) >> 31;
+    dma_b128(dst, ra, a_goff0 + dead0 * kOobOffset);
+    dma_b128(dst + 1024, ra, a_goff1 + dead1 * kOobOffset);
+    const uint32_t bk = (uint32_t)((int64_t)k0 * ldb * 2);
+#pragma unroll
+    for (int i = 0; i < kBBytes / 1024; ++i) dma_b128(dst + kABytes + i * 1024, rb_full, bk + b_goff + i * b_rstep);
+  };
+
+  // fragment offsets within a slot
+  const int fr = lane & 15, fg = lane >> 4;
+  uint32_t a_off[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) a_off[q] = fr * (kKS * 2) + (((4 * q + fg) ^ swz16(fr)) * 16);
+  const uint32_t b_off = kABytes + (8 * fg + (fr >> 2)) * (kNS * 2) + 4 * (fr & 3) * 2;
+
+  f32x4 acc[2] = {f32x4{}, f32x4{}};
+  auto compute = [&](int slot) {
+    const char LDS_AS* sl = ring + slot * kSlot;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const half8 af = *(const half8 LDS_AS*)(sl + a_off[q]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const char LDS_AS* bp = sl + b_off + (32 * q) * (kNS * 2) + 16 * j * 2;
+        fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)bp);
+        fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)(bp + 4 * kNS * 2));
+        const half8 bf = __builtin_shufflevector(__builtin_bit_cast(half4, lo), __builtin_bit_cast(half4, hi), 0, 1,
+                                                 2, 3, 4, 5, 6, 7);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
+      }
+    }
+  };
+
+  constexpr int P = kSlots - 1;
+  for (int s = 0; s < P; ++s)
+    if (s < nst) issue(s, s);
+  int cur = 0, nxt = P;
+  int t = 0;
+  for (; t + P < nst; ++t) {
+    wait_vmcnt<(P - 1) * kLoadsPerSlot>();  // step t landed (this wave's own loads)
+    wait_lgkm0();                           // this wave's reads of slot nxt (step t-1) are done
+    issue(t + P, nxt);
+    compute(cur);
+    cur = cur + 1 == kSlots ? 0 : cur + 1;
+    nxt = nxt + 1 == kSlots ? 0 : nxt + 1;
+  }
+  for (; t < nst; ++t) {
+    wait_vmcnt<0>();
+    compute(cur);
+    cur = cur + 1 == kSlots ? 0 : cur + 1;
+  }
+
+  // K-partials -> LDS (after every wave is done with its ring), fixed-order sum, store.
+  __syncthreads();
+  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][16][32]
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[(w * 16 + 4 * fg + v) * kNS + 16 * j + fr] = acc[j][v];
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int idx = tid + 256 * e;  // 0..511 -> (row, col)
+    const int row = idx / kNS, col = idx % kNS;
+    const float sum = ((part[(0 * 16 + row) * kNS + col] + part[(1 * 16 + row) * kNS + col]) +
+                       part[(2 * 16 + row) * kNS + col]) +
+                      part[(3 * 16 + row) * kNS + col];
+    if (row < M && n0 + col < N) p.C[(int64_t)row * p.ldc + n0 + col] = sum;
+  }
+}
+
+bool skinny_ok(const GemmProblem& p) {
+  const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
+  if (p.M > 16 || p.M < 1) return false;
+  if ((a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8) return false;
+  if ((int64_t)16 * p.lda * 2 >= (int64_t)kOobOffset) return false;
+  // B offsets are taken from the strip base: the whole operand must fit a 32-bit offset
+  if ((int64_t)p.K * p.ldb * 2 >= (int64_t)kOobOffset) return false;
+  return true;
+}
+
+hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream) {
+  const int strips = (p.N + kNS - 1) / kNS;
+  hipLaunchKernelGGL(gemm_skinny_kernel, dim3(strips), dim3(256), 0, stream, p, strips);
+  return hipGetLastError();
+}
+
+}  // namespace mmm

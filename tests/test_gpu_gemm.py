@@ -165,6 +165,53 @@ def test_exact_every_tile(mm, cuda, tile, K):
     assert np.array_equal(C, truth)
 
 
+@pytest.mark.parametrize("tile", [None, "128x128"])
+def test_exact_ragged_full_size(mm, cuda, tile):
+    """The ragged configuration's shape with integer inputs: every output bit-exact.  Rows of
+    A and B are only 2-byte aligned (unaligned direct-to-LDS loads) and the last K tile is
+    gathered through VGPRs.  fp64 BLAS is exact here (all partial sums below 2^53)."""
+    M, N, K = 4097, 4095, 4111
+    rng = np.random.default_rng(4111)
+    A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
+    truth = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B), tile=tile).cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
+@pytest.mark.parametrize("shape", [(300, 270, 1001), (129, 65, 2055), (64, 4100, 515)], ids=lambda s: "x".join(map(str, s)))
+def test_exact_unaligned_rows(mm, cuda, shape):
+    """Odd leading dimensions across many K tiles (unaligned direct-to-LDS rows)."""
+    M, N, K = shape
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    A, B, truth = _int_inputs(rng, M, N, K)
+    C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B)).cpu().numpy()
+    assert np.array_equal(C, truth)
+
+
+@pytest.mark.parametrize("shape", [(16, 8192, 8192), (5, 1000, 2000), (16, 96, 72), (1, 64, 8), (11, 520, 4104)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_exact_skinny(mm, cuda, shape):
+    """M <= 16 runs on the streaming kernel (K split over four waves, fixed-order reduction)."""
+    M, N, K = shape
+    rng = np.random.default_rng(M * 13 + N + K)
+    A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
+    truth = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)
+    C = Cd.cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
+def test_skinny_deterministic(mm, cuda, orc):
+    A = to_dev(cuda, orc.uniform_f16((16, 8192), 4, 0))
+    B = to_dev(cuda, orc.uniform_f16((8192, 8192), 4, 1))
+    C1 = mm.gemm(A, B).cpu().numpy()
+    C2 = mm.gemm(A, B).cpu().numpy()
+    assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))
+
+
 def test_identity(mm, cuda, orc):
     """A = I gives C = float(B) exactly."""
     n = 384
