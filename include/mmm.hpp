@@ -1,0 +1,52 @@
+// mmm.hpp -- C++ layer over the C ABI (mmm.h) that keeps the reference's kernel-entry shape.
+//
+// The reference launches
+//     WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J><<<grid, dim3(32, WAVES_I*WAVES_J)>>>(A, B, C)
+// with the sizes in the compile-time globals DIM_I/DIM_J/DIM_K (mmm.cpp:13-15, 1214-1215,
+// 1461-1472, 1496), and the tensor variant with the packed G (mmmTensor.cpp:44-45, 345-371).
+// Its template parameters fix the block tile: (WAVES_I*WAVE_M*16) x (WAVES_J*WAVE_N*16)
+// outputs (mmm.cpp:706-716).  Here the same spelling takes the sizes at run time and keeps
+// that meaning -- the block tile -- on the MI355X kernels: a block tile that one of the
+// library's gfx950 instantiations provides is used as asked; any other falls back to the
+// library's own tile choice (mmm_gemm_f16f32), which is also what WMMA_Auto does.
+#ifndef MMM_HPP
+#define MMM_HPP
+
+#include "mmm.h"
+
+namespace mmm {
+
+// Row-major C[DIM_I][DIM_J] (fp32) = A[DIM_I][DIM_K] * B[DIM_K][DIM_J] (fp16), dense rows.
+template <int WAVE_M, int WAVE_N, int WAVES_I, int WAVES_J>
+inline hipError_t WMMA_Swizzled_Full(const mmm_half* A, const mmm_half* B, float* C, int DIM_I, int DIM_J, int DIM_K,
+                                     hipStream_t stream = nullptr) {
+  constexpr int BLOCK_M = WAVES_I * WAVE_M * 16, BLOCK_N = WAVES_J * WAVE_N * 16;
+  static_assert(BLOCK_M > 0 && BLOCK_N > 0, "tile parameters must be positive");
+  // gfx950 instantiations (32x32 MFMA tiles per wave, 2x2 waves): block tile -> parameters
+  constexpr int wm = BLOCK_M / 64, wn = BLOCK_N / 64;
+  constexpr bool have = (BLOCK_M == 128 || BLOCK_M == 256) && (BLOCK_N == 128 || BLOCK_N == 256);
+  if constexpr (have)
+    return mmm_gemm_f16f32_tiled(A, B, C, DIM_I, DIM_J, DIM_K, DIM_K, DIM_J, DIM_J, wm, wn, 2, 2, stream);
+  else
+    return mmm_gemm_f16f32(A, B, C, DIM_I, DIM_J, DIM_K, DIM_K, DIM_J, DIM_J, stream);
+}
+
+// Library-chosen tile (recommended: includes the M <= 16 streaming kernel).
+inline hipError_t WMMA_Auto(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                            int64_t ldb, int64_t ldc, hipStream_t stream = nullptr) {
+  return mmm_gemm_f16f32(A, B, C, M, N, K, lda, ldb, ldc, stream);
+}
+
+// The reference's tensor program (mmmTensor.cpp): Out[m][b][r] = sum_{n,l} G[r][n][m][l] *
+// Input[b][n][l], without the host pack of G (mmmTensor.cpp:329-343).
+inline hipError_t WMMA_Tensor(const mmm_half* G, const mmm_half* Input, float* Out, int mt, int bt, int rt, int nt,
+                              int rt_l, hipStream_t stream = nullptr) {
+  mmm_contract_desc d;
+  hipError_t e = mmm_contract_desc_reference(&d, mt, bt, rt, nt, rt_l);
+  if (e != hipSuccess) return e;
+  return mmm_contract5d_f16f32(&d, G, Input, Out, stream);
+}
+
+}  // namespace mmm
+
+#endif  // MMM_HPP

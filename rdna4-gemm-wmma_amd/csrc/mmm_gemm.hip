@@ -38,6 +38,14 @@
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
 
+// Compile-time schedule options of the MFMA main loop (measured choices are the defaults).
+#ifndef MMM_PIPE_FRAGS
+#define MMM_PIPE_FRAGS 0  // 1: double-buffer fragments across the K steps of a stage
+#endif
+#ifndef MMM_SETPRIO
+#define MMM_SETPRIO 0  // 1: raise wave priority while issuing MFMAs
+#endif
+
 namespace mmm {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -151,25 +159,51 @@ template <class T, bool BKM, class Hook>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const char LDS_AS* b_st,
                                               const uint32_t (&a_off)[T::KSTEPS], const uint32_t (&b_off)[4],
                                               f32x16 (&acc)[T::FM][T::FN], Hook&& after_first_reads) {
+  struct Frags {
+    half8 a[T::FM], b[T::FN];
+  };
+  auto load = [&](int kk, Frags& f) {
 #pragma unroll
-  for (int kk = 0; kk < T::KSTEPS; ++kk) {
-    half8 af[T::FM], bf[T::FN];
-#pragma unroll
-    for (int mb = 0; mb < T::FM; ++mb) af[mb] = lds_read_a(a_st + a_off[kk] + mb * 32 * T::BK * 2);
+    for (int mb = 0; mb < T::FM; ++mb) f.a[mb] = lds_read_a(a_st + a_off[kk] + mb * 32 * T::BK * 2);
 #pragma unroll
     for (int nb = 0; nb < T::FN; ++nb) {
       if constexpr (BKM)
-        bf[nb] = lds_read_a(b_st + b_off[kk] + nb * 32 * T::BK * 2);
+        f.b[nb] = lds_read_a(b_st + b_off[kk] + nb * 32 * T::BK * 2);
       else
-        bf[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * 16) * T::BN * 2, b_st + b_off[nb] + (kk * 16 + 4) * T::BN * 2);
+        f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * 16) * T::BN * 2, b_st + b_off[nb] + (kk * 16 + 4) * T::BN * 2);
     }
-    if (kk == 0) after_first_reads();
+  };
+  auto mfma = [&](const Frags& f) {
+    if (MMM_SETPRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int mb = 0; mb < T::FM; ++mb)
 #pragma unroll
       for (int nb = 0; nb < T::FN; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[nb], af[mb], acc[mb][nb], 0, 0, 0);
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[nb], f.a[mb], acc[mb][nb], 0, 0, 0);
+    if (MMM_SETPRIO) __builtin_amdgcn_s_setprio(0);
+  };
+#if MMM_PIPE_FRAGS
+  // Fragments double-buffered in registers: step kk+1's reads are issued before step kk's
+  // MFMAs (scheduling barriers keep that order), so LDS latency hides under MFMA work.
+  Frags f[2];
+  load(0, f[0]);
+  after_first_reads();
+#pragma unroll
+  for (int kk = 0; kk < T::KSTEPS; ++kk) {
+    if (kk + 1 < T::KSTEPS) load(kk + 1, f[(kk + 1) & 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(f[kk & 1]);
+    __builtin_amdgcn_sched_barrier(0);
   }
+#else
+#pragma unroll
+  for (int kk = 0; kk < T::KSTEPS; ++kk) {
+    Frags f;
+    load(kk, f);
+    if (kk == 0) after_first_reads();
+    mfma(f);
+  }
+#endif
 }
 
 struct NoHook {
@@ -314,13 +348,24 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int ti
       if (s < KT) issue_tile(s, s);
     int cur = 0, nxt = P;  // ring slots of tile t and tile t+P
     int t = 0;
-    for (; t + P < KT; ++t) {
+    // steady state: the tile refilled (t+P) is never the last one, so this loop holds only
+    // DMA issue, LDS reads and MFMAs
+    for (; t + P < KT - 1; ++t) {
+      wait_vmcnt<(P - 1) * LPT>();
+      block_sync();
+      const char LDS_AS* st = lds_base + cur * T::STAGE;
+      compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue(t + P, nxt); });
+      cur = cur + 1 == T::STAGES ? 0 : cur + 1;
+      nxt = nxt + 1 == T::STAGES ? 0 : nxt + 1;
+    }
+    if (t + P == KT - 1) {  // the iteration that refills the last tile (possibly gathered)
+      // A gathered last tile leaves no DMA outstanding, so the next wait must drain the ring.
       wait_vmcnt<(P - 1) * LPT>();
       block_sync();
       const char LDS_AS* st = lds_base + cur * T::STAGE;
       compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue_tile(t + P, nxt); });
       cur = cur + 1 == T::STAGES ? 0 : cur + 1;
-      nxt = nxt + 1 == T::STAGES ? 0 : nxt + 1;
+      ++t;
     }
     for (; t < KT; ++t) {
       wait_dma();

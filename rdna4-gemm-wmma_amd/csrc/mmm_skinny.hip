@@ -9,8 +9,8 @@
 //    what it loaded itself, so the loop has no workgroup barrier: a wave waits on its own
 //    vmcnt only.  Five slots in flight per wave (80 KB of B per CU) cover ~2.5 us of memory
 //    latency at 8 TB/s / 256 CUs.
-//  * A slot holds a 64-deep K step: A [16][64] (2 KB, rows swizzled by chunk ^ ((row>>1)&7)
-//    so 16 rows at one chunk hit 16 bank groups) and B [64][32] (4 KB, N contiguous).
+//  * A slot holds a KS-deep K step: A [16][KS] (rows swizzled so 16 rows at one chunk hit
+//    16 bank groups) and B [KS][NS] (N contiguous).
 //  * Math: v_mfma_f32_16x16x32_f16, A fragment by ds_read_b128, B fragment by two
 //    ds_read_b64_tr_b16 (transposing 4x16 blocks into the K-contiguous operand layout).
 //  * The four K-partial 16x32 tiles are summed through LDS in a fixed order (deterministic).
@@ -33,14 +33,27 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 #define LDS_AS __attribute__((address_space(3)))
 
-constexpr int kNS = 32;             // columns per workgroup
-constexpr int kKS = 64;             // K rows per ring slot
-constexpr int kSlots = 6;           // ring slots per wave
+#ifndef MMM_SKINNY_NS
+#define MMM_SKINNY_NS 32
+#endif
+#ifndef MMM_SKINNY_KS
+#define MMM_SKINNY_KS 64
+#endif
+#ifndef MMM_SKINNY_SLOTS
+#define MMM_SKINNY_SLOTS 6
+#endif
+constexpr int kNS = MMM_SKINNY_NS;        // columns per workgroup
+constexpr int kKS = MMM_SKINNY_KS;        // K rows per ring slot
+constexpr int kSlots = MMM_SKINNY_SLOTS;  // ring slots per wave
 constexpr int kWaves = 4;
-constexpr int kABytes = 16 * kKS * 2;   // 2 KB
-constexpr int kBBytes = kKS * kNS * 2;  // 4 KB
+constexpr int kABytes = 16 * kKS * 2;   // A [16][KS]
+constexpr int kBBytes = kKS * kNS * 2;  // B [KS][NS]
 constexpr int kSlot = kABytes + kBBytes;
 constexpr int kLoadsPerSlot = kABytes / 1024 + kBBytes / 1024;  // 1 KB per wave-wide DMA
+constexpr int kNT = kNS / 16;           // 16-column MFMA tiles per strip
+constexpr int kCPR = kNS / 8;           // 16-byte chunks per B row
+static_assert(kKS == 32 || kKS == 64, "K rows per slot");
+static_assert(kNS == 32 || kNS == 64, "strip width");
 constexpr int kRsrcWord3 = 0x00020000;
 constexpr uint32_t kOobOffset = 0x7ffffff0u;
 static_assert(kWaves * kSlots * kSlot <= 160 * 1024, "rings must fit the LDS");
@@ -75,7 +88,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-__device__ __forceinline__ int swz16(int row) { return (row >> 1) & 7; }
+// A-slot swizzle: 16 rows at one logical chunk land in 16 distinct 16-byte bank groups.
+// Rows of 128 B (KS = 64): chunk ^ ((row >> 1) & 7).  Rows of 64 B (KS = 32): four rows
+// share a 256-byte window, so chunk ^ ((row >> 2) & 3).
+__device__ __forceinline__ int swz_a(int row) { return kKS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
 
 }  // namespace
 
@@ -97,26 +113,34 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
   char LDS_AS* ring = (char LDS_AS*)lds + w * kSlots * kSlot;
   const uint32_t ring_addr = (uint32_t)(uintptr_t)ring;
 
-  // DMA map.  A: instruction i covers rows 8i..8i+7, lane -> row 8i + lane/8, slot chunk
-  // lane%8 holding logical chunk (lane%8) ^ swz16(row).  B: instruction i covers rows
-  // 16i..16i+15, lane -> row 16i + lane/4, chunk lane%4 (natural layout).
-  const int a_row = lane >> 3;  // + 8i
-  const uint32_t a_goff0 = (uint32_t)((a_row * lda + 8 * ((lane & 7) ^ swz16(a_row))) * 2);
-  const uint32_t a_goff1 = (uint32_t)(((a_row + 8) * lda + 8 * ((lane & 7) ^ swz16(a_row + 8))) * 2);
-  const int a_kc0 = 8 * ((lane & 7) ^ swz16(a_row)), a_kc1 = 8 * ((lane & 7) ^ swz16(a_row + 8));
-  const uint32_t b_goff = (uint32_t)(((lane >> 2) * ldb + 8 * (lane & 3)) * 2);
-  const uint32_t b_rstep = (uint32_t)(16 * ldb * 2);
+  // DMA map.  A [16][KS]: CA = KS/8 chunks per row; one wave-wide instruction covers
+  // 64/CA rows, lane -> row lane/CA (+ 64/CA per instruction), slot chunk lane%CA holding
+  // logical chunk (lane%CA) ^ swz(row).  B [KS][NS]: lane -> row lane/CPR (+ 64/CPR per
+  // instruction), chunk lane%CPR (natural layout).
+  constexpr int CA = kKS / 8, RPI_A = 64 / CA, NA = kABytes / 1024;
+  const int a_row = lane / CA;
+  uint32_t a_goff[NA];
+  int a_kc[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int row = a_row + i * RPI_A;
+    a_kc[i] = 8 * ((lane % CA) ^ swz_a(row));
+    a_goff[i] = (uint32_t)((row * lda + a_kc[i]) * 2);
+  }
+  const uint32_t b_goff = (uint32_t)(((lane / kCPR) * ldb + 8 * (lane % kCPR)) * 2);
+  const uint32_t b_rstep = (uint32_t)((64 / kCPR) * ldb * 2);
   const i32x4 rb_full = make_rsrc(p.B + n0, clip_records(((int64_t)(K - 1) * ldb + N - n0) * 2));
 
   auto issue = [&](int s, int slot) {
     const int k0 = (s_begin + s) * kKS;
     const i32x4 ra = make_rsrc(p.A + k0, clip_records(((int64_t)(M - 1) * lda + K - k0) * 2));
     const uint32_t dst = ring_addr + slot * kSlot;
-    // K tail: chunks at or past K are pushed out of the descriptor's range (read as zero)
-    const uint32_t dead0 = (uint32_t)(K - 1 - (k0 + a_kc0)) >> 31;
-    const uint32_t dead1 = (uint32_t)(K - 1 - (k0 + a_kc1)) >> 31;
-    dma_b128(dst, ra, a_goff0 + dead0 * kOobOffset);
-    dma_b128(dst + 1024, ra, a_goff1 + dead1 * kOobOffset);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      // K tail: chunks at or past K are pushed out of the descriptor's range (read as zero)
+      const uint32_t dead = (uint32_t)(K - 1 - (k0 + a_kc[i])) >> 31;
+      dma_b128(dst + i * 1024, ra, a_goff[i] + dead * kOobOffset);
+    }
     const uint32_t bk = (uint32_t)((int64_t)k0 * ldb * 2);
 #pragma unroll
     for (int i = 0; i < kBBytes / 1024; ++i) dma_b128(dst + kABytes + i * 1024, rb_full, bk + b_goff + i * b_rstep);
@@ -124,19 +148,22 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
 
   // fragment offsets within a slot
   const int fr = lane & 15, fg = lane >> 4;
-  uint32_t a_off[2];
+  constexpr int KQ = kKS / 32;  // 32-deep MFMA steps per slot
+  uint32_t a_off[KQ];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) a_off[q] = fr * (kKS * 2) + (((4 * q + fg) ^ swz16(fr)) * 16);
+  for (int q = 0; q < KQ; ++q) a_off[q] = fr * (kKS * 2) + (((4 * q + fg) ^ swz_a(fr)) * 16);
   const uint32_t b_off = kABytes + (8 * fg + (fr >> 2)) * (kNS * 2) + 4 * (fr & 3) * 2;
 
-  f32x4 acc[2] = {f32x4{}, f32x4{}};
+  f32x4 acc[kNT];
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) acc[j] = f32x4{};
   auto compute = [&](int slot) {
     const char LDS_AS* sl = ring + slot * kSlot;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < KQ; ++q) {
       const half8 af = *(const half8 LDS_AS*)(sl + a_off[q]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < kNT; ++j) {
         const char LDS_AS* bp = sl + b_off + (32 * q) * (kNS * 2) + 16 * j * 2;
         fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)bp);
         fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)(bp + 4 * kNS * 2));
@@ -168,15 +195,15 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
 
   // K-partials -> LDS (after every wave is done with its ring), fixed-order sum, store.
   __syncthreads();
-  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][16][32]
+  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][16][NS]
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < kNT; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) part[(w * 16 + 4 * fg + v) * kNS + 16 * j + fr] = acc[j][v];
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int idx = tid + 256 * e;  // 0..511 -> (row, col)
+  for (int e = 0; e < 16 * kNS / 256; ++e) {
+    const int idx = tid + 256 * e;  // -> (row, col)
     const int row = idx / kNS, col = idx % kNS;
     const float sum = ((part[(0 * 16 + row) * kNS + col] + part[(1 * 16 + row) * kNS + col]) +
                        part[(2 * 16 + row) * kNS + col]) +

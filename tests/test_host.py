@@ -124,3 +124,30 @@ def test_header_is_plain_c():
                         "-I", "/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", "-"], input=src, capture_output=True,
                        text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_cpp_header_drop_in(mm, tmp_path):
+    """include/mmm.hpp (the reference's template spelling) compiles and links against the
+    library; with null pointers every entry point reports hipErrorInvalidValue (no GPU needed)."""
+    src = tmp_path / "use_mmm.cpp"
+    src.write_text("""
+#include <cstdio>
+#include "mmm.hpp"
+int main() {
+  int bad = 0;
+  bad += mmm::WMMA_Swizzled_Full<2, 2, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_Swizzled_Full<4, 4, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_Auto(nullptr, nullptr, nullptr, 8, 8, 8, 8, 8, 8) != hipErrorInvalidValue;
+  bad += mmm::WMMA_Tensor(nullptr, nullptr, nullptr, 2, 3, 4, 5, 6) != hipErrorInvalidValue;
+  std::printf("%d\\n", bad);
+  return bad;
+}
+""")
+    exe = tmp_path / "use_mmm"
+    libdir = os.path.dirname(mm.LIB_PATH)
+    r = subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(REPO, "include"),
+                        "-I", "/opt/rocm/include", str(src), "-o", str(exe), f"-L{libdir}", "-lmmm",
+                        f"-Wl,-rpath,{libdir}"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip() == "0", r.stdout + r.stderr

@@ -1,6 +1,6 @@
 """Pins the CPU oracle (no GPU).
 
-The reference has no golden vectors (SURVEY: its only check is a run-time rocBLAS
+The reference has no golden vectors (its only check is a run-time rocBLAS
 comparison), so each oracle function is pinned by something independent of it:
 numpy's IEEE conversions, exact integer arithmetic, numpy/einsum in fp64, published
 splitmix64 output, the reference's own index formulas evaluated by brute force, and
