@@ -196,6 +196,26 @@ hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M
   if (K == 0) return launch_zero_f32(C, M, N, ldc, stream);
   GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
   if (skinny_ok(p)) return launch_gemm_skinny(p, stream);  // M <= 16: HBM-bound streaming kernel
+  // A few rows past a whole number of 256-row tiles (4097 = 16*256 + 1) would cost a full
+  // extra round of tiles; those rows go to the streaming kernel instead when that saves a round.
+  const int rem = M % 256;
+  if (M > 256 && rem > 0 && rem <= 16) {
+    const int Mm = M - rem;
+    const int64_t tn = (N + 255) / 256;
+    const int64_t rounds_full = ((int64_t)((M + 255) / 256) * tn + 255) / 256;
+    const int64_t rounds_main = ((int64_t)(Mm / 256) * tn + 255) / 256;
+    GemmProblem pr = p;
+    pr.M = rem;
+    pr.A = A + (int64_t)Mm * lda;
+    pr.C = C + (int64_t)Mm * ldc;
+    if (rounds_main < rounds_full && skinny_ok(pr)) {
+      GemmProblem pm = p;
+      pm.M = Mm;
+      hipError_t e = launch_gemm_nn(pm, pick_tile(Mm, N), stream);
+      if (e != hipSuccess) return e;
+      return launch_gemm_skinny(pr, stream);
+    }
+  }
   return launch_gemm_nn(p, pick_tile(M, N), stream);
 }
 

@@ -146,6 +146,47 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
     for (int i = 0; i < kBBytes / 1024; ++i) dma_b128(dst + kABytes + i * 1024, rb_full, bk + b_goff + i * b_rstep);
   };
 
+  // The globally last K slot of an unaligned problem (K or N not a multiple of 8, or rows
+  // not 16-byte aligned) is gathered element by element through VGPRs into the same layout:
+  // its chunks may straddle K, N or the end of an operand.  Every earlier slot lies wholly
+  // inside both operands.  The ring is private to the wave, so LDS ordering within the wave
+  // is all the gathered slot needs.
+  const _Float16* Ah = (const _Float16*)p.A;
+  const _Float16* Bh = (const _Float16*)p.B;
+  auto gather = [&](int s, int slot) {
+    const int k0 = (s_begin + s) * kKS;
+    char LDS_AS* dst = ring + slot * kSlot + lane * 16;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int row = a_row + i * RPI_A, k = k0 + a_kc[i];
+      half8 v = {};
+      if (row < M) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (k + e < K) v[e] = Ah[(int64_t)row * lda + k + e];
+      }
+      *(half8 LDS_AS*)(dst + i * 1024) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < kBBytes / 1024; ++i) {
+      const int k = k0 + i * (64 / kCPR) + lane / kCPR, n = n0 + 8 * (lane % kCPR);
+      half8 v = {};
+      if (k < K) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < N) v[e] = Bh[(int64_t)k * ldb + n + e];
+      }
+      *(half8 LDS_AS*)(dst + kABytes + i * 1024) = v;
+    }
+  };
+  const bool gather_last = p.tail_regs && s_end == nst_all && nst > 0;  // uniform
+  auto fill = [&](int s, int slot) {
+    if (gather_last && s == nst - 1)
+      gather(s, slot);
+    else
+      issue(s, slot);
+  };
+
   // fragment offsets within a slot
   const int fr = lane & 15, fg = lane >> 4;
   constexpr int KQ = kKS / 32;  // 32-deep MFMA steps per slot
@@ -176,10 +217,10 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
 
   constexpr int P = kSlots - 1;
   for (int s = 0; s < P; ++s)
-    if (s < nst) issue(s, s);
+    if (s < nst) fill(s, s);
   int cur = 0, nxt = P;
   int t = 0;
-  for (; t + P < nst; ++t) {
+  for (; t + P < nst - 1; ++t) {            // refills a slot that is not the last
     wait_vmcnt<(P - 1) * kLoadsPerSlot>();  // step t landed (this wave's own loads)
     wait_lgkm0();                           // this wave's reads of slot nxt (step t-1) are done
     issue(t + P, nxt);
@@ -187,7 +228,15 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
     cur = cur + 1 == kSlots ? 0 : cur + 1;
     nxt = nxt + 1 == kSlots ? 0 : nxt + 1;
   }
-  for (; t < nst; ++t) {
+  if (t + P == nst - 1) {  // refills the last slot (possibly gathered)
+    wait_vmcnt<(P - 1) * kLoadsPerSlot>();
+    wait_lgkm0();
+    fill(t + P, nxt);
+    compute(cur);
+    cur = cur + 1 == kSlots ? 0 : cur + 1;
+    ++t;
+  }
+  for (; t < nst; ++t) {  // a gathered last slot leaves nothing outstanding: drain everything
     wait_vmcnt<0>();
     compute(cur);
     cur = cur + 1 == kSlots ? 0 : cur + 1;
@@ -215,14 +264,17 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
 bool skinny_ok(const GemmProblem& p) {
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   if (p.M > 16 || p.M < 1) return false;
-  if ((a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8) return false;
+  if ((a & 1) || (b & 1)) return false;
   if ((int64_t)16 * p.lda * 2 >= (int64_t)kOobOffset) return false;
   // B offsets are taken from the strip base: the whole operand must fit a 32-bit offset
-  if ((int64_t)p.K * p.ldb * 2 >= (int64_t)kOobOffset) return false;
+  if (((int64_t)p.K * p.ldb + kNS) * 2 >= (int64_t)kOobOffset) return false;
   return true;
 }
 
-hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream) {
+hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
+  GemmProblem p = p0;
+  const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
+  p.tail_regs = (a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8;
   const int strips = (p.N + kNS - 1) / kNS;
   hipLaunchKernelGGL(gemm_skinny_kernel, dim3(strips), dim3(256), 0, stream, p, strips);
   return hipGetLastError();

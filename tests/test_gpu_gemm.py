@@ -204,6 +204,36 @@ def test_exact_skinny(mm, cuda, shape):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
+@pytest.mark.parametrize("shape", [(3, 1001, 777), (16, 4095, 4111), (9, 130, 2050), (1, 4095, 4111)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_exact_skinny_unaligned(mm, cuda, shape):
+    """Streaming kernel on odd N/K (unaligned rows; last K slot gathered element-wise)."""
+    M, N, K = shape
+    rng = np.random.default_rng(M * 31 + N + 7 * K)
+    A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
+    truth = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)
+    C = Cd.cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
+@pytest.mark.parametrize("shape", [(16 * 256 + 1, 1024, 520), (8 * 256 + 16, 4096, 264), (2 * 256 + 7, 300, 1001)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_exact_row_remainder_split(mm, cuda, shape):
+    """M = 256*k + r (r <= 16): the r rows run on the streaming kernel, the rest on the tile kernel."""
+    M, N, K = shape
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
+    truth = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)
+    C = Cd.cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
 def test_skinny_deterministic(mm, cuda, orc):
     A = to_dev(cuda, orc.uniform_f16((16, 8192), 4, 0))
     B = to_dev(cuda, orc.uniform_f16((8192, 8192), 4, 1))
