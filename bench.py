@@ -48,6 +48,8 @@ WORKLOADS = {
     "ragged": (4097, 4095, 4111, "gemm", 2, "uniform"),
     "contraction": (8192, 2048, 2048, "contraction", 3, "normal"),
     "skinny": (16, 8192, 8192, "gemm", 4, "uniform"),
+    # the reference's own contraction (mmmTensor.cpp:20-28): G[r][n][m][l] x Input[b][n][l]
+    "contraction_ref": (8192, 8192, 8192, "contraction_ref", 5, "uniform"),
     # known-size reference for the HBM byte counters: a 256 MiB fp32 device-to-device copy
     "copy": (8192, 8192, 1, "copy", 0, "uniform"),
 }
@@ -57,6 +59,8 @@ DESCRIPTIONS = {
     "ragged": "gemm_nn 4097x4095x4111 fp16 row-major, U[-1,1) seed 2",
     "contraction": "contract5d C[b,i,j]=sum_kl A[b,i,k,l] B[k,l,j], b=8 i=1024 k=32 l=64 j=2048, N(0,1)*0.1 seed 3",
     "skinny": "gemm_nn 16x8192x8192 fp16 row-major, U[-1,1) seed 4, 3 rotating B buffers",
+    "contraction_ref": "contract5d Out[m][b][r]=sum_nl G[r][n][m][l] In[b][n][l], mt=128 bt=8192 rt=64 nt=64 rt_l=128, "
+                       "U[-1,1) seed 5",
     "copy": "copy 256 MiB fp32 device-to-device (counter scaling reference), zeros",
 }
 
@@ -75,6 +79,16 @@ def make_workload(name, torch, mmm):
         dst = torch.empty_like(src)
         return {"launch": lambda: dst.copy_(src), "witness": None, "host_inputs": None, "M": M, "N": N, "K": K,
                 "bytes": 2.0 * src.numel() * 4}
+    if kind == "contraction_ref":
+        mt, bt, rt, nt, rt_l = 128, 8192, 64, 64, 128
+        G = torch.empty((rt, nt, mt, rt_l), dtype=torch.float16, device=dev)
+        In = torch.empty((bt, nt, rt_l), dtype=torch.float16, device=dev)
+        fill(G, seed, 0)
+        fill(In, seed, 1)
+        Out = torch.empty((mt, bt, rt), dtype=torch.float32, device=dev)
+        desc = mmm.contract_desc_reference(mt, bt, rt, nt, rt_l)
+        return {"launch": lambda: mmm.contract(desc, G, In, Out), "witness": None, "host_inputs": None,
+                "M": M, "N": N, "K": K}
     if kind == "contraction":
         b, i, k, l, j = 8, 1024, 32, 64, 2048
         A = torch.empty((b, i, k, l), dtype=torch.float16, device=dev)
@@ -255,7 +269,7 @@ def main() -> int:
 
     if args.report:
         report = []
-        for name in ["gemm8192", "contraction", "ragged", "skinny", "gemm256"]:
+        for name in ["gemm8192", "contraction", "ragged", "skinny", "gemm256", "contraction_ref"]:
             _log(f"[bench] {name}")
             r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=False,
                              with_witness=not args.no_witness)

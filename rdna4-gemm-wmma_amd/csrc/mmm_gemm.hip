@@ -62,10 +62,11 @@ constexpr int kRsrcWord3 = 0x00020000;
 // Byte offset used for masked-off chunks; every descriptor's range is clipped below it.
 constexpr uint32_t kOobOffset = 0x7ffffff0u;
 
-// Block tile BM x BN, K step BK (32 or 64), WGM x WGN waves, STAGES-deep LDS ring.
-template <int BM_, int BN_, int WGM_, int WGN_, int BK_, int STAGES_>
+// Block tile BM x BN, K step BK (32 or 64), WGM x WGN waves, STAGES-deep LDS ring, OCC
+// workgroups per CU targeted by the launch bounds (OCC > 1 caps registers accordingly).
+template <int BM_, int BN_, int WGM_, int WGN_, int BK_, int STAGES_, int OCC_ = 1>
 struct Tile {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_, OCC = OCC_;
   static constexpr int NT = 64 * WGM * WGN;
   static constexpr int TM = BM / WGM, TN = BN / WGN;
   static constexpr int FM = TM / 32, FN = TN / 32;
@@ -91,7 +92,7 @@ struct Tile {
   static_assert(FN <= 4, "at most 4 B fragments per wave");
   static_assert(CB >= 16, "B swizzle needs rows of at least 16 chunks (BN >= 128)");
   static_assert((BM * CA) % NT == 0 && (BK * CB) % NT == 0, "chunks must divide evenly over threads");
-  static_assert(STAGES >= 2 && STAGES * STAGE <= 160 * 1024, "LDS ring must fit the 160 KB LDS");
+  static_assert(STAGES >= 2 && OCC * STAGES * STAGE <= 160 * 1024, "LDS rings must fit the 160 KB LDS");
 };
 
 // B-row swizzle (chunk c of row k stored at c ^ swz_b(k)), {0, 6, 10, 12} by k % 4.
@@ -216,7 +217,7 @@ __device__ __forceinline__ void block_sync() { __syncthreads(); }
 //                  16-byte-aligned A and B (checked by the host).
 // GENERIC = true : element-wise masked loads through VGPRs; any shape and alignment.
 template <class T, bool GENERIC>
-__global__ __launch_bounds__(T::NT, 1) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
+__global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
 
   int tm, tn;
@@ -627,6 +628,123 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
 }
 
 // ------------------------------------------------------------------------------------
+// Folded problem on the direct-to-LDS path, for folds whose K sub-index is contiguous in
+// both operands (k_lo stride 1) and whose K tiles never straddle a k_hi boundary -- the
+// reference's contraction: G[r][n][m][l] x Input[b][n][l] -> Out[m][b][r] (mmmTensor.cpp).
+//  * A row m = (m_hi, m_lo) starts at m_hi*am0 + m_lo*am1; a 64-deep K tile at k0 adds
+//    (k0 / k_lo)*ak0 + k0 % k_lo and is contiguous from there, so each 16-byte chunk is one
+//    DMA load at a per-lane row base plus a uniform tile offset.
+//  * B is K-major (Input[b][n][l]: column b of B is contiguous in k), staged [BN][64] like A
+//    and read with ds_read_b128 fragments.
+//  * Rows past M and columns past N are pushed out of the descriptor range (read as zero);
+//    the host requires K to be a multiple of the tile depth.
+//  * Output scattered through the C strides: lanes own consecutive m, so an output whose
+//    m_lo is contiguous (Out[m][b][r]) is written in 128-byte runs.
+// ------------------------------------------------------------------------------------
+template <class T>
+__global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProblem p, int tiles_m, int tiles_n,
+                                                                      uint32_t a_bytes, uint32_t b_bytes) {
+  __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
+  static_assert(T::BN * T::CA % T::NT == 0, "K-major B chunks must divide over threads");
+  constexpr int RBK = T::BN * T::CA / T::NT;  // K-major B chunks per thread
+  constexpr int RPA = T::NT / T::CA;          // rows per round (A and B alike)
+  static_assert(RPA % T::SWZ_A_ROWS == 0, "round strides must preserve the swizzle");
+
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, 4, &tm, &tn);
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * T::BM), n0 = __builtin_amdgcn_readfirstlane(tn * T::BN);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / T::WGN, wn = w % T::WGN;
+  const int M = p.M, N = p.N, K = p.K;
+
+  const int row0 = w * (64 / T::CA) + lane / T::CA;
+  const int kc = 8 * ((lane % T::CA) ^ T::swz_a(row0));
+  uint32_t a_voff[T::RA], b_voff[RBK];
+#pragma unroll
+  for (int r = 0; r < T::RA; ++r) {
+    const int m = m0 + row0 + r * RPA;
+    a_voff[r] = m < M ? (uint32_t)((fold_off(m, p.m_lo, p.am[0], p.am[1]) + kc) * 2) : kOobOffset;
+  }
+#pragma unroll
+  for (int r = 0; r < RBK; ++r) {
+    const int n = n0 + row0 + r * RPA;
+    b_voff[r] = n < N ? (uint32_t)((fold_off(n, p.n_lo, p.bn[0], p.bn[1]) + kc) * 2) : kOobOffset;
+  }
+
+  uint32_t a_off[T::KSTEPS], b_off[4] = {0, 0, 0, 0};
+  {
+    const int m = wm * T::TM + (lane & 31), n = wn * T::TN + (lane & 31);
+#pragma unroll
+    for (int kk = 0; kk < T::KSTEPS; ++kk) {
+      a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(m)) * 16;
+      b_off[kk] = n * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(n)) * 16;
+    }
+  }
+
+  f32x16 acc[T::FM][T::FN];
+#pragma unroll
+  for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x16{};
+
+  char LDS_AS* lds_base = (char LDS_AS*)lds;
+  const i32x4 ra = make_rsrc(p.A, a_bytes);
+  const i32x4 rb = make_rsrc(p.B, b_bytes);
+  auto issue = [&](int t, int stage) {
+    const int k0 = t * T::BK;
+    const uint32_t ka = (uint32_t)(((k0 / p.k_lo) * p.ak[0] + k0 % p.k_lo) * 2);
+    const uint32_t kb = (uint32_t)(((k0 / p.k_lo) * p.bk[0] + k0 % p.k_lo) * 2);
+    const uint32_t a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
+    const uint32_t b_dst = a_dst + T::A_BYTES;
+#pragma unroll
+    for (int r = 0; r < T::RA; ++r) dma_b128(a_dst + r * T::NT * 16, ra, a_voff[r] + ka);
+#pragma unroll
+    for (int r = 0; r < RBK; ++r) dma_b128(b_dst + r * T::NT * 16, rb, b_voff[r] + kb);
+  };
+
+  const int KT = K / T::BK;
+  constexpr int P = T::STAGES - 1;
+  constexpr int LPT = T::RA + RBK;
+  for (int s = 0; s < P; ++s)
+    if (s < KT) issue(s, s);
+  int cur = 0, nxt = P;
+  int t = 0;
+  for (; t + P < KT; ++t) {
+    wait_vmcnt<(P - 1) * LPT>();
+    block_sync();
+    const char LDS_AS* st = lds_base + cur * T::STAGE;
+    compute_stage<T, true>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue(t + P, nxt); });
+    cur = cur + 1 == T::STAGES ? 0 : cur + 1;
+    nxt = nxt + 1 == T::STAGES ? 0 : nxt + 1;
+  }
+  for (; t < KT; ++t) {
+    wait_dma();
+    block_sync();
+    const char LDS_AS* st = lds_base + cur * T::STAGE;
+    compute_stage<T, true>(st, st + T::A_BYTES, a_off, b_off, acc, NoHook{});
+    cur = cur + 1 == T::STAGES ? 0 : cur + 1;
+  }
+
+  float* C = p.C;
+#pragma unroll
+  for (int mb = 0; mb < T::FM; ++mb) {
+    const int m = m0 + wm * T::TM + 32 * mb + (lane & 31);
+    if (m >= M) continue;
+    const int64_t crow = fold_off(m, p.m_lo, p.cm[0], p.cm[1]);
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int n = n0 + wn * T::TN + 32 * nb + 8 * q + 4 * (lane >> 5) + e;
+          if (n < N) C[crow + fold_off(n, p.n_lo, p.cn[0], p.cn[1])] = acc[mb][nb][4 * q + e];
+        }
+  }
+}
+
+// ------------------------------------------------------------------------------------
 // Host-side launch
 // ------------------------------------------------------------------------------------
 template <class T, bool GENERIC>
@@ -656,9 +774,36 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
 #ifndef MMM_DMA_WGN
 #define MMM_DMA_WGN 4
 #endif
+// 256x128 / 128x256 tiles: 4 waves; K step, ring depth and workgroups per CU
+// (measured at 8192^3: 32 x 3 stages with two workgroups per CU 1031-1064 TFLOP/s vs
+// 64 x 2 with one 868-908; two independent workgroups per CU desynchronise their barriers)
+#ifndef MMM_T2_BK
+#define MMM_T2_BK 32
+#endif
+#ifndef MMM_T2_STAGES
+#define MMM_T2_STAGES 3
+#endif
+#ifndef MMM_T2_OCC
+#define MMM_T2_OCC 2
+#endif
 template <int BM, int BN>
-using DmaTile = Tile<BM, BN, (BM == 256 && BN == 256 ? MMM_DMA_WGM : 2), (BM == 256 && BN == 256 ? MMM_DMA_WGN : 2),
-                     MMM_DMA_BK, MMM_DMA_STAGES>;
+struct DmaCfg {  // 128x128
+  using T = Tile<BM, BN, 2, 2, 64, 2, 2>;
+};
+template <>
+struct DmaCfg<256, 256> {
+  using T = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1>;
+};
+template <>
+struct DmaCfg<256, 128> {
+  using T = Tile<256, 128, 2, 2, MMM_T2_BK, MMM_T2_STAGES, MMM_T2_OCC>;
+};
+template <>
+struct DmaCfg<128, 256> {
+  using T = Tile<128, 256, 2, 2, MMM_T2_BK, MMM_T2_STAGES, MMM_T2_OCC>;
+};
+template <int BM, int BN>
+using DmaTile = typename DmaCfg<BM, BN>::T;
 // Register-staged path: 64-deep stages, double-buffered.
 template <int BM, int BN>
 using RegTile = Tile<BM, BN, 2, 2, 64, 2>;
@@ -704,7 +849,32 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
   }
 }
 
+// Largest element offset (+1) an operand's fold can address, or -1 if a stride is negative.
+static int64_t fold_extent(int64_t e_hi, int64_t e_lo, int64_t s_hi, int64_t s_lo, int64_t f_hi, int64_t f_lo,
+                           int64_t t_hi, int64_t t_lo) {
+  if (s_hi < 0 || s_lo < 0 || t_hi < 0 || t_lo < 0) return -1;
+  return (e_hi - 1) * s_hi + (e_lo - 1) * s_lo + (f_hi - 1) * t_hi + (f_lo - 1) * t_lo + 1;
+}
+
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream) {
+  // direct-to-LDS fold path: K contiguous in both operands, K tiles inside one k_hi block,
+  // 16-byte-aligned chunks, offsets within 32 bits
+  using TD = DmaTile<256, 256>;
+  const int m_hi = (p.M + p.m_lo - 1) / p.m_lo, n_hi = (p.N + p.n_lo - 1) / p.n_lo, k_hi = p.K / p.k_lo;
+  const int64_t a_ext = fold_extent(m_hi, p.m_lo, p.am[0], p.am[1], k_hi, p.k_lo, p.ak[0], p.ak[1]);
+  const int64_t b_ext = fold_extent(n_hi, p.n_lo, p.bn[0], p.bn[1], k_hi, p.k_lo, p.bk[0], p.bk[1]);
+  const bool fast = TD::BK == 64 && p.ak[1] == 1 && p.bk[1] == 1 && p.k_lo % TD::BK == 0 && p.K % p.k_lo == 0 &&
+                    p.am[0] % 8 == 0 && p.am[1] % 8 == 0 && p.bn[0] % 8 == 0 && p.bn[1] % 8 == 0 &&
+                    p.ak[0] % 8 == 0 && p.bk[0] % 8 == 0 && ((uintptr_t)p.A & 15) == 0 && ((uintptr_t)p.B & 15) == 0 &&
+                    a_ext > 0 && b_ext > 0 && a_ext * 2 < (int64_t)kOobOffset / 2 && b_ext * 2 < (int64_t)kOobOffset / 2 &&
+                    p.M % p.m_lo == 0 && p.N % p.n_lo == 0;
+  if (fast) {
+    const int tiles_m = (p.M + TD::BM - 1) / TD::BM;
+    const int tiles_n = (p.N + TD::BN - 1) / TD::BN;
+    hipLaunchKernelGGL((gemm_fold_dma_kernel<TD>), dim3((unsigned)(tiles_m * tiles_n)), dim3(TD::NT), 0, stream, p,
+                       tiles_m, tiles_n, (uint32_t)(a_ext * 2), (uint32_t)(b_ext * 2));
+    return hipGetLastError();
+  }
   using T = RegTile<128, 128>;
   const int tiles_m = (p.M + T::BM - 1) / T::BM;
   const int tiles_n = (p.N + T::BN - 1) / T::BN;

@@ -336,6 +336,40 @@ def test_contraction_reference_layout_exact(mm, cuda, orc, dims):
     assert np.array_equal(got, gemm.reshape(mt, rt, bt).transpose(0, 2, 1).astype(np.float32))
 
 
+@pytest.mark.parametrize("dims", [(8, 300, 64, 3, 128), (4, 520, 32, 2, 64)], ids=lambda d: "x".join(map(str, d)))
+def test_contraction_reference_layout_dma_exact(mm, cuda, orc, dims):
+    """Reference layout on the direct-to-LDS fold path (K tiles inside one n block): bit-exact."""
+    mt, bt, rt, nt, rt_l = dims
+    rng = np.random.default_rng(sum(dims) + 1)
+    G = rng.integers(-4, 5, size=(rt, nt, mt, rt_l)).astype(np.float16)
+    In = rng.integers(-4, 5, size=(bt, nt, rt_l)).astype(np.float16)
+    hA = orc.pack_reference_G(G).astype(np.float64)
+    truth = (hA @ In.reshape(bt, nt * rt_l).astype(np.float64).T).reshape(mt, rt, bt).transpose(0, 2, 1)
+    Out = cuda.full((mt, bt, rt), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), to_dev(cuda, G), to_dev(cuda, In), Out)
+    assert np.array_equal(Out.cpu().numpy(), truth.astype(np.float32))
+
+
+def test_contraction_reference_layout_full_size(mm, cuda, orc):
+    """The reference's own contraction size (mmmTensor.cpp:20-28): M = N = K = 8192."""
+    mt, bt, rt, nt, rt_l = 128, 8192, 64, 64, 128
+    G = cuda.empty((rt, nt, mt, rt_l), dtype=cuda.float16, device="cuda")
+    In = cuda.empty((bt, nt, rt_l), dtype=cuda.float16, device="cuda")
+    mm.fill_uniform(G, 5, 0)
+    mm.fill_uniform(In, 5, 1)
+    Out = cuda.full((mt, bt, rt), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), G, In, Out)
+    got = Out.cpu().numpy()
+    assert not np.isnan(got).any()
+    Gh, Inh = G.cpu().numpy(), In.cpu().numpy()
+    rng = np.random.default_rng(15)
+    mr = _sample(mt * rt, 16, rng, must=(0, 63, 64, mt * rt - 1))
+    T, S = orc.contract_reference_f64(Gh, Inh, mr)
+    Cs = np.ascontiguousarray(got.transpose(0, 2, 1).reshape(mt * rt, bt)[mr])
+    bad, worst = orc.check_tol(Cs, T, S, TOL)
+    assert bad == 0, f"{bad} violations (worst {worst:.3g})"
+
+
 def test_contraction_reference_layout_tolerance(mm, cuda, orc):
     mt, bt, rt, nt, rt_l = 16, 512, 64, 8, 128
     G = orc.normal_f16((rt, nt, mt, rt_l), 6, 0, 0.1)
