@@ -104,6 +104,28 @@ hipError_t mmm_contract5d_f16f32(const mmm_contract_desc* d, const mmm_half* A, 
                                  hipStream_t stream);
 
 /*
+ * On-device cross-check: the reference's GEMM_Naive (mmm.cpp:52-62) with run-time sizes and
+ * leading dimensions.  One fp32 accumulator per output, k ascending, acc += float(a)*float(b);
+ * the result is bit-identical to that loop run on a CPU.  SIMT only; slow by design.
+ */
+hipError_t mmm_gemm_naive_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                                 int64_t ldb, int64_t ldc, hipStream_t stream);
+
+/*
+ * fp64 ground truth for validating a full-size output: T[i][j] = sum_k a*b and, when S is not
+ * NULL, S[i][j] = sum_k |a*b| (both fp64, k ascending; T and S share the leading dimension
+ * ldt).  An fp32 result C is within tolerance when |C - T| <= rel * S.  No reference
+ * counterpart: it takes the place of the reference's rocBLAS comparison
+ * (mmm.cpp:1387-1407, 1519-1545; mmmTensor.cpp:278-306, 393-420).
+ */
+hipError_t mmm_gemm_truth_f64(const mmm_half* A, const mmm_half* B, double* T, double* S, int M, int N, int K,
+                              int64_t lda, int64_t ldb, int64_t ldt, hipStream_t stream);
+
+/* The same for a contraction: T and S are written at the offsets d gives C. */
+hipError_t mmm_contract5d_truth_f64(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, double* T,
+                                    double* S, hipStream_t stream);
+
+/*
  * Seeded synthetic inputs, generated on the device (the reference fills with unseeded
  * rand()/RAND_MAX on the host, mmm.cpp:1409-1414; these are reproducible instead):
  *   key = splitmix64(seed * 0x9E3779B97F4A7C15 + tensor_id + 1), x_i = splitmix64(key + i)

@@ -183,6 +183,45 @@ static bool collapse(int64_t ext_hi, int64_t ext_lo, int64_t s_hi, int64_t s_lo,
   return false;
 }
 
+// Descriptor -> FoldProblem with validated extents.  C may be null (the fp64 check writes its
+// own outputs at C's offsets); the caller checks it where it is needed.
+static hipError_t fold_from_desc(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
+                                 FoldProblem* out) {
+  if (!d) return hipErrorInvalidValue;
+  for (int q = 0; q < 2; ++q)
+    if (d->m_ext[q] < 0 || d->n_ext[q] < 0 || d->k_ext[q] < 0) return hipErrorInvalidValue;
+  const int64_t M = d->m_ext[0] * d->m_ext[1], N = d->n_ext[0] * d->n_ext[1], K = d->k_ext[0] * d->k_ext[1];
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return hipErrorInvalidValue;
+  FoldProblem& p = *out;
+  p = FoldProblem{};
+  p.A = A, p.B = B, p.C = C;
+  p.M = (int)M, p.N = (int)N, p.K = (int)K;
+  if (M == 0 || N == 0) return hipSuccess;
+  if (K > 0 && (!A || !B)) return hipErrorInvalidValue;
+  p.m_lo = (int)(d->m_ext[1] > 0 ? d->m_ext[1] : 1);
+  p.n_lo = (int)(d->n_ext[1] > 0 ? d->n_ext[1] : 1);
+  p.k_lo = (int)(d->k_ext[1] > 0 ? d->k_ext[1] : 1);
+  for (int q = 0; q < 2; ++q) {
+    p.am[q] = d->a_m_stride[q], p.ak[q] = d->a_k_stride[q];
+    p.bk[q] = d->b_k_stride[q], p.bn[q] = d->b_n_stride[q];
+    p.cm[q] = d->c_m_stride[q], p.cn[q] = d->c_n_stride[q];
+  }
+  return hipSuccess;
+}
+
+// A row-major GEMM as a fold whose high sub-indices have extent 1.
+static FoldProblem fold_of_gemm(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                                int64_t ldb, int64_t ldc) {
+  FoldProblem p{};
+  p.A = A, p.B = B, p.C = C;
+  p.M = M, p.N = N, p.K = K;
+  p.m_lo = M > 0 ? M : 1, p.n_lo = N > 0 ? N : 1, p.k_lo = K > 0 ? K : 1;
+  p.am[1] = lda, p.ak[1] = 1;
+  p.bk[1] = ldb, p.bn[1] = 1;
+  p.cm[1] = ldc, p.cn[1] = 1;
+  return p;
+}
+
 }  // namespace mmm
 
 using namespace mmm;
@@ -267,13 +306,11 @@ hipError_t mmm_contract_desc_reference(mmm_contract_desc* d, int mt, int bt, int
 
 hipError_t mmm_contract5d_f16f32(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
                                  hipStream_t stream) {
-  if (!d) return hipErrorInvalidValue;
-  for (int q = 0; q < 2; ++q)
-    if (d->m_ext[q] < 0 || d->n_ext[q] < 0 || d->k_ext[q] < 0) return hipErrorInvalidValue;
-  const int64_t M = d->m_ext[0] * d->m_ext[1], N = d->n_ext[0] * d->n_ext[1], K = d->k_ext[0] * d->k_ext[1];
-  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return hipErrorInvalidValue;
-  if (M == 0 || N == 0) return hipSuccess;
-  if (!C || (K > 0 && (!A || !B))) return hipErrorInvalidValue;
+  FoldProblem p{};
+  hipError_t e = fold_from_desc(d, A, B, C, &p);
+  if (e != hipSuccess || p.M == 0 || p.N == 0) return e;
+  if (!C) return hipErrorInvalidValue;
+  const int64_t M = p.M, N = p.N, K = p.K;
 
   // A fold that is a plain row-major GEMM runs on the GEMM kernels (the benchmark's
   // A[b,i,k,l] x B[k,l,j] -> C[b,i,j] is one: M = b*i, K = k*l, N = j).
@@ -286,20 +323,33 @@ hipError_t mmm_contract5d_f16f32(const mmm_contract_desc* d, const mmm_half* A, 
                      collapse(d->n_ext[0], d->n_ext[1], d->c_n_stride[0], d->c_n_stride[1], &cn) && cn == 1 &&
                      am >= K && bk >= N && cm >= N;
   if (plain) return mmm_gemm_f16f32(A, B, C, (int)M, (int)N, (int)K, am, bk, cm, stream);
-
-  FoldProblem p{};
-  p.A = A, p.B = B, p.C = C;
-  p.M = (int)M, p.N = (int)N, p.K = (int)K;
-  p.m_lo = (int)(d->m_ext[1] > 0 ? d->m_ext[1] : 1);
-  p.n_lo = (int)(d->n_ext[1] > 0 ? d->n_ext[1] : 1);
-  p.k_lo = (int)(d->k_ext[1] > 0 ? d->k_ext[1] : 1);
-  for (int q = 0; q < 2; ++q) {
-    p.am[q] = d->a_m_stride[q], p.ak[q] = d->a_k_stride[q];
-    p.bk[q] = d->b_k_stride[q], p.bn[q] = d->b_n_stride[q];
-    p.cm[q] = d->c_m_stride[q], p.cn[q] = d->c_n_stride[q];
-  }
   if (K == 0) return launch_zero_fold(p, stream);
   return launch_gemm_fold(p, stream);
+}
+
+hipError_t mmm_gemm_naive_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                                 int64_t ldb, int64_t ldc, hipStream_t stream) {
+  hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
+  if (e != hipSuccess || M == 0 || N == 0) return e;
+  if (K == 0) return launch_zero_f32(C, M, N, ldc, stream);
+  return launch_check_fold(fold_of_gemm(A, B, C, M, N, K, lda, ldb, ldc), nullptr, nullptr, stream);
+}
+
+hipError_t mmm_gemm_truth_f64(const mmm_half* A, const mmm_half* B, double* T, double* S, int M, int N, int K,
+                              int64_t lda, int64_t ldb, int64_t ldt, hipStream_t stream) {
+  if (M < 0 || N < 0 || K < 0) return hipErrorInvalidValue;
+  if (M == 0 || N == 0) return hipSuccess;
+  if (!T || (K > 0 && (!A || !B)) || lda < K || ldb < N || ldt < N) return hipErrorInvalidValue;
+  return launch_check_fold(fold_of_gemm(A, B, nullptr, M, N, K, lda, ldb, ldt), T, S, stream);
+}
+
+hipError_t mmm_contract5d_truth_f64(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, double* T,
+                                    double* S, hipStream_t stream) {
+  FoldProblem p{};
+  hipError_t e = fold_from_desc(d, A, B, nullptr, &p);
+  if (e != hipSuccess || p.M == 0 || p.N == 0) return e;
+  if (!T) return hipErrorInvalidValue;
+  return launch_check_fold(p, T, S, stream);
 }
 
 hipError_t mmm_fill_uniform_f16(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream) {

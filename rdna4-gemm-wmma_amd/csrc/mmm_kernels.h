@@ -42,5 +42,8 @@ hipError_t launch_fill_normal(mmm_half* out, int64_t n, uint64_t seed, uint32_t 
                               hipStream_t stream);
 hipError_t launch_zero_f32(float* C, int M, int N, int64_t ldc, hipStream_t stream);
 hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream);
+// Cross-check kernels: fp32 ascending-k accumulation into p.C when T is null, else fp64
+// T = sum a*b and (S non-null) S = sum |a*b|, both at p's C offsets.
+hipError_t launch_check_fold(const FoldProblem& p, double* T, double* S, hipStream_t stream);
 
 }  // namespace mmm

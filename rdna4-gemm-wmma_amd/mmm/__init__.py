@@ -107,9 +107,13 @@ def lib() -> C.CDLL:
     L.mmm_fill_uniform_f16.argtypes = [p, i64, C.c_uint64, C.c_uint32, s]
     L.mmm_fill_normal_f16.argtypes = [p, i64, C.c_uint64, C.c_uint32, C.c_double, s]
     L.mmm_tile_of_block.argtypes = [i, i, i, C.POINTER(i), C.POINTER(i)]
+    L.mmm_gemm_naive_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, s]
+    L.mmm_gemm_truth_f64.argtypes = [p, p, p, p, i, i, i, i64, i64, i64, s]
+    L.mmm_contract5d_truth_f64.argtypes = [C.POINTER(ContractDesc), p, p, p, p, s]
     for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_tiled", "mmm_contract_desc_baseline",
                  "mmm_contract_desc_reference", "mmm_contract5d_f16f32", "mmm_fill_uniform_f16",
-                 "mmm_fill_normal_f16", "mmm_tile_of_block"):
+                 "mmm_fill_normal_f16", "mmm_tile_of_block", "mmm_gemm_naive_f16f32", "mmm_gemm_truth_f64",
+                 "mmm_contract5d_truth_f64"):
         getattr(L, name).restype = C.c_int
     L.mmm_version.restype = C.c_char_p
     L.mmm_version.argtypes = []
@@ -177,6 +181,66 @@ def gemm(A, B, C_out=None, tile=None, stream=None):
         _check("mmm_gemm_f16f32_tiled",
                L.mmm_gemm_f16f32_tiled(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, *params, st))
     return C_out
+
+
+def _gemm_shapes(A, B, out):
+    _check_f16("A", A)
+    _check_f16("B", B)
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[0]:
+        raise ValueError("A must be [M,K] and B [K,N]")
+    if A.stride(1) != 1 or B.stride(1) != 1:
+        raise ValueError("A and B must be row-major (unit stride along the last dimension)")
+    M, K = A.shape
+    N = B.shape[1]
+    lda = A.stride(0) if M > 1 else max(K, 1)
+    ldb = B.stride(0) if K > 1 else max(N, 1)
+    ldo = out.stride(0) if M > 1 else max(N, 1)
+    if out.stride(1) != 1 or tuple(out.shape) != (M, N):
+        raise ValueError("outputs must be row-major [M,N] tensors")
+    return M, N, K, lda, ldb, ldo
+
+
+def gemm_naive(A, B, C_out=None, stream=None):
+    """The reference's GEMM_Naive on the device: fp32 accumulator, k ascending (cross-check)."""
+    import torch
+
+    if C_out is None:
+        C_out = torch.empty((A.shape[0], B.shape[1]), dtype=torch.float32, device=A.device)
+    if C_out.dtype != torch.float32:
+        raise ValueError("C must be float32")
+    M, N, K, lda, ldb, ldc = _gemm_shapes(A, B, C_out)
+    _check("mmm_gemm_naive_f16f32",
+           lib().mmm_gemm_naive_f16f32(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, _stream(stream)))
+    return C_out
+
+
+def gemm_truth(A, B, with_scale: bool = True, stream=None):
+    """fp64 T = A @ B and S = sum_k |a*b| on the device; returns (T, S) (S is None unless asked)."""
+    import torch
+
+    M, N = A.shape[0], B.shape[1]
+    T = torch.empty((M, N), dtype=torch.float64, device=A.device)
+    S = torch.empty_like(T) if with_scale else None
+    M, N, K, lda, ldb, ldt = _gemm_shapes(A, B, T)
+    _check("mmm_gemm_truth_f64",
+           lib().mmm_gemm_truth_f64(_ptr(A), _ptr(B), _ptr(T), _ptr(S) if S is not None else None, M, N, K,
+                                    lda, ldb, ldt, _stream(stream)))
+    return T, S
+
+
+def contract_truth(desc: "ContractDesc", A, B, T_out, S_out=None, stream=None):
+    """fp64 truth (and scale) of a contraction, written at C's offsets into T_out / S_out."""
+    import torch
+
+    _check_f16("A", A)
+    _check_f16("B", B)
+    for t in (T_out, S_out):
+        if t is not None and (t.dtype != torch.float64 or not t.is_cuda):
+            raise TypeError("T and S must be CUDA float64 tensors")
+    _check("mmm_contract5d_truth_f64",
+           lib().mmm_contract5d_truth_f64(C.byref(desc), _ptr(A), _ptr(B), _ptr(T_out),
+                                          _ptr(S_out) if S_out is not None else None, _stream(stream)))
+    return T_out, S_out
 
 
 def contract_desc_baseline(b: int, i: int, k: int, l: int, j: int) -> ContractDesc:
