@@ -240,6 +240,54 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness):
     return res
 
 
+# shapes of the tile sweep (--sweep): squares, the configs, and tall / wide / deep / shallow cases
+SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
+                (6144, 6144, 6144), (8192, 8192, 8192), (8192, 2048, 2048), (2048, 8192, 2048), (4097, 4095, 4111),
+                (16384, 1024, 4096), (1024, 16384, 4096), (8192, 8192, 1024), (1024, 1024, 8192), (3000, 5000, 1000),
+                (64, 4096, 4096), (1536, 1536, 12288)]
+
+
+def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool) -> None:
+    """Every instantiated tile and the library's own choice on each SWEEP_SHAPES problem;
+    median per-launch TFLOP/s, written as a markdown table to path."""
+    tiles = list(mmm.TILES)
+    lines = ["| M x N x K | library pick | pick TFLOP/s | " + " | ".join(tiles) + " | best | pick / best | hipBLASLt |",
+             "|" + "---|" * (len(tiles) + 6)]
+    for (M, N, K) in SWEEP_SHAPES:
+        A = torch.empty((M, K), dtype=torch.float16, device="cuda")
+        B = torch.empty((K, N), dtype=torch.float16, device="cuda")
+        mmm.fill_uniform(A, 7, 0)
+        mmm.fill_uniform(B, 7, 1)
+        Cm = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        flops = 2.0 * M * N * K
+
+        def tf(fn):
+            _, per, _ = time_launches(torch, fn, steps, warmup)
+            return flops / (statistics.median(per) * 1e-3) / 1e12
+
+        plan = mmm.gemm_plan(M, N, K, A=A, B=B, C_out=Cm)
+        pick = plan["kernel"] if plan["kernel"] != "tile" else f"{plan['block_m']}x{plan['block_n']}"
+        if plan["kernel"] == "tile+stream":
+            pick = f"{plan['block_m']}x{plan['block_n']} + stream {plan['stream_rows']}"
+        auto = tf(lambda: mmm.gemm(A, B, Cm))
+        per_tile = {t: tf(lambda t=t: mmm.gemm(A, B, Cm, tile=t)) for t in tiles}
+        best = max(per_tile, key=per_tile.get)
+        wit = float("nan")
+        if with_witness:
+            try:
+                wit = tf(lambda: mmm.witness_hipblaslt(A, B, Cm))
+            except Exception as e:  # witness library absent or hipBLASLt refused the shape
+                _log(f"[sweep] hipBLASLt unavailable for {M}x{N}x{K}: {e}")
+        row = (f"| {M} x {N} x {K} | {pick} | {auto:.1f} | " + " | ".join(f"{per_tile[t]:.1f}" for t in tiles) +
+               f" | {best} | {auto / per_tile[best]:.2f} | {wit:.1f} |")
+        lines.append(row)
+        _log("[sweep] " + row)
+        del A, B, Cm
+        torch.cuda.empty_cache()
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +297,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-witness", action="store_true", help="skip the hipBLASLt comparison")
     ap.add_argument("--report", metavar="PATH", help="measure every workload and write a JSON report to PATH")
+    ap.add_argument("--sweep", metavar="PATH", help="time every tile against the library's pick over a shape "
+                                                     "grid and write a markdown table to PATH")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -266,6 +316,9 @@ def main() -> int:
         print(json.dumps({"error": "no GPU visible"}))
         return 1
     mmm.lib()
+
+    if args.sweep:
+        run_sweep(args.sweep, torch, mmm, args.steps, args.warmup, with_witness=not args.no_witness)
 
     if args.report:
         report = []

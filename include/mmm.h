@@ -61,6 +61,31 @@ hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C,
                                  int64_t lda, int64_t ldb, int64_t ldc, int wave_m, int wave_n, int waves_i,
                                  int waves_j, hipStream_t stream);
 
+/* Kernels mmm_gemm_f16f32 can launch (mmm_gemm_plan.kernel). */
+#define MMM_KERNEL_NONE 0        /* M == 0 or N == 0: nothing */
+#define MMM_KERNEL_ZERO 1        /* K == 0: C = 0 */
+#define MMM_KERNEL_TILE 2        /* matrix-core tile kernel over all of C */
+#define MMM_KERNEL_STREAM 3      /* M <= 16: HBM-streaming kernel */
+#define MMM_KERNEL_TILE_STREAM 4 /* tile kernel on the first tile_rows rows, streaming kernel on the rest */
+
+typedef struct mmm_gemm_plan {
+    int kernel;                            /* MMM_KERNEL_* */
+    int wave_m, wave_n, waves_i, waves_j;  /* tile kernel, as mmm_gemm_f16f32_tiled takes it (0 if none) */
+    int block_m, block_n;                  /* its block tile */
+    int direct_to_lds;                     /* 1: operands stream HBM -> LDS directly; 0: staged in registers */
+    int tile_rows, stream_rows;            /* rows of C on each kernel */
+    int64_t tile_workgroups, stream_workgroups;
+} mmm_gemm_plan;
+
+/*
+ * The launch mmm_gemm_f16f32 makes for these arguments, without launching (host only; no GPU
+ * call).  A, B, C are used only for their alignment and may be NULL (taken as 256-byte
+ * aligned).  No reference counterpart: the reference fixes one tile, <2,2,4,4>, for every
+ * size (mmm.cpp:1462-1465); this exposes the size-dependent choice that replaces it.
+ */
+hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const float* C, int M, int N, int K,
+                                int64_t lda, int64_t ldb, int64_t ldc, mmm_gemm_plan* plan);
+
 /*
  * 5-D tensor contraction descriptor.  Each GEMM axis (m, n, k) is a pair of sub-indices
  * (hi, lo), folded as  m = m_hi * m_ext[1] + m_lo  (same for n and k), and each operand

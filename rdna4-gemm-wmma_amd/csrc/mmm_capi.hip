@@ -148,6 +148,37 @@ static int pick_tile(int M, int N) {
   return best;
 }
 
+static int tile_rows_of(int tile) { return tile == kTile256x256 || tile == kTile256x128 ? 256 : 128; }
+static int tile_cols_of(int tile) { return tile == kTile256x256 || tile == kTile128x256 ? 256 : 128; }
+
+// What mmm_gemm_f16f32 launches for a validated problem.
+struct GemmPlan {
+  int kind;       // MMM_KERNEL_*
+  int tile;       // TileId of the matrix-core kernel, -1 if none
+  int tile_rows;  // rows of C on the matrix-core kernel (the rest on the streaming kernel)
+};
+
+static GemmPlan plan_gemm(const GemmProblem& p) {
+  if (p.M == 0 || p.N == 0) return {MMM_KERNEL_NONE, -1, 0};
+  if (p.K == 0) return {MMM_KERNEL_ZERO, -1, 0};
+  if (skinny_ok(p)) return {MMM_KERNEL_STREAM, -1, 0};  // M <= 16: HBM-bound streaming kernel
+  // A few rows past a whole number of 256-row tiles (4097 = 16*256 + 1) would cost a full
+  // extra round of tiles; those rows go to the streaming kernel instead when that saves a round.
+  const int rem = p.M % 256;
+  if (p.M > 256 && rem > 0 && rem <= 16) {
+    const int Mm = p.M - rem;
+    const int64_t tn = (p.N + 255) / 256;
+    const int64_t rounds_full = ((int64_t)((p.M + 255) / 256) * tn + 255) / 256;
+    const int64_t rounds_main = ((int64_t)(Mm / 256) * tn + 255) / 256;
+    GemmProblem pr = p;
+    pr.M = rem;
+    pr.A = p.A + (int64_t)Mm * p.lda;
+    pr.C = p.C + (int64_t)Mm * p.ldc;
+    if (rounds_main < rounds_full && skinny_ok(pr)) return {MMM_KERNEL_TILE_STREAM, pick_tile(Mm, p.N), Mm};
+  }
+  return {MMM_KERNEL_TILE, pick_tile(p.M, p.N), p.M};
+}
+
 static hipError_t check_gemm(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
                              int64_t ldb, int64_t ldc) {
   if (M < 0 || N < 0 || K < 0) return hipErrorInvalidValue;
@@ -231,31 +262,63 @@ extern "C" {
 hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
                            int64_t ldb, int64_t ldc, hipStream_t stream) {
   hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
-  if (e != hipSuccess || M == 0 || N == 0) return e;
-  if (K == 0) return launch_zero_f32(C, M, N, ldc, stream);
-  GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
-  if (skinny_ok(p)) return launch_gemm_skinny(p, stream);  // M <= 16: HBM-bound streaming kernel
-  // A few rows past a whole number of 256-row tiles (4097 = 16*256 + 1) would cost a full
-  // extra round of tiles; those rows go to the streaming kernel instead when that saves a round.
-  const int rem = M % 256;
-  if (M > 256 && rem > 0 && rem <= 16) {
-    const int Mm = M - rem;
-    const int64_t tn = (N + 255) / 256;
-    const int64_t rounds_full = ((int64_t)((M + 255) / 256) * tn + 255) / 256;
-    const int64_t rounds_main = ((int64_t)(Mm / 256) * tn + 255) / 256;
-    GemmProblem pr = p;
-    pr.M = rem;
-    pr.A = A + (int64_t)Mm * lda;
-    pr.C = C + (int64_t)Mm * ldc;
-    if (rounds_main < rounds_full && skinny_ok(pr)) {
-      GemmProblem pm = p;
-      pm.M = Mm;
-      hipError_t e = launch_gemm_nn(pm, pick_tile(Mm, N), stream);
+  if (e != hipSuccess) return e;
+  const GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
+  const GemmPlan pl = plan_gemm(p);
+  switch (pl.kind) {
+    case MMM_KERNEL_NONE:
+      return hipSuccess;
+    case MMM_KERNEL_ZERO:
+      return launch_zero_f32(C, M, N, ldc, stream);
+    case MMM_KERNEL_STREAM:
+      return launch_gemm_skinny(p, stream);
+    case MMM_KERNEL_TILE_STREAM: {
+      GemmProblem pm = p, pr = p;
+      pm.M = pl.tile_rows;
+      pr.M = M - pl.tile_rows;
+      pr.A = A + (int64_t)pl.tile_rows * lda;
+      pr.C = C + (int64_t)pl.tile_rows * ldc;
+      e = launch_gemm_nn(pm, pl.tile, stream);
       if (e != hipSuccess) return e;
       return launch_gemm_skinny(pr, stream);
     }
+    default:
+      return launch_gemm_nn(p, pl.tile, stream);
   }
-  return launch_gemm_nn(p, pick_tile(M, N), stream);
+}
+
+hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const float* C, int M, int N, int K,
+                                int64_t lda, int64_t ldb, int64_t ldc, mmm_gemm_plan* plan) {
+  if (!plan) return hipErrorInvalidValue;
+  // only the addresses' alignment matters here; null stands for a 256-byte-aligned buffer
+  const mmm_half* a = A ? A : (const mmm_half*)(uintptr_t)256;
+  const mmm_half* b = B ? B : (const mmm_half*)(uintptr_t)256;
+  float* c = C ? (float*)C : (float*)(uintptr_t)256;
+  hipError_t e = check_gemm(a, b, c, M, N, K, lda, ldb, ldc);
+  if (e != hipSuccess) return e;
+  const GemmProblem p{a, b, c, M, N, K, lda, ldb, ldc, false, false};
+  const GemmPlan pl = plan_gemm(p);
+  *plan = mmm_gemm_plan{};
+  plan->kernel = pl.kind;
+  if (pl.tile >= 0) {
+    static const int params[4][4] = {{4, 4, 2, 2}, {2, 4, 2, 2}, {4, 2, 2, 2}, {2, 2, 2, 2}};
+    plan->wave_m = params[pl.tile][0], plan->wave_n = params[pl.tile][1];
+    plan->waves_i = params[pl.tile][2], plan->waves_j = params[pl.tile][3];
+    plan->block_m = tile_rows_of(pl.tile), plan->block_n = tile_cols_of(pl.tile);
+    plan->tile_rows = pl.tile_rows;
+    plan->tile_workgroups = (int64_t)((pl.tile_rows + plan->block_m - 1) / plan->block_m) *
+                            ((N + plan->block_n - 1) / plan->block_n);
+    GemmProblem pm = p;
+    pm.M = pl.tile_rows;
+    plan->direct_to_lds = gemm_nn_direct_to_lds(pm, pl.tile) ? 1 : 0;
+  }
+  if (pl.kind == MMM_KERNEL_STREAM || pl.kind == MMM_KERNEL_TILE_STREAM) {
+    GemmProblem pr = p;
+    pr.M = M - pl.tile_rows;
+    plan->stream_rows = pr.M;
+    plan->stream_workgroups = skinny_workgroups(pr);
+  }
+  return hipSuccess;
 }
 
 hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,

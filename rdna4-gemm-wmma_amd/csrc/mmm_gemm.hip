@@ -827,6 +827,10 @@ static bool tail_aligned(const GemmProblem& p) {
   return !((a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8);
 }
 
+bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id) {
+  return dma_ok(p, tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128);
+}
+
 hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream) {
   GemmProblem p = p0;
   p.c_vec4 = ((uintptr_t)p.C % 16 == 0) && (p.ldc % 4 == 0);

@@ -34,9 +34,11 @@ struct FoldProblem {
 enum TileId { kTile256x256 = 0, kTile128x256 = 1, kTile256x128 = 2, kTile128x128 = 3 };
 
 hipError_t launch_gemm_nn(const GemmProblem& p, int tile_id, hipStream_t stream);
+bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id);  // else the register-staged path
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
 bool skinny_ok(const GemmProblem& p);  // M <= 16 and aligned operands
 hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);
+int skinny_workgroups(const GemmProblem& p);
 hipError_t launch_fill_uniform(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream);
 hipError_t launch_fill_normal(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, double scale,
                               hipStream_t stream);

@@ -271,6 +271,8 @@ bool skinny_ok(const GemmProblem& p) {
   return true;
 }
 
+int skinny_workgroups(const GemmProblem& p) { return (p.N + kNS - 1) / kNS; }
+
 hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
   GemmProblem p = p0;
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;

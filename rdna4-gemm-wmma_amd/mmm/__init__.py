@@ -45,6 +45,14 @@ def _error_name(code: int) -> str:
         return "unknown"
 
 
+class GemmPlan(C.Structure):
+    """mmm_gemm_plan (include/mmm.h)."""
+    _fields_ = [("kernel", C.c_int), ("wave_m", C.c_int), ("wave_n", C.c_int), ("waves_i", C.c_int),
+                ("waves_j", C.c_int), ("block_m", C.c_int), ("block_n", C.c_int), ("direct_to_lds", C.c_int),
+                ("tile_rows", C.c_int), ("stream_rows", C.c_int), ("tile_workgroups", C.c_int64),
+                ("stream_workgroups", C.c_int64)]
+
+
 class ContractDesc(C.Structure):
     """mmm_contract_desc (include/mmm.h)."""
 
@@ -110,10 +118,11 @@ def lib() -> C.CDLL:
     L.mmm_gemm_naive_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, s]
     L.mmm_gemm_truth_f64.argtypes = [p, p, p, p, i, i, i, i64, i64, i64, s]
     L.mmm_contract5d_truth_f64.argtypes = [C.POINTER(ContractDesc), p, p, p, p, s]
+    L.mmm_gemm_plan_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, C.POINTER(GemmPlan)]
     for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_tiled", "mmm_contract_desc_baseline",
                  "mmm_contract_desc_reference", "mmm_contract5d_f16f32", "mmm_fill_uniform_f16",
                  "mmm_fill_normal_f16", "mmm_tile_of_block", "mmm_gemm_naive_f16f32", "mmm_gemm_truth_f64",
-                 "mmm_contract5d_truth_f64"):
+                 "mmm_contract5d_truth_f64", "mmm_gemm_plan_f16f32"):
         getattr(L, name).restype = C.c_int
     L.mmm_version.restype = C.c_char_p
     L.mmm_version.argtypes = []
@@ -181,6 +190,21 @@ def gemm(A, B, C_out=None, tile=None, stream=None):
         _check("mmm_gemm_f16f32_tiled",
                L.mmm_gemm_f16f32_tiled(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, *params, st))
     return C_out
+
+
+KERNELS = {0: "none", 1: "zero", 2: "tile", 3: "stream", 4: "tile+stream"}
+
+
+def gemm_plan(M: int, N: int, K: int, lda=None, ldb=None, ldc=None, A=None, B=None, C_out=None) -> dict:
+    """The launch mmm_gemm_f16f32 would make (host-only query; pointers only matter for alignment)."""
+    pl = GemmPlan()
+    addr = lambda t: C.c_void_p(t.data_ptr() if hasattr(t, "data_ptr") else t) if t is not None else None
+    _check("mmm_gemm_plan_f16f32",
+           lib().mmm_gemm_plan_f16f32(addr(A), addr(B), addr(C_out), M, N, K, K if lda is None else lda,
+                                      N if ldb is None else ldb, N if ldc is None else ldc, C.byref(pl)))
+    out = {f: getattr(pl, f) for f, _ in GemmPlan._fields_}
+    out["kernel"] = KERNELS[pl.kernel]
+    return out
 
 
 def _gemm_shapes(A, B, out):

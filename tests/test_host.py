@@ -151,3 +151,52 @@ int main() {
     assert r.returncode == 0, r.stderr
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0 and r.stdout.strip() == "0", r.stdout + r.stderr
+
+
+def test_isa_report(tmp_path):
+    """Every gfx950 kernel: wave64, no VGPR spill or scratch, LDS within one CU's 160 KiB; the
+    main tiles issue matrix-core ops and direct-to-LDS loads; the committed report lists them."""
+    from mmm import isa
+
+    rows = isa.collect(str(tmp_path))
+    names = [r["kernel"] for r in rows]
+    assert any(n.startswith("gemm_nn_kernel") for n in names)
+    assert "gemm_skinny_kernel" in names
+    assert any(n.startswith("check_fold_kernel") for n in names)
+    for r in rows:
+        assert r["wavefront"] == 64, r["kernel"]
+        assert r["scratch"] == 0 and r["vgpr_spill"] == 0, r["kernel"]
+        assert r["lds"] <= isa.LDS_PER_CU, r["kernel"]
+        assert r["vgpr_total"] <= isa.VGPRS_PER_SIMD, r["kernel"]
+        assert r["wg_per_cu"] >= 1, r["kernel"]
+    main = [r for r in rows if r["kernel"].startswith("gemm_nn_kernel<Tile<256, 256, 2, 4")]
+    assert main and main[0]["mfma"] > 0 and main[0]["dma_lds"] > 0
+    committed = open(os.path.join(REPO, "profiles", "isa_resources.md")).read()
+    missing = [n for n in names if f"`{n}`" not in committed]
+    assert not missing, f"profiles/isa_resources.md is stale; regenerate it (missing {missing})"
+
+
+def test_gemm_plan(mm):
+    """The launch the library chooses, queried without a GPU (mmm_gemm_plan_f16f32)."""
+    p = mm.gemm_plan(8192, 8192, 8192)
+    assert p["kernel"] == "tile" and (p["block_m"], p["block_n"]) == (256, 256)
+    assert p["direct_to_lds"] == 1 and p["tile_workgroups"] == 32 * 32 and p["stream_rows"] == 0
+    p = mm.gemm_plan(4097, 4095, 4111)  # one row past 16 tile rows: that row streams
+    assert p["kernel"] == "tile+stream" and p["tile_rows"] == 4096 and p["stream_rows"] == 1
+    assert p["stream_workgroups"] == (4095 + 31) // 32
+    p = mm.gemm_plan(16, 8192, 8192)
+    assert p["kernel"] == "stream" and p["stream_rows"] == 16 and p["tile_workgroups"] == 0
+    assert mm.gemm_plan(5, 5, 0)["kernel"] == "zero"
+    assert mm.gemm_plan(0, 5, 5)["kernel"] == "none"
+    # odd addresses cannot use the direct-to-LDS loads or the streaming kernel
+    p = mm.gemm_plan(300, 264, 200, A=3)
+    assert p["kernel"] == "tile" and p["direct_to_lds"] == 0
+    assert mm.gemm_plan(8, 64, 64, A=3)["kernel"] == "tile"
+    for shape in [(256, 256, 256), (1000, 3000, 70), (8192, 2048, 2048), (17, 4096, 4096), (6000, 200, 50)]:
+        p = mm.gemm_plan(*shape)
+        assert (p["wave_m"], p["wave_n"], p["waves_i"], p["waves_j"]) in mm.TILES.values()
+        assert p["block_m"] == p["waves_i"] * p["wave_m"] * 32 and p["block_n"] == p["waves_j"] * p["wave_n"] * 32
+    with pytest.raises(mm.MMMError):
+        mm.gemm_plan(64, 64, 64, lda=32)
+    with pytest.raises(mm.MMMError):
+        mm.gemm_plan(-1, 64, 64)
