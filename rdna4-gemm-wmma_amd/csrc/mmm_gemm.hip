@@ -45,6 +45,15 @@
 #ifndef MMM_SETPRIO
 #define MMM_SETPRIO 0  // 1: raise wave priority while issuing MFMAs
 #endif
+#ifndef MMM_XSTAGE
+#define MMM_XSTAGE 1  // 1: cross-stage pipeline (next tile's barrier and first reads under the last K-step)
+#endif
+#ifndef MMM_XFENCE
+#define MMM_XFENCE 0  // cross-stage loop: 1 keeps every earlier MFMA ahead of the tile barrier
+#endif
+#ifndef MMM_XSCHED
+#define MMM_XSCHED 1  // cross-stage loop: 0 compiler order, 1 next-step reads before MFMAs, 2 reads 1:1 among MFMAs
+#endif
 
 namespace mmm {
 
@@ -77,6 +86,7 @@ struct Tile {
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int RA = BM * CA / NT;  // A chunks per thread per stage
   static constexpr int RB = BK * CB / NT;  // B chunks per thread per stage
+  static constexpr int LPT = RA + RB;      // direct-to-LDS loads per thread per stage
   // A-row swizzle (chunk c of row m stored at c ^ swz_a(m)).  Rows of 128 B (BK = 64):
   // 8 consecutive rows take 8 distinct chunk slots and 16 consecutive rows 16 distinct
   // 16-byte bank groups of the 256-byte bank window.  Rows of 64 B (BK = 32): four rows share
@@ -142,6 +152,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
 
+// Wait until at most n tiles of LPT loads each are still in flight (0 <= n <= NMAX; n is
+// wave-uniform, the branch is scalar).
+template <int LPT, int NMAX>
+__device__ __forceinline__ void wait_tiles(int n) {
+  static_assert(NMAX * LPT <= 63, "vmcnt range");
+  if constexpr (NMAX == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (n >= NMAX)
+      wait_vmcnt<NMAX * LPT>();
+    else
+      wait_tiles<LPT, NMAX - 1>(n);
+  }
+}
+
 __device__ __forceinline__ uint32_t lds_addr_of(const char LDS_AS* p) { return (uint32_t)(uintptr_t)p; }
 
 __device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
@@ -156,33 +181,46 @@ __device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
 //              b_off[nb] addresses fragment nb, K-steps add whole rows.
 // BKM = true : B stage is [BN][BK] (K contiguous, swizzled like A), fragments by one
 //              ds_read_b128; b_off[kk] addresses K-step kk, fragments add 32 rows.
+// One K-step's MFMA operands for a wave: FM A fragments and FN B fragments.
+template <class T>
+struct Frags {
+  half8 a[T::FM], b[T::FN];
+};
+
+// Fragment reads of K-step kk from an LDS stage (layouts as for compute_stage below).
+template <class T, bool BKM>
+__device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char LDS_AS* b_st,
+                                           const uint32_t (&a_off)[T::KSTEPS], const uint32_t (&b_off)[4], int kk,
+                                           Frags<T>& f) {
+#pragma unroll
+  for (int mb = 0; mb < T::FM; ++mb) f.a[mb] = lds_read_a(a_st + a_off[kk] + mb * 32 * T::BK * 2);
+#pragma unroll
+  for (int nb = 0; nb < T::FN; ++nb) {
+    if constexpr (BKM)
+      f.b[nb] = lds_read_a(b_st + b_off[kk] + nb * 32 * T::BK * 2);
+    else
+      f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * 16) * T::BN * 2, b_st + b_off[nb] + (kk * 16 + 4) * T::BN * 2);
+  }
+}
+
+template <class T>
+__device__ __forceinline__ void mfma_frags(const Frags<T>& f, f32x16 (&acc)[T::FM][T::FN]) {
+  if (MMM_SETPRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+  for (int mb = 0; mb < T::FM; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb)
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[nb], f.a[mb], acc[mb][nb], 0, 0, 0);
+  if (MMM_SETPRIO) __builtin_amdgcn_s_setprio(0);
+}
+
 template <class T, bool BKM, class Hook>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const char LDS_AS* b_st,
                                               const uint32_t (&a_off)[T::KSTEPS], const uint32_t (&b_off)[4],
                                               f32x16 (&acc)[T::FM][T::FN], Hook&& after_first_reads) {
-  struct Frags {
-    half8 a[T::FM], b[T::FN];
-  };
-  auto load = [&](int kk, Frags& f) {
-#pragma unroll
-    for (int mb = 0; mb < T::FM; ++mb) f.a[mb] = lds_read_a(a_st + a_off[kk] + mb * 32 * T::BK * 2);
-#pragma unroll
-    for (int nb = 0; nb < T::FN; ++nb) {
-      if constexpr (BKM)
-        f.b[nb] = lds_read_a(b_st + b_off[kk] + nb * 32 * T::BK * 2);
-      else
-        f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * 16) * T::BN * 2, b_st + b_off[nb] + (kk * 16 + 4) * T::BN * 2);
-    }
-  };
-  auto mfma = [&](const Frags& f) {
-    if (MMM_SETPRIO) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int mb = 0; mb < T::FM; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < T::FN; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[nb], f.a[mb], acc[mb][nb], 0, 0, 0);
-    if (MMM_SETPRIO) __builtin_amdgcn_s_setprio(0);
-  };
+  using Frags = mmm::Frags<T>;
+  auto load = [&](int kk, Frags& f) { load_frags<T, BKM>(a_st, b_st, a_off, b_off, kk, f); };
+  auto mfma = [&](const Frags& f) { mfma_frags<T>(f, acc); };
 #if MMM_PIPE_FRAGS
   // Fragments double-buffered in registers: step kk+1's reads are issued before step kk's
   // MFMAs (scheduling barriers keep that order), so LDS latency hides under MFMA work.
@@ -338,6 +376,79 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         issue(t, stage);
     };
 
+#if MMM_XSTAGE
+    // Ring of S slots, tile u in slot u % S.  Cross-stage pipeline: during the last K-step of
+    // tile t, this wave waits for its own loads of tile t+1, then the barrier (a) publishes
+    // tile t+1 -- every wave's loads of it have landed -- and (b) retires slot t % S: every
+    // wave has completed its reads of tile t, since a barrier waits for outstanding LDS reads
+    // and tile t's last fragments were read before it.  After the barrier the wave reads
+    // tile t+1's first fragments and refills slot t % S with tile t+S, and only then issues
+    // tile t's last MFMAs, which cover the barrier and the first reads' latency.
+    constexpr int S = T::STAGES;
+    static_assert(T::KSTEPS % 2 == 0, "fragment double buffer alternates per K-step");
+    const int first = KT < S ? KT : S;
+    for (int s = 0; s < first; ++s) issue_tile(s, s);
+    // tile 0 must land; later tiles may stay in flight (a gathered last tile has no loads)
+    wait_tiles<T::LPT, S - 1>(first - 1 - ((p.tail_regs && first == KT) ? 1 : 0));
+    block_sync();
+    Frags<T> f[2];
+    load_frags<T, false>(lds_base, lds_base + T::A_BYTES, a_off, b_off, 0, f[0]);
+    int cur = 0;
+    // K-steps 0 .. KSTEPS-2 of the tile in slot `cur` (each step's MFMAs run while the next
+    // step's fragments are read).
+    auto tile_body = [&] {
+      const char LDS_AS* st = lds_base + cur * T::STAGE;
+#pragma unroll
+      for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
+        load_frags<T, false>(st, st + T::A_BYTES, a_off, b_off, kk + 1, f[(kk + 1) & 1]);
+        mfma_frags<T>(f[kk & 1], acc);
+        if constexpr (MMM_XSCHED == 1) {
+          __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);  // the step's LDS reads
+          __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);      // then its MFMAs
+        } else if constexpr (MMM_XSCHED == 2) {
+#pragma unroll
+          for (int i = 0; i < T::FM * T::FN; ++i) {
+            if (i < T::FM + 2 * T::FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          }
+        }
+      }
+    };
+    // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
+    // retired slot (`refill` loads tile t+S into slot `cur`), then the MFMAs.
+    auto tile_next = [&](int t, auto&& refill) {
+      const int issued = t + S < KT ? t + S : KT;  // tiles 0 .. issued-1 are issued
+      int ahead = issued - (t + 2);                // of those, after t+1 (may stay in flight)
+      if (p.tail_regs && issued == KT && ahead > 0) --ahead;
+      if constexpr (MMM_XFENCE) __builtin_amdgcn_sched_barrier(0);
+      wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(ahead);
+      block_sync();
+      const int nslot = cur + 1 == S ? 0 : cur + 1;
+      const char LDS_AS* ns = lds_base + nslot * T::STAGE;
+      load_frags<T, false>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
+      refill();
+      mfma_frags<T>(f[1], acc);
+      cur = nslot;
+    };
+    // steady state refills by DMA only; the refill of the last tile (possibly gathered
+    // through VGPRs) is peeled so the loop carries no gather registers
+    int t = 0;
+    for (; t + S < KT - 1; ++t) {
+      tile_body();
+      tile_next(t, [&] { issue(t + S, cur); });
+    }
+    if (t + S == KT - 1) {
+      tile_body();
+      tile_next(t, [&] { issue_tile(t + S, cur); });
+      ++t;
+    }
+    for (; t + 1 < KT; ++t) {
+      tile_body();
+      tile_next(t, [] {});
+    }
+    tile_body();
+    mfma_frags<T>(f[1], acc);
+#else
     // Ring of STAGES slots, P = STAGES-1 tiles in flight ahead of the one computed.  At the
     // top of iteration t: wait until tile t has landed (this wave's loads complete in order,
     // so at most (P-1) tiles' loads may stay outstanding), barrier (every wave's part of tile
@@ -375,6 +486,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, NoHook{});
       cur = cur + 1 == T::STAGES ? 0 : cur + 1;
     }
+#endif
   } else {
     static_assert(!GENERIC || T::STAGES == 2, "the register-staged path double-buffers");
     u32x4 ra[T::RA], rb[T::RB];
