@@ -13,8 +13,12 @@
  *
  * Conventions (all entry points):
  *  - fp16 tensors are passed as pointers to IEEE binary16 bit patterns (mmm_half).
- *  - Pointers are device pointers owned by the caller.  No entry point allocates device
- *    memory, synchronises the host, or exits the process.
+ *  - Pointers are device pointers owned by the caller.  No entry point synchronises the host
+ *    or exits the process.  The only device memory the library allocates is the workspace
+ *    of the M <= 16 streaming kernel's K split: 4 MiB + 64 KiB per (device, stream), on the
+ *    first such call on that stream, kept until the process exits.  A call made while its
+ *    stream is being captured into a graph never allocates: without a workspace it runs a
+ *    variant that needs none (same results).
  *  - C is overwritten (alpha = 1, beta = 0, as mmm.cpp:1512-1513 and the kernel's store at
  *    mmm.cpp:1370); C is never read.
  *  - Errors: hipErrorInvalidValue for null pointers, negative sizes or leading dimensions
@@ -22,7 +26,9 @@
  *    M == 0 or N == 0 is a no-op; K == 0 writes zeros to C.
  *  - Work is enqueued on `stream` (0 = the null stream, as the reference) and is
  *    asynchronous, as the reference's launches are (the caller synchronises, mmm.cpp:1491).
- *  - Thread safety: the library keeps no mutable global state.
+ *  - Thread safety: the only mutable global state is the workspace table, guarded by a
+ *    mutex.  Calls on one stream are ordered and share its workspace; different streams
+ *    never share one.
  */
 #ifndef MMM_H
 #define MMM_H
@@ -75,6 +81,8 @@ typedef struct mmm_gemm_plan {
     int direct_to_lds;                     /* 1: operands stream HBM -> LDS directly; 0: staged in registers */
     int tile_rows, stream_rows;            /* rows of C on each kernel */
     int64_t tile_workgroups, stream_workgroups;
+    int stream_splits;                     /* K ranges of the streaming kernel reduced across
+                                              workgroups (0: split among one workgroup's waves) */
 } mmm_gemm_plan;
 
 /*

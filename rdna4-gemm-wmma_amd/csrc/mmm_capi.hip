@@ -317,6 +317,7 @@ hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const floa
     pr.M = M - pl.tile_rows;
     plan->stream_rows = pr.M;
     plan->stream_workgroups = skinny_workgroups(pr);
+    plan->stream_splits = skinny_splits(pr);
   }
   return hipSuccess;
 }

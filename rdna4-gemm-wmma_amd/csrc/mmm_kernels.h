@@ -39,6 +39,7 @@ hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
 bool skinny_ok(const GemmProblem& p);  // M <= 16 and aligned operands
 hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);
 int skinny_workgroups(const GemmProblem& p);
+int skinny_splits(const GemmProblem& p);  // K ranges reduced across workgroups (0: within one)
 hipError_t launch_fill_uniform(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream);
 hipError_t launch_fill_normal(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, double scale,
                               hipStream_t stream);

@@ -17,6 +17,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "mmm.h"
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
@@ -95,22 +99,14 @@ __device__ __forceinline__ int swz_a(int row) { return kKS == 64 ? ((row >> 1) &
 
 }  // namespace
 
-__global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int strips) {
-  __shared__ __attribute__((aligned(1024))) char lds[kWaves * kSlots * kSlot];
-  const int strip = __builtin_amdgcn_readfirstlane(xcd_compact(blockIdx.x, strips));
-  const int n0 = strip * kNS;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+// Streams K steps [s_begin, s_end) of the 32-column strip at n0 through this wave's private
+// LDS ring and accumulates the 16 x 32 product into acc (16x16 tiles j, lane (fr, fg) holding
+// rows 4*fg .. 4*fg+3 of column 16*j + fr).  No barrier: the wave waits on its own loads only.
+__device__ __forceinline__ void stream_columns(const GemmProblem& p, int n0, int s_begin, int s_end, int nst_all,
+                                               char LDS_AS* ring, int lane, f32x4 (&acc)[kNT]) {
   const int M = p.M, N = p.N, K = p.K;
   const int64_t lda = p.lda, ldb = p.ldb;
-
-  // this wave's K steps
-  const int nst_all = (K + kKS - 1) / kKS;
-  const int s_begin = __builtin_amdgcn_readfirstlane((w * nst_all) / kWaves);
-  const int s_end = __builtin_amdgcn_readfirstlane(((w + 1) * nst_all) / kWaves);
   const int nst = s_end - s_begin;
-
-  char LDS_AS* ring = (char LDS_AS*)lds + w * kSlots * kSlot;
   const uint32_t ring_addr = (uint32_t)(uintptr_t)ring;
 
   // DMA map.  A [16][KS]: CA = KS/8 chunks per row; one wave-wide instruction covers
@@ -195,9 +191,6 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
   for (int q = 0; q < KQ; ++q) a_off[q] = fr * (kKS * 2) + (((4 * q + fg) ^ swz_a(fr)) * 16);
   const uint32_t b_off = kABytes + (8 * fg + (fr >> 2)) * (kNS * 2) + 4 * (fr & 3) * 2;
 
-  f32x4 acc[kNT];
-#pragma unroll
-  for (int j = 0; j < kNT; ++j) acc[j] = f32x4{};
   auto compute = [&](int slot) {
     const char LDS_AS* sl = ring + slot * kSlot;
 #pragma unroll
@@ -241,6 +234,25 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
     compute(cur);
     cur = cur + 1 == kSlots ? 0 : cur + 1;
   }
+}
+
+__global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int strips) {
+  __shared__ __attribute__((aligned(1024))) char lds[kWaves * kSlots * kSlot];
+  const int strip = __builtin_amdgcn_readfirstlane(xcd_compact(blockIdx.x, strips));
+  const int n0 = strip * kNS;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = p.M, N = p.N, K = p.K;
+
+  // this wave's K steps (the four waves split K; their partials are summed through LDS)
+  const int nst_all = (K + kKS - 1) / kKS;
+  const int s_begin = __builtin_amdgcn_readfirstlane((w * nst_all) / kWaves);
+  const int s_end = __builtin_amdgcn_readfirstlane(((w + 1) * nst_all) / kWaves);
+  f32x4 acc[kNT];
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) acc[j] = f32x4{};
+  stream_columns(p, n0, s_begin, s_end, nst_all, (char LDS_AS*)lds + w * kSlots * kSlot, lane, acc);
+  const int fr = lane & 15, fg = lane >> 4;
 
   // K-partials -> LDS (after every wave is done with its ring), fixed-order sum, store.
   __syncthreads();
@@ -261,6 +273,60 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
   }
 }
 
+// One workgroup per 128-column strip and K split: the four waves stream adjacent 32-column
+// strips over the same K range (256 contiguous bytes of each B row per CU), and the
+// `splits` K ranges of a strip run in separate workgroups.  With splits == 1 the waves store
+// C directly; otherwise each workgroup stores its 16 x 128 partial to the workspace and
+// reduce_splits_kernel, launched next on the same stream, sums the partials of every strip
+// in split order (a fixed order: results are deterministic).  The kernel boundary orders
+// the partial stores before their reads; no workgroup waits for another.
+__global__ __launch_bounds__(256, 1) void gemm_stream_kernel(GemmProblem p, int strips, int splits, float* partials) {
+  __shared__ __attribute__((aligned(1024))) char lds[kWaves * kSlots * kSlot];
+  const int b = blockIdx.x;
+  const int strip = b % strips, q = b / strips;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = p.M, N = p.N, K = p.K;
+  const int n0 = strip * 128 + w * kNS;
+  const int nst_all = (K + kKS - 1) / kKS;
+  const int s_begin = __builtin_amdgcn_readfirstlane((q * nst_all) / splits);
+  const int s_end = __builtin_amdgcn_readfirstlane(((q + 1) * nst_all) / splits);
+  f32x4 acc[kNT];
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) acc[j] = f32x4{};
+  stream_columns(p, n0, s_begin, s_end, nst_all, (char LDS_AS*)lds + w * kSlots * kSlot, lane, acc);
+  const int fr = lane & 15, fg = lane >> 4;
+
+  if (splits == 1) {
+#pragma unroll
+    for (int j = 0; j < kNT; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 4 * fg + v, col = n0 + 16 * j + fr;
+        if (row < M && col < N) p.C[(int64_t)row * p.ldc + col] = acc[j][v];
+      }
+    return;
+  }
+  float* mine = partials + (int64_t)(strip * splits + q) * (16 * 128);
+#pragma unroll
+  for (int j = 0; j < kNT; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) mine[(4 * fg + v) * 128 + w * kNS + 16 * j + fr] = acc[j][v];
+}
+
+// C[16][strip * 128 + c] = sum over q = 0 .. splits-1 (in that order) of the strip's partials;
+// one thread per element of the 16 x 128 strip tiles.
+__global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int strips, int splits,
+                                                            const float* partials) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int strip = idx >> 11, e = idx & 2047, row = e >> 7, col = strip * 128 + (e & 127);
+  if (strip >= strips) return;
+  const float* base = partials + (int64_t)strip * splits * 2048 + e;
+  float sum = base[0];
+  for (int q = 1; q < splits; ++q) sum += base[q * 2048];
+  if (row < p.M && col < p.N) p.C[(int64_t)row * p.ldc + col] = sum;
+}
+
 bool skinny_ok(const GemmProblem& p) {
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   if (p.M > 16 || p.M < 1) return false;
@@ -271,12 +337,76 @@ bool skinny_ok(const GemmProblem& p) {
   return true;
 }
 
-int skinny_workgroups(const GemmProblem& p) { return (p.N + kNS - 1) / kNS; }
+// ---- launch shape.  Split kernel: 128-column strips x `splits` K ranges, aiming at one
+// workgroup per CU (256), at least 4 ring slots of K per split, and at most kWsTiles partial
+// tiles in the workspace.  A split count of 1 needs no workspace; it is used when the strips
+// alone fill the chip.  Otherwise the wave-split kernel (32-column strips) runs.
+constexpr int kWsTiles = 512;  // 16 x 128 fp32 partial tiles (4 MiB)
+constexpr size_t kWsBytes = (size_t)kWsTiles * 16 * 128 * 4;
+
+struct StreamShape {
+  int strips, splits;  // split kernel: grid strips * splits; splits == 0: wave-split kernel
+};
+
+static StreamShape stream_shape(const GemmProblem& p) {
+  const int strips = (p.N + 127) / 128;
+  const int nst_all = (p.K + kKS - 1) / kKS;
+  int splits = (256 + strips - 1) / strips;
+  splits = splits < 16 ? splits : 16;
+  splits = splits < nst_all / 4 ? splits : nst_all / 4;
+  if (splits > kWsTiles / strips) splits = kWsTiles / strips;
+  if (splits < 1) splits = 1;
+  if (splits == 1 && strips < 256) return {strips, 0};
+  return {strips, splits};
+}
+
+int skinny_splits(const GemmProblem& p) { return stream_shape(p).splits; }
+
+int skinny_workgroups(const GemmProblem& p) {
+  const StreamShape sh = stream_shape(p);
+  return sh.splits ? sh.strips * sh.splits : (p.N + kNS - 1) / kNS;
+}
+
+// ---- workspace of the split kernel: partial tiles, one workspace per (device, stream),
+// allocated on first use outside stream capture and kept until the process exits.  Calls on
+// one stream are ordered, so they share its workspace safely; different streams never share.
+static std::mutex g_ws_mu;
+static std::map<std::pair<int, uintptr_t>, float*> g_ws;
+
+static float* stream_workspace(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  const auto key = std::make_pair(dev, (uintptr_t)stream);
+  const auto it = g_ws.find(key);
+  if (it != g_ws.end()) return it->second;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  void* mem = nullptr;
+  if (hipMalloc(&mem, kWsBytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  g_ws[key] = (float*)mem;
+  return (float*)mem;
+}
 
 hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
   GemmProblem p = p0;
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   p.tail_regs = (a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8;
+  const StreamShape sh = stream_shape(p);
+  float* ws = sh.splits > 1 ? stream_workspace(stream) : nullptr;
+  if (sh.splits == 1 || ws) {
+    hipLaunchKernelGGL(gemm_stream_kernel, dim3(sh.strips * sh.splits), dim3(256), 0, stream, p, sh.strips,
+                       sh.splits, ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || sh.splits == 1) return e;
+    hipLaunchKernelGGL(reduce_splits_kernel, dim3(sh.strips * 8), dim3(256), 0, stream, p, sh.strips, sh.splits,
+                       (const float*)ws);
+    return hipGetLastError();
+  }
+  // wave-split kernel: no workspace (also the path under stream capture before a workspace exists)
   const int strips = (p.N + kNS - 1) / kNS;
   hipLaunchKernelGGL(gemm_skinny_kernel, dim3(strips), dim3(256), 0, stream, p, strips);
   return hipGetLastError();

@@ -234,6 +234,81 @@ def test_exact_row_remainder_split(mm, cuda, shape):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
+def _exact_case(rng, M, N, K):
+    A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
+    return A, B, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
+
+
+# (M, N, K) -> K ranges the streaming kernel reduces across workgroups (0: within one workgroup)
+STREAM_SPLITS = [((16, 8192, 8192), 4), ((7, 16384, 4096), 2), ((16, 4096, 8192), 8), ((5, 1024, 8192), 16),
+                 ((16, 32768, 512), 1), ((3, 2000, 4000), 15), ((16, 4095, 4111), 8), ((1, 130, 9000), 16),
+                 ((16, 8192, 256), 0), ((2, 264, 200), 0)]
+
+
+@pytest.mark.parametrize("case", STREAM_SPLITS, ids=lambda c: "x".join(map(str, c[0])) + f"-s{c[1]}")
+def test_exact_stream_splits(mm, cuda, case):
+    """The streaming kernel at every K-split count, the unsplit wide launch and the in-workgroup
+    split; exact against int64 (the partial sums are integers, so any order is exact)."""
+    (M, N, K), splits = case
+    assert mm.gemm_plan(M, N, K)["stream_splits"] == splits
+    A, B, truth = _exact_case(np.random.default_rng(M * 7 + N + K), M, N, K)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)
+    C = Cd.cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
+def test_stream_split_repeat_and_resize(mm, cuda):
+    """Arrival counters return to zero after every call: shapes with different strip and
+    split counts alternate on one stream, each checked."""
+    rng = np.random.default_rng(5)
+    cases = [_exact_case(rng, *shp) for shp in [(16, 8192, 2048), (4, 1024, 4096), (16, 4096, 1024)]]
+    dev = [(to_dev(cuda, A), to_dev(cuda, B), truth) for A, B, truth in cases]
+    for _ in range(3):
+        for A, B, truth in dev:
+            assert np.array_equal(mm.gemm(A, B).cpu().numpy(), truth)
+
+
+def test_stream_split_concurrent_streams(mm, cuda):
+    """Two streams run split launches at the same time; each stream has its own workspace."""
+    rng = np.random.default_rng(6)
+    A1, B1, t1 = _exact_case(rng, 16, 8192, 4096)
+    A2, B2, t2 = _exact_case(rng, 8, 8192, 4096)
+    A1, B1, A2, B2 = (to_dev(cuda, x) for x in (A1, B1, A2, B2))
+    s1, s2 = cuda.cuda.Stream(), cuda.cuda.Stream()
+    outs = []
+    cuda.cuda.synchronize()
+    for _ in range(4):
+        with cuda.cuda.stream(s1):
+            C1 = mm.gemm(A1, B1)
+        with cuda.cuda.stream(s2):
+            C2 = mm.gemm(A2, B2)
+        outs.append((C1, C2))
+    cuda.cuda.synchronize()
+    for C1, C2 in outs:
+        assert np.array_equal(C1.cpu().numpy(), t1)
+        assert np.array_equal(C2.cpu().numpy(), t2)
+
+
+def test_stream_graph_capture(mm, cuda):
+    """Captured into a HIP graph (no allocation during capture: a stream without a workspace
+    takes the in-workgroup kernel); every replay, with eager work in between, matches eager."""
+    rng = np.random.default_rng(8)
+    A, B, truth = _exact_case(rng, 16, 8192, 2048)
+    A, B = to_dev(cuda, A), to_dev(cuda, B)
+    C = cuda.full((16, 8192), float("nan"), dtype=cuda.float32, device="cuda")
+    g = cuda.cuda.CUDAGraph()
+    with cuda.cuda.graph(g):
+        mm.gemm(A, B, C)
+    for i in range(3):
+        C.fill_(float("nan"))
+        g.replay()
+        cuda.cuda.synchronize()
+        assert np.array_equal(C.cpu().numpy(), truth), f"replay {i}"
+        assert np.array_equal(mm.gemm(A, B).cpu().numpy(), truth)
+
+
 def test_skinny_deterministic(mm, cuda, orc):
     A = to_dev(cuda, orc.uniform_f16((16, 8192), 4, 0))
     B = to_dev(cuda, orc.uniform_f16((8192, 8192), 4, 1))

@@ -183,9 +183,14 @@ def test_gemm_plan(mm):
     assert p["direct_to_lds"] == 1 and p["tile_workgroups"] == 32 * 32 and p["stream_rows"] == 0
     p = mm.gemm_plan(4097, 4095, 4111)  # one row past 16 tile rows: that row streams
     assert p["kernel"] == "tile+stream" and p["tile_rows"] == 4096 and p["stream_rows"] == 1
-    assert p["stream_workgroups"] == (4095 + 31) // 32
+    # 32 strips of 128 columns, K split 8 ways across workgroups
+    assert p["stream_workgroups"] == 32 * 8 and p["stream_splits"] == 8
     p = mm.gemm_plan(16, 8192, 8192)
     assert p["kernel"] == "stream" and p["stream_rows"] == 16 and p["tile_workgroups"] == 0
+    assert p["stream_splits"] == 4 and p["stream_workgroups"] == 64 * 4
+    # too little K to split: 32-column strips, K split among each workgroup's waves
+    p = mm.gemm_plan(16, 8192, 128)
+    assert p["stream_splits"] == 0 and p["stream_workgroups"] == 8192 // 32
     assert mm.gemm_plan(5, 5, 0)["kernel"] == "zero"
     assert mm.gemm_plan(0, 5, 5)["kernel"] == "none"
     # odd addresses cannot use the direct-to-LDS loads or the streaming kernel
