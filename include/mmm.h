@@ -15,10 +15,11 @@
  *  - fp16 tensors are passed as pointers to IEEE binary16 bit patterns (mmm_half).
  *  - Pointers are device pointers owned by the caller.  No entry point synchronises the host
  *    or exits the process.  The only device memory the library allocates is the workspace
- *    of the M <= 16 streaming kernel's K split: 4 MiB + 64 KiB per (device, stream), on the
- *    first such call on that stream, kept until the process exits.  A call made while its
- *    stream is being captured into a graph never allocates: without a workspace it runs a
- *    variant that needs none (same results).
+ *    of its K splits (launches that would leave most of the chip idle split K across
+ *    workgroups and sum the partials in a fixed order): 32 MiB per (device, stream), on the
+ *    first split call on that stream, kept until the process exits.  A call made while its
+ *    stream is being captured into a graph never allocates: without a workspace it runs
+ *    unsplit (the streaming kernel's variant gives the same results bit for bit).
  *  - C is overwritten (alpha = 1, beta = 0, as mmm.cpp:1512-1513 and the kernel's store at
  *    mmm.cpp:1370); C is never read.
  *  - Errors: hipErrorInvalidValue for null pointers, negative sizes or leading dimensions
@@ -83,6 +84,8 @@ typedef struct mmm_gemm_plan {
     int64_t tile_workgroups, stream_workgroups;
     int stream_splits;                     /* K ranges of the streaming kernel reduced across
                                               workgroups (0: split among one workgroup's waves) */
+    int tile_splits;                       /* K ranges of the tile kernel (1: no split); a split
+                                              launch is followed by an ordered reduction kernel */
 } mmm_gemm_plan;
 
 /*

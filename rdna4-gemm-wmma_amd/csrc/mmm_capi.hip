@@ -4,11 +4,43 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "mmm.h"
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
 
 namespace mmm {
+
+// ---------------------------------------------------------------- split-reduction workspace
+// One workspace per (device, stream), allocated on first use outside stream capture and kept
+// until the process exits.  Calls on one stream are ordered, so they share its workspace
+// safely (a split launch and its reduction finish before the next call's kernels start);
+// different streams never share one.  Nothing in it needs initialising: every partial a
+// reduction reads is written by the launch before it.
+static std::mutex g_ws_mu;
+static std::map<std::pair<int, uintptr_t>, float*> g_ws;
+
+float* stream_workspace(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  const auto key = std::make_pair(dev, (uintptr_t)stream);
+  const auto it = g_ws.find(key);
+  if (it != g_ws.end()) return it->second;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  void* mem = nullptr;
+  if (hipMalloc(&mem, kStreamWorkspaceBytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  g_ws[key] = (float*)mem;
+  return (float*)mem;
+}
 
 // ---------------------------------------------------------------- seeded input generator
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
@@ -122,27 +154,36 @@ hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------- tile selection
-// Estimated cost of a tile shape: rounds of 256 concurrent workgroups (one per CU) times
-// the work per tile over the tile's relative MFMA efficiency (larger wave tiles read less
-// LDS per MAC).
-static int pick_tile(int M, int N) {
-  struct Cand {
-    int id, bm, bn;
+// Estimated time of a tile launch, in seconds: rounds of 256 concurrent workgroups (one per
+// CU) times the MFMA time of one tile's K range at the tile's relative efficiency (measured
+// at 8192^3: 256x256 1.0, 128x256 0.92, 256x128 0.87, 128x128 0.83 -- larger wave tiles read
+// less LDS per MAC), a fixed per-round cost (prologue, epilogue), and, for a K split, the
+// reduction's traffic and launch.
+static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
+  static const struct {
+    int bm, bn;
     double eff;
-  };
-  const Cand cands[] = {{kTile256x256, 256, 256, 1.0},
-                        {kTile256x128, 256, 128, 0.85},
-                        {kTile128x256, 128, 256, 0.85},
-                        {kTile128x128, 128, 128, 0.70}};
-  int best = kTile256x256;
+  } shape[4] = {{256, 256, 1.0}, {128, 256, 0.92}, {256, 128, 0.87}, {128, 128, 0.83}};
+  const int bm = shape[tile].bm, bn = shape[tile].bn;
+  const int splits = gemm_nn_splits(p, tile);
+  const double tiles = (double)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+  const double rounds = std::ceil(tiles * splits / 256.0);
+  const double k = std::ceil((double)p.K / splits / 64.0) * 64.0;
+  const double per_cu_flops = 4.4e12;  // sustained MFMA rate of one CU under load
+  double t = rounds * (2.0 * bm * bn * k / (per_cu_flops * shape[tile].eff) + 3e-6);
+  if (splits > 1) t += tiles * bm * bn * 4.0 * (splits + 1) / 4e12 + 3e-6;
+  *splits_out = splits;
+  return t;
+}
+
+static int pick_tile(const GemmProblem& p) {
+  int best = kTile256x256, s = 1;
   double best_cost = 1e300;
-  for (const Cand& c : cands) {
-    const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-    const int64_t rounds = (tiles + 255) / 256;
-    const double cost = (double)rounds * c.bm * c.bn / c.eff;
-    if (cost < best_cost * 0.999) {
-      best_cost = cost;
-      best = c.id;
+  for (int tile : {kTile256x256, kTile128x256, kTile256x128, kTile128x128}) {
+    const double c = tile_cost(p, tile, &s);
+    if (c < best_cost * 0.999) {
+      best_cost = c;
+      best = tile;
     }
   }
   return best;
@@ -174,9 +215,11 @@ static GemmPlan plan_gemm(const GemmProblem& p) {
     pr.M = rem;
     pr.A = p.A + (int64_t)Mm * p.lda;
     pr.C = p.C + (int64_t)Mm * p.ldc;
-    if (rounds_main < rounds_full && skinny_ok(pr)) return {MMM_KERNEL_TILE_STREAM, pick_tile(Mm, p.N), Mm};
+    GemmProblem pm = p;
+    pm.M = Mm;
+    if (rounds_main < rounds_full && skinny_ok(pr)) return {MMM_KERNEL_TILE_STREAM, pick_tile(pm), Mm};
   }
-  return {MMM_KERNEL_TILE, pick_tile(p.M, p.N), p.M};
+  return {MMM_KERNEL_TILE, pick_tile(p), p.M};
 }
 
 static hipError_t check_gemm(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
@@ -311,6 +354,7 @@ hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const floa
     GemmProblem pm = p;
     pm.M = pl.tile_rows;
     plan->direct_to_lds = gemm_nn_direct_to_lds(pm, pl.tile) ? 1 : 0;
+    plan->tile_splits = gemm_nn_splits(pm, pl.tile);
   }
   if (pl.kind == MMM_KERNEL_STREAM || pl.kind == MMM_KERNEL_TILE_STREAM) {
     GemmProblem pr = p;

@@ -258,8 +258,13 @@ template <class T, bool GENERIC>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
 
+  // K split (direct-to-LDS path only): blocks [q * tiles, (q+1) * tiles) compute K range q of
+  // every tile; each split layer walks the tiles in the same XCD-aware order.
+  const int nsplit = (!GENERIC && p.k_splits > 1) ? p.k_splits : 1;
+  const int ntiles = tiles_m * tiles_n;
+  const int q = __builtin_amdgcn_readfirstlane((int)blockIdx.x / ntiles);
   int tm, tn;
-  tile_of_block(blockIdx.x, tiles_m, tiles_n, 4, &tm, &tn);
+  tile_of_block((int)blockIdx.x - q * ntiles, tiles_m, tiles_n, 4, &tm, &tn);
   // The tile origin is uniform; readfirstlane keeps it (and everything derived from it, such
   // as the buffer descriptors) in SGPRs -- the integer divisions above are expanded on the VALU.
   const int m0 = __builtin_amdgcn_readfirstlane(tm * T::BM), n0 = __builtin_amdgcn_readfirstlane(tn * T::BN);
@@ -303,7 +308,10 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
 #pragma unroll
     for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x16{};
 
-  const int KT = (K + T::BK - 1) / T::BK;
+  const int KT_all = (K + T::BK - 1) / T::BK;
+  const int t_begin = __builtin_amdgcn_readfirstlane((q * KT_all) / nsplit);
+  const int t_end = __builtin_amdgcn_readfirstlane(((q + 1) * KT_all) / nsplit);
+  const int KT = t_end - t_begin;  // K tiles of this block
   char LDS_AS* lds_base = (char LDS_AS*)lds;
 
   if constexpr (!GENERIC) {
@@ -313,7 +321,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
 
     // DMA of K tile t into ring slot `stage`: RA + RB buffer_load_dwordx4 ... lds per thread.
     auto issue = [&](int t, int stage) {
-      const int k0 = t * T::BK;
+      const int k0 = (t_begin + t) * T::BK;
       // Each range ends at the operand's last element (row M-1, column K-1 of A; row K-1,
       // column N-1 of B), so nothing past the caller's data is ever fetched; rows past the
       // end read as zero.  With N, K multiples of 8 no chunk straddles a range end.
@@ -340,7 +348,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     const _Float16* Ah = (const _Float16*)p.A;
     const _Float16* Bh = (const _Float16*)p.B;
     auto fill_regs = [&](int t, int stage) {
-      const int k0 = t * T::BK;
+      const int k0 = (t_begin + t) * T::BK;
       char LDS_AS* a_dst = lds_base + stage * T::STAGE + (w * 64 + lane) * 16;
       char LDS_AS* b_dst = a_dst + T::A_BYTES;
 #pragma unroll
@@ -368,7 +376,8 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         *(half8 LDS_AS*)(b_dst + r * T::NT * 16) = v;
       }
     };
-    const bool tail_regs = p.tail_regs;
+    // only the block holding the globally last K tile gathers it
+    const bool tail_regs = p.tail_regs && t_end == KT_all;
     auto issue_tile = [&](int t, int stage) {
       if (tail_regs && t == KT - 1)
         fill_regs(t, stage);
@@ -389,7 +398,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     const int first = KT < S ? KT : S;
     for (int s = 0; s < first; ++s) issue_tile(s, s);
     // tile 0 must land; later tiles may stay in flight (a gathered last tile has no loads)
-    wait_tiles<T::LPT, S - 1>(first - 1 - ((p.tail_regs && first == KT) ? 1 : 0));
+    wait_tiles<T::LPT, S - 1>(first - 1 - ((tail_regs && first == KT) ? 1 : 0));
     block_sync();
     Frags<T> f[2];
     load_frags<T, false>(lds_base, lds_base + T::A_BYTES, a_off, b_off, 0, f[0]);
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     auto tile_next = [&](int t, auto&& refill) {
       const int issued = t + S < KT ? t + S : KT;  // tiles 0 .. issued-1 are issued
       int ahead = issued - (t + 2);                // of those, after t+1 (may stay in flight)
-      if (p.tail_regs && issued == KT && ahead > 0) --ahead;
+      if (tail_regs && issued == KT && ahead > 0) --ahead;
       if constexpr (MMM_XFENCE) __builtin_amdgcn_sched_barrier(0);
       wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(ahead);
       block_sync();
@@ -489,6 +498,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
 #endif
   } else {
     static_assert(!GENERIC || T::STAGES == 2, "the register-staged path double-buffers");
+    (void)t_begin;
     u32x4 ra[T::RA], rb[T::RB];
     const _Float16* A = (const _Float16*)p.A;
     const _Float16* B = (const _Float16*)p.B;
@@ -547,6 +557,20 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   }
 
   // ---- epilogue: lane owns row m, columns n..n+3 for each (mb, nb, q).
+  if (nsplit > 1) {  // K split: the whole tile (rows/columns past M/N included) to the partials
+    float* part = p.partials + ((int64_t)(tm * tiles_n + tn) * nsplit + q) * (T::BM * T::BN);
+#pragma unroll
+    for (int mb = 0; mb < T::FM; ++mb) {
+      float* prow = part + (wm * T::TM + 32 * mb + (lane & 31)) * T::BN + wn * T::TN + 4 * (lane >> 5);
+#pragma unroll
+      for (int nb = 0; nb < T::FN; ++nb)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq)
+          *(f32x4*)(prow + 32 * nb + 8 * qq) = f32x4{acc[mb][nb][4 * qq + 0], acc[mb][nb][4 * qq + 1],
+                                                      acc[mb][nb][4 * qq + 2], acc[mb][nb][4 * qq + 3]};
+    }
+    return;
+  }
   float* C = p.C;
   const int64_t ldc = p.ldc;
   const bool vec_ok = p.c_vec4;
@@ -859,13 +883,43 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
 // ------------------------------------------------------------------------------------
 // Host-side launch
 // ------------------------------------------------------------------------------------
+// C tile = sum over the K splits, in split order (fixed order: deterministic), of the partial
+// tiles written by gemm_nn_kernel; one thread per 4 consecutive columns.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void reduce_tiles_kernel(GemmProblem p, int tiles_n, int splits) {
+  constexpr int F4 = BM * BN / 4;  // float4s per tile
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int tile = (int)(g / F4), e = (int)(g % F4);
+  const int r = e / (BN / 4), c = 4 * (e % (BN / 4));
+  const int m = (tile / tiles_n) * BM + r, n = (tile % tiles_n) * BN + c;
+  if (m >= p.M || n >= p.N) return;
+  const f32x4* src = (const f32x4*)(p.partials + (int64_t)tile * splits * (BM * BN)) + e;
+  f32x4 sum = src[0];
+  for (int s = 1; s < splits; ++s) sum += src[(int64_t)s * F4];
+  float* crow = p.C + (int64_t)m * p.ldc;
+  if (p.c_vec4 && n + 3 < p.N) {
+    *(f32x4*)(crow + n) = sum;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (n + i < p.N) crow[n + i] = sum[i];
+  }
+}
+
 template <class T, bool GENERIC>
 static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
   const int tiles_m = (p.M + T::BM - 1) / T::BM;
   const int tiles_n = (p.N + T::BN - 1) / T::BN;
-  const int64_t blocks = (int64_t)tiles_m * tiles_n;
-  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_nn_kernel<T, GENERIC>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m, tiles_n);
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
+  const int splits = p.k_splits > 1 ? p.k_splits : 1;
+  if (tiles * splits > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_nn_kernel<T, GENERIC>), dim3((unsigned)(tiles * splits)), dim3(T::NT), 0, stream, p,
+                     tiles_m, tiles_n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  const int64_t per_tile = T::BM * T::BN / 4 / 256;  // blocks of 256 float4s per tile
+  hipLaunchKernelGGL((reduce_tiles_kernel<T::BM, T::BN>), dim3((unsigned)(tiles * per_tile)), dim3(256), 0, stream,
+                     p, tiles_n, splits);
   return hipGetLastError();
 }
 
@@ -943,10 +997,35 @@ bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id) {
   return dma_ok(p, tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128);
 }
 
+// K splits for a tile launch that leaves most of the chip idle: enough layers to reach about
+// one workgroup per CU (256), at least 8 K tiles per split, at most 16 splits, and the partial
+// tiles within the stream workspace.  Direct-to-LDS path only.
+int gemm_nn_splits(const GemmProblem& p, int tile_id) {
+  if (!gemm_nn_direct_to_lds(p, tile_id)) return 1;
+  const int bm = tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128;
+  const int bn = tile_id == kTile256x256 || tile_id == kTile128x256 ? 256 : 128;
+  const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+  if (tiles >= 128) return 1;
+  const int kt = (p.K + 63) / 64;  // 64-deep K tiles (the 32-deep tiles have twice as many)
+  int64_t splits = 256 / tiles;
+  if (splits > kt / 8) splits = kt / 8;
+  if (splits > 16) splits = 16;
+  const int64_t cap = (int64_t)(kStreamWorkspaceBytes / ((size_t)bm * bn * 4)) / tiles;
+  if (splits > cap) splits = cap;
+  return splits >= 2 ? (int)splits : 1;
+}
+
 hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream) {
   GemmProblem p = p0;
   p.c_vec4 = ((uintptr_t)p.C % 16 == 0) && (p.ldc % 4 == 0);
   p.tail_regs = !tail_aligned(p);
+  p.k_splits = 1;
+  p.partials = nullptr;
+  const int splits = gemm_nn_splits(p, tile_id);
+  if (splits > 1) {
+    float* ws = stream_workspace(stream);  // none under stream capture: no split then
+    if (ws) p.k_splits = splits, p.partials = ws;
+  }
   switch (tile_id) {
     case kTile256x256:
       return dma_ok(p, 256) ? launch_nn<DmaTile<256, 256>, false>(p, stream)

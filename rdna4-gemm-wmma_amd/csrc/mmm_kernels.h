@@ -17,6 +17,8 @@ struct GemmProblem {
   int64_t lda, ldb, ldc;
   bool c_vec4;     // set by the launcher: C 16-byte aligned and ldc % 4 == 0
   bool tail_regs;  // set by the launcher: gather the last K tile through VGPRs
+  int k_splits;    // tile kernel: K ranges computed by separate workgroups (<= 1: none)
+  float* partials; // k_splits > 1: [tile][split][BM][BN] fp32 partial tiles
 };
 
 // Folded problem (the 5-D contraction descriptor, see mmm.h), with int32 extents.
@@ -35,6 +37,11 @@ enum TileId { kTile256x256 = 0, kTile128x256 = 1, kTile256x128 = 2, kTile128x128
 
 hipError_t launch_gemm_nn(const GemmProblem& p, int tile_id, hipStream_t stream);
 bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id);  // else the register-staged path
+int gemm_nn_splits(const GemmProblem& p, int tile_id);          // K splits the tile launch would use
+// Per-(device, stream) scratch for split reductions (partial tiles), allocated on first use
+// outside stream capture; null when unavailable.  kStreamWorkspaceBytes long.
+constexpr size_t kStreamWorkspaceBytes = (size_t)32 << 20;
+float* stream_workspace(hipStream_t stream);
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
 bool skinny_ok(const GemmProblem& p);  // M <= 16 and aligned operands
 hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);

@@ -17,9 +17,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <map>
-#include <mutex>
-#include <utility>
 
 #include "mmm.h"
 #include "mmm_kernels.h"
@@ -341,8 +338,8 @@ bool skinny_ok(const GemmProblem& p) {
 // workgroup per CU (256), at least 4 ring slots of K per split, and at most kWsTiles partial
 // tiles in the workspace.  A split count of 1 needs no workspace; it is used when the strips
 // alone fill the chip.  Otherwise the wave-split kernel (32-column strips) runs.
-constexpr int kWsTiles = 512;  // 16 x 128 fp32 partial tiles (4 MiB)
-constexpr size_t kWsBytes = (size_t)kWsTiles * 16 * 128 * 4;
+constexpr int kWsTiles = 512;  // 16 x 128 fp32 partial tiles (4 MiB of the stream workspace)
+static_assert((size_t)kWsTiles * 16 * 128 * 4 <= kStreamWorkspaceBytes, "partials must fit the workspace");
 
 struct StreamShape {
   int strips, splits;  // split kernel: grid strips * splits; splits == 0: wave-split kernel
@@ -365,30 +362,6 @@ int skinny_splits(const GemmProblem& p) { return stream_shape(p).splits; }
 int skinny_workgroups(const GemmProblem& p) {
   const StreamShape sh = stream_shape(p);
   return sh.splits ? sh.strips * sh.splits : (p.N + kNS - 1) / kNS;
-}
-
-// ---- workspace of the split kernel: partial tiles, one workspace per (device, stream),
-// allocated on first use outside stream capture and kept until the process exits.  Calls on
-// one stream are ordered, so they share its workspace safely; different streams never share.
-static std::mutex g_ws_mu;
-static std::map<std::pair<int, uintptr_t>, float*> g_ws;
-
-static float* stream_workspace(hipStream_t stream) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  const auto key = std::make_pair(dev, (uintptr_t)stream);
-  const auto it = g_ws.find(key);
-  if (it != g_ws.end()) return it->second;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-  void* mem = nullptr;
-  if (hipMalloc(&mem, kWsBytes) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  g_ws[key] = (float*)mem;
-  return (float*)mem;
 }
 
 hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {

@@ -309,6 +309,45 @@ def test_stream_graph_capture(mm, cuda):
         assert np.array_equal(mm.gemm(A, B).cpu().numpy(), truth)
 
 
+# (M, N, K, tile or None) -> K splits of the tile kernel
+TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((64, 4096, 4096, None), 8), ((300, 264, 2048, None), 4),
+               ((100, 200, 1001, None), 2), ((256, 512, 4096, "256x256"), 8), ((256, 512, 2048, "256x128"), 4),
+               ((200, 300, 3000, "128x256"), 5), ((2000, 2000, 512, None), 1)]
+
+
+@pytest.mark.parametrize("case", TILE_SPLITS, ids=lambda c: "x".join(map(str, c[0][:3])) + f"-{c[0][3]}-s{c[1]}")
+def test_exact_tile_splits(mm, cuda, case):
+    """K split across workgroups on every tile (and with a gathered last K tile): exact."""
+    (M, N, K, tile), splits = case
+    if tile is None:
+        assert mm.gemm_plan(M, N, K)["tile_splits"] == splits
+    A, B, truth = _exact_case(np.random.default_rng(M + 3 * N + K), M, N, K)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd, tile=tile)
+    C = Cd.cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
+def test_tile_split_deterministic_and_graph(mm, cuda, orc):
+    """A split launch is bitwise reproducible, and a captured graph's replays match it."""
+    A = to_dev(cuda, orc.uniform_f16((1024, 8192), 9, 0))
+    B = to_dev(cuda, orc.uniform_f16((8192, 1024), 9, 1))
+    C1 = mm.gemm(A, B).cpu().numpy()
+    C2 = mm.gemm(A, B).cpu().numpy()
+    assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))
+    C = cuda.full((1024, 1024), float("nan"), dtype=cuda.float32, device="cuda")
+    g = cuda.cuda.CUDAGraph()
+    with cuda.cuda.graph(g):
+        mm.gemm(A, B, C)
+    T, S = mm.gemm_truth(A, B)
+    for i in range(3):
+        C.fill_(float("nan"))
+        g.replay()
+        cuda.cuda.synchronize()
+        d = (C.double() - T).abs()
+        assert bool((d <= 1e-3 * S).all()), f"replay {i}"
+
+
 def test_skinny_deterministic(mm, cuda, orc):
     A = to_dev(cuda, orc.uniform_f16((16, 8192), 4, 0))
     B = to_dev(cuda, orc.uniform_f16((8192, 8192), 4, 1))
