@@ -1,19 +1,20 @@
-// Skinny GEMM for M <= 16 (decode-shaped, e.g. 16 x 8192 x 8192): HBM-bound, so the design
-// goal is to stream B once at full bandwidth with the MFMA work hidden underneath.
+// Streaming GEMM for M <= 16 (decode-shaped, e.g. 16 x 8192 x 8192): HBM-bound, so the design
+// goal is to stream B once at full bandwidth with the MFMA work hidden underneath.  Two kernels:
 //
-//  * One 256-thread workgroup per 32-column strip of C (= of B).  Strips are ordered so each
-//    XCD owns a contiguous range of them: neighbouring strips share 128-byte lines of B, and
-//    those lines are then fetched into one L2 only.
-//  * The four waves split K into contiguous ranges.  Each wave streams its range through its
-//    own 6-slot LDS ring (36 KB per wave) with direct-to-LDS buffer loads, and only reads
-//    what it loaded itself, so the loop has no workgroup barrier: a wave waits on its own
-//    vmcnt only.  Five slots in flight per wave (80 KB of B per CU) cover ~2.5 us of memory
-//    latency at 8 TB/s / 256 CUs.
-//  * A slot holds a KS-deep K step: A [16][KS] (rows swizzled so 16 rows at one chunk hit
-//    16 bank groups) and B [KS][NS] (N contiguous).
-//  * Math: v_mfma_f32_16x16x32_f16, A fragment by ds_read_b128, B fragment by two
-//    ds_read_b64_tr_b16 (transposing 4x16 blocks into the K-contiguous operand layout).
-//  * The four K-partial 16x32 tiles are summed through LDS in a fixed order (deterministic).
+//  * gemm_stream_wide_kernel (the default when a workspace is available): one workgroup per
+//    128-column strip and K range; every wave streams the strip's full 256-byte rows of B
+//    over its quarter of the range; K partials summed through LDS, K ranges across
+//    workgroups summed by reduce_splits_kernel in a fixed order.
+//  * gemm_skinny_kernel (no workspace, e.g. under graph capture): one workgroup per 32-column
+//    strip, XCD-contiguous; the four waves split K; partials summed through LDS.
+//
+// Common to both: each wave streams through its own LDS ring with direct-to-LDS buffer loads
+// and only reads what it loaded itself, so the loop has no workgroup barrier (a wave waits on
+// its own vmcnt only).  A slot holds a KS-deep K step: A [16][KS] (rows swizzled so 16 rows
+// at one chunk hit 16 bank groups) and B [KS][NS] (N contiguous).  Math:
+// v_mfma_f32_16x16x32_f16, A fragment by ds_read_b128, B fragment by two ds_read_b64_tr_b16
+// (transposing 4x16 blocks into the K-contiguous operand layout).  All sums run in fixed
+// orders, so results are deterministic.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -270,47 +271,6 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
   }
 }
 
-// One workgroup per 128-column strip and K split: the four waves stream adjacent 32-column
-// strips over the same K range (256 contiguous bytes of each B row per CU), and the
-// `splits` K ranges of a strip run in separate workgroups.  With splits == 1 the waves store
-// C directly; otherwise each workgroup stores its 16 x 128 partial to the workspace and
-// reduce_splits_kernel, launched next on the same stream, sums the partials of every strip
-// in split order (a fixed order: results are deterministic).  The kernel boundary orders
-// the partial stores before their reads; no workgroup waits for another.
-__global__ __launch_bounds__(256, 1) void gemm_stream_kernel(GemmProblem p, int strips, int splits, float* partials) {
-  __shared__ __attribute__((aligned(1024))) char lds[kWaves * kSlots * kSlot];
-  const int b = blockIdx.x;
-  const int strip = b % strips, q = b / strips;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int M = p.M, N = p.N, K = p.K;
-  const int n0 = strip * 128 + w * kNS;
-  const int nst_all = (K + kKS - 1) / kKS;
-  const int s_begin = __builtin_amdgcn_readfirstlane((q * nst_all) / splits);
-  const int s_end = __builtin_amdgcn_readfirstlane(((q + 1) * nst_all) / splits);
-  f32x4 acc[kNT];
-#pragma unroll
-  for (int j = 0; j < kNT; ++j) acc[j] = f32x4{};
-  stream_columns(p, n0, s_begin, s_end, nst_all, (char LDS_AS*)lds + w * kSlots * kSlot, lane, acc);
-  const int fr = lane & 15, fg = lane >> 4;
-
-  if (splits == 1) {
-#pragma unroll
-    for (int j = 0; j < kNT; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 4 * fg + v, col = n0 + 16 * j + fr;
-        if (row < M && col < N) p.C[(int64_t)row * p.ldc + col] = acc[j][v];
-      }
-    return;
-  }
-  float* mine = partials + (int64_t)(strip * splits + q) * (16 * 128);
-#pragma unroll
-  for (int j = 0; j < kNT; ++j)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) mine[(4 * fg + v) * 128 + w * kNS + 16 * j + fr] = acc[j][v];
-}
-
 // C[16][strip * 128 + c] = sum over q = 0 .. splits-1 (in that order) of the strip's partials;
 // one thread per element of the 16 x 128 strip tiles.
 __global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int strips, int splits,
@@ -334,10 +294,206 @@ bool skinny_ok(const GemmProblem& p) {
   return true;
 }
 
+// ------------------------------------------------------------------------------------
+// Split streaming kernel (M <= 16, enough K): one workgroup per 128-column strip and K range
+// q of `splits`.  Each wave streams the whole strip -- 256 contiguous bytes of every B row --
+// over its own quarter of the workgroup's K range, through a private LDS ring (no barrier in
+// the loop); the four K partials are summed through LDS in wave order.  With splits == 1 the
+// sum goes to C; otherwise to the workspace, and reduce_splits_kernel, launched next on the
+// same stream, sums the splits of every strip in split order (fixed orders throughout:
+// deterministic; the kernel boundary orders the partial stores before their reads).  B slots
+// [KS][128] use the tile kernel's row swizzle (chunk c of row k at c ^ {0,6,10,12}[k & 3]) so
+// the transposing reads of four 256-byte rows hit distinct banks.
+// ------------------------------------------------------------------------------------
+#ifndef MMM_WIDE_KS
+#define MMM_WIDE_KS 64
+#endif
+#ifndef MMM_WIDE_SLOTS
+#define MMM_WIDE_SLOTS 2
+#endif
+namespace wide {
+constexpr int NS = 128, KS = MMM_WIDE_KS, SLOTS = MMM_WIDE_SLOTS;
+constexpr int ABYTES = 16 * KS * 2, BBYTES = KS * NS * 2, SLOT = ABYTES + BBYTES;
+constexpr int NA = ABYTES / 1024, NB = BBYTES / 1024, LOADS = NA + NB;
+constexpr int NT = NS / 16, CPR = NS / 8, RPI = 64 / CPR;  // 8 tiles, 16 chunks per row, 4 rows
+constexpr int CA = KS / 8, RPI_A = 64 / CA;
+static_assert(KS == 32 || KS == 64, "K rows per slot");
+static_assert(kWaves * SLOTS * SLOT <= 160 * 1024, "rings must fit the LDS");
+__device__ __forceinline__ int wswz_a(int row) { return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
+__device__ __forceinline__ int wswz_b(int k) { return (0xCA60 >> (4 * (k & 3))) & 15; }
+}  // namespace wide
+
+__global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p, int strips, int splits,
+                                                                  float* partials) {
+  using namespace wide;
+  __shared__ __attribute__((aligned(1024))) char lds[kWaves * SLOTS * SLOT];
+  const int b = blockIdx.x;
+  const int strip = b % strips, q = b / strips;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int M = p.M, N = p.N, K = p.K;
+  const int64_t lda = p.lda, ldb = p.ldb;
+  const int n0 = strip * NS;
+  const int nst_all = (K + KS - 1) / KS;
+  // the workgroup's K slots, then this wave's quarter of them
+  const int g_begin = (q * nst_all) / splits, g_end = ((q + 1) * nst_all) / splits;
+  const int s_begin = __builtin_amdgcn_readfirstlane(g_begin + (w * (g_end - g_begin)) / kWaves);
+  const int s_end = __builtin_amdgcn_readfirstlane(g_begin + ((w + 1) * (g_end - g_begin)) / kWaves);
+  const int nst = s_end - s_begin;
+  char LDS_AS* ring = (char LDS_AS*)lds + w * SLOTS * SLOT;
+  const uint32_t ring_addr = (uint32_t)(uintptr_t)ring;
+
+  // DMA map.  A [16][KS]: lane -> row lane/CA (+ RPI_A per instruction), slot chunk lane%CA
+  // holding logical chunk (lane%CA) ^ wswz_a(row).  B [KS][128]: lane -> row lane/CPR (+ RPI
+  // per instruction), slot chunk lane%CPR holding logical chunk (lane%CPR) ^ wswz_b(row).
+  const int a_row = lane / CA;
+  uint32_t a_goff[NA];
+  int a_kc[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int row = a_row + i * RPI_A;
+    a_kc[i] = 8 * ((lane % CA) ^ wswz_a(row));
+    a_goff[i] = (uint32_t)((row * lda + a_kc[i]) * 2);
+  }
+  const int b_row = lane / CPR;
+  const int b_nc = 8 * ((lane % CPR) ^ wswz_b(b_row));  // swz_b depends on row % 4 = b_row (RPI = 4)
+  const uint32_t b_goff = (uint32_t)((b_row * ldb + b_nc) * 2);
+  const uint32_t b_rstep = (uint32_t)(RPI * ldb * 2);
+  const i32x4 rb_full = make_rsrc(p.B + n0, clip_records(((int64_t)(K - 1) * ldb + N - n0) * 2));
+
+  auto issue = [&](int s, int slot) {
+    const int k0 = (s_begin + s) * KS;
+    const i32x4 ra = make_rsrc(p.A + k0, clip_records(((int64_t)(M - 1) * lda + K - k0) * 2));
+    const uint32_t dst = ring_addr + slot * SLOT;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const uint32_t dead = (uint32_t)(K - 1 - (k0 + a_kc[i])) >> 31;
+      dma_b128(dst + i * 1024, ra, a_goff[i] + dead * kOobOffset);
+    }
+    const uint32_t bk = (uint32_t)((int64_t)k0 * ldb * 2);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) dma_b128(dst + ABYTES + i * 1024, rb_full, bk + b_goff + i * b_rstep);
+  };
+  // globally last K slot of an unaligned problem: gathered element by element (same layout)
+  const _Float16* Ah = (const _Float16*)p.A;
+  const _Float16* Bh = (const _Float16*)p.B;
+  auto gather = [&](int s, int slot) {
+    const int k0 = (s_begin + s) * KS;
+    char LDS_AS* dst = ring + slot * SLOT + lane * 16;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int row = a_row + i * RPI_A, k = k0 + a_kc[i];
+      half8 v = {};
+      if (row < M) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (k + e < K) v[e] = Ah[(int64_t)row * lda + k + e];
+      }
+      *(half8 LDS_AS*)(dst + i * 1024) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int k = k0 + i * RPI + b_row, n = n0 + b_nc;
+      half8 v = {};
+      if (k < K) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n + e < N) v[e] = Bh[(int64_t)k * ldb + n + e];
+      }
+      *(half8 LDS_AS*)(dst + ABYTES + i * 1024) = v;
+    }
+  };
+  const bool gather_last = p.tail_regs && s_end == nst_all && nst > 0;
+  auto fill = [&](int s, int slot) {
+    if (gather_last && s == nst - 1)
+      gather(s, slot);
+    else
+      issue(s, slot);
+  };
+
+  // fragments: A row fr, k 8*fg..; B column 16*j + fr, k rows 8*fg + (fr>>2) (+4)
+  const int fr = lane & 15, fg = lane >> 4;
+  constexpr int KQ = KS / 32;
+  uint32_t a_off[KQ];
+#pragma unroll
+  for (int qq = 0; qq < KQ; ++qq) a_off[qq] = fr * (KS * 2) + (((4 * qq + fg) ^ wswz_a(fr)) * 16);
+  const int bk_row = 8 * fg + (fr >> 2);
+  const int bsw = wswz_b(bk_row);  // same for the +4 row
+  f32x4 acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) acc[j] = f32x4{};
+  auto compute = [&](int slot) {
+    const char LDS_AS* sl = ring + slot * SLOT;
+#pragma unroll
+    for (int qq = 0; qq < KQ; ++qq) {
+      const half8 af = *(const half8 LDS_AS*)(sl + a_off[qq]);
+      const char LDS_AS* brow = sl + ABYTES + (32 * qq + bk_row) * (NS * 2);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int n = 16 * j + 4 * (fr & 3);
+        const char LDS_AS* bp = brow + (((n >> 3) ^ bsw) * 16) + (n & 7) * 2;
+        fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)bp);
+        fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)(bp + 4 * NS * 2));
+        const half8 bf = __builtin_shufflevector(__builtin_bit_cast(half4, lo), __builtin_bit_cast(half4, hi), 0, 1,
+                                                 2, 3, 4, 5, 6, 7);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
+      }
+    }
+  };
+
+  constexpr int P = SLOTS - 1;
+  for (int s = 0; s < P; ++s)
+    if (s < nst) fill(s, s);
+  int cur = 0, nxt = P;
+  int t = 0;
+  for (; t + P < nst - 1; ++t) {
+    wait_vmcnt<(P - 1) * LOADS>();
+    wait_lgkm0();
+    issue(t + P, nxt);
+    compute(cur);
+    cur = cur + 1 == SLOTS ? 0 : cur + 1;
+    nxt = nxt + 1 == SLOTS ? 0 : nxt + 1;
+  }
+  if (t + P == nst - 1) {
+    wait_vmcnt<(P - 1) * LOADS>();
+    wait_lgkm0();
+    fill(t + P, nxt);
+    compute(cur);
+    cur = cur + 1 == SLOTS ? 0 : cur + 1;
+    ++t;
+  }
+  for (; t < nst; ++t) {
+    wait_vmcnt<0>();
+    compute(cur);
+    cur = cur + 1 == SLOTS ? 0 : cur + 1;
+  }
+
+  // four K partials -> LDS, summed in wave order, to C (one split) or the workspace
+  __syncthreads();
+  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][16][128]
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[(w * 16 + 4 * fg + v) * NS + 16 * j + fr] = acc[j][v];
+  __syncthreads();
+  float* mine = splits > 1 ? partials + (int64_t)(strip * splits + q) * (16 * NS) : nullptr;
+#pragma unroll
+  for (int e = 0; e < 16 * NS / 256; ++e) {
+    const int idx = tid + 256 * e, row = idx / NS, col = idx % NS;
+    const float sum = ((part[(0 * 16 + row) * NS + col] + part[(1 * 16 + row) * NS + col]) +
+                       part[(2 * 16 + row) * NS + col]) +
+                      part[(3 * 16 + row) * NS + col];
+    if (mine)
+      mine[idx] = sum;
+    else if (row < M && n0 + col < N)
+      p.C[(int64_t)row * p.ldc + n0 + col] = sum;
+  }
+}
+
 // ---- launch shape.  Split kernel: 128-column strips x `splits` K ranges, aiming at one
-// workgroup per CU (256), at least 4 ring slots of K per split, and at most kWsTiles partial
-// tiles in the workspace.  A split count of 1 needs no workspace; it is used when the strips
-// alone fill the chip.  Otherwise the wave-split kernel (32-column strips) runs.
+// workgroup per CU (256), at least four 64-deep K steps per split, and at most kWsTiles
+// partial tiles in the workspace.  A split count of 1 needs no workspace; it is used when the
+// strips alone fill the chip.  Otherwise the wave-split kernel (32-column strips) runs.
 constexpr int kWsTiles = 512;  // 16 x 128 fp32 partial tiles (4 MiB of the stream workspace)
 static_assert((size_t)kWsTiles * 16 * 128 * 4 <= kStreamWorkspaceBytes, "partials must fit the workspace");
 
@@ -347,7 +503,7 @@ struct StreamShape {
 
 static StreamShape stream_shape(const GemmProblem& p) {
   const int strips = (p.N + 127) / 128;
-  const int nst_all = (p.K + kKS - 1) / kKS;
+  const int nst_all = (p.K + 63) / 64;  // 64-deep K steps
   int splits = (256 + strips - 1) / strips;
   splits = splits < 16 ? splits : 16;
   splits = splits < nst_all / 4 ? splits : nst_all / 4;
@@ -371,7 +527,7 @@ hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
   const StreamShape sh = stream_shape(p);
   float* ws = sh.splits > 1 ? stream_workspace(stream) : nullptr;
   if (sh.splits == 1 || ws) {
-    hipLaunchKernelGGL(gemm_stream_kernel, dim3(sh.strips * sh.splits), dim3(256), 0, stream, p, sh.strips,
+    hipLaunchKernelGGL(gemm_stream_wide_kernel, dim3(sh.strips * sh.splits), dim3(256), 0, stream, p, sh.strips,
                        sh.splits, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || sh.splits == 1) return e;
