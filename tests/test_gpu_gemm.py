@@ -328,6 +328,22 @@ def test_exact_tile_splits(mm, cuda, case):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
+# Grids of several rounds of workgroups, on every tile, with row/column edges and a K tail.
+LARGE_GRIDS = [((8192, 4096, 128), "256x256"), ((8190, 4104, 200), "256x256"), ((8192, 4096, 520), "256x128"),
+           ((4096, 8192, 64), "128x256"), ((4096, 4096, 192), "128x128"), ((4000, 4100, 136), "128x128")]
+
+
+@pytest.mark.parametrize("case", LARGE_GRIDS, ids=lambda c: "x".join(map(str, c[0])) + "-" + c[1])
+def test_exact_large_grids(mm, cuda, case):
+    """Multi-round tile grids on every tile: exact on integer inputs."""
+    (M, N, K), tile = case
+    A, B, truth = _exact_case(np.random.default_rng(M + N + 5 * K), M, N, K)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd, tile=tile)
+    C = Cd.cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
 def test_tile_split_deterministic_and_graph(mm, cuda, orc):
     """A split launch is bitwise reproducible, and a captured graph's replays match it."""
     A = to_dev(cuda, orc.uniform_f16((1024, 8192), 9, 0))
