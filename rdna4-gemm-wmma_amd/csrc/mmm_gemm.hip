@@ -320,15 +320,22 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     const uint32_t a_rstep = (uint32_t)(RPA * lda * 2), b_rstep = (uint32_t)(RPB * ldb * 2);
 
     // DMA of K tile t into ring slot `stage`: RA + RB buffer_load_dwordx4 ... lds per thread.
+    // Each range ends at the operand's last element (row M-1, column K-1 of A; row K-1,
+    // column N-1 of B), so nothing past the caller's data is ever fetched; rows past the end
+    // read as zero.  With N, K multiples of 8 no chunk straddles a range end.  K tiles are
+    // issued in order (t = 0, 1, ...), so bases and remaining byte counts advance by a
+    // constant per tile instead of being recomputed.
+    const char* a_ptr = (const char*)(p.A + (int64_t)m0 * lda + (int64_t)t_begin * T::BK);
+    const char* b_ptr = (const char*)(p.B + (int64_t)t_begin * T::BK * ldb + n0);
+    int64_t a_left = ((int64_t)(M - 1 - m0) * lda + K - (int64_t)t_begin * T::BK) * 2;
+    int64_t b_left = ((int64_t)(K - 1 - t_begin * T::BK) * ldb + N - n0) * 2;
+    const int64_t b_step = (int64_t)T::BK * ldb * 2;
     auto issue = [&](int t, int stage) {
       const int k0 = (t_begin + t) * T::BK;
-      // Each range ends at the operand's last element (row M-1, column K-1 of A; row K-1,
-      // column N-1 of B), so nothing past the caller's data is ever fetched; rows past the
-      // end read as zero.  With N, K multiples of 8 no chunk straddles a range end.
-      const i32x4 ra =
-          make_rsrc(p.A + (int64_t)m0 * lda + k0, clip_records(((int64_t)(M - 1 - m0) * lda + K - k0) * 2));
-      const i32x4 rb =
-          make_rsrc(p.B + (int64_t)k0 * ldb + n0, clip_records(((int64_t)(K - 1 - k0) * ldb + N - n0) * 2));
+      const i32x4 ra = make_rsrc(a_ptr, clip_records(a_left));
+      const i32x4 rb = make_rsrc(b_ptr, clip_records(b_left));
+      a_ptr += T::BK * 2, a_left -= T::BK * 2;
+      b_ptr += b_step, b_left -= b_step;
       const uint32_t a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
       const uint32_t b_dst = a_dst + T::A_BYTES;
       // K tail: a chunk at or past K gets kOobOffset added, which puts it beyond the
