@@ -38,23 +38,6 @@
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
 
-// Compile-time schedule options of the MFMA main loop (measured choices are the defaults).
-#ifndef MMM_PIPE_FRAGS
-#define MMM_PIPE_FRAGS 0  // 1: double-buffer fragments across the K steps of a stage
-#endif
-#ifndef MMM_SETPRIO
-#define MMM_SETPRIO 0  // 1: raise wave priority while issuing MFMAs
-#endif
-#ifndef MMM_XSTAGE
-#define MMM_XSTAGE 1  // 1: cross-stage pipeline (next tile's barrier and first reads under the last K-step)
-#endif
-#ifndef MMM_XFENCE
-#define MMM_XFENCE 0  // cross-stage loop: 1 keeps every earlier MFMA ahead of the tile barrier
-#endif
-#ifndef MMM_XSCHED
-#define MMM_XSCHED 1  // cross-stage loop: 0 compiler order, 1 next-step reads before MFMAs, 2 reads 1:1 among MFMAs
-#endif
-
 namespace mmm {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -205,13 +188,11 @@ __device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char L
 
 template <class T>
 __device__ __forceinline__ void mfma_frags(const Frags<T>& f, f32x16 (&acc)[T::FM][T::FN]) {
-  if (MMM_SETPRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int mb = 0; mb < T::FM; ++mb)
 #pragma unroll
     for (int nb = 0; nb < T::FN; ++nb)
       acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[nb], f.a[mb], acc[mb][nb], 0, 0, 0);
-  if (MMM_SETPRIO) __builtin_amdgcn_s_setprio(0);
 }
 
 template <class T, bool BKM, class Hook>
@@ -221,20 +202,6 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
   using Frags = mmm::Frags<T>;
   auto load = [&](int kk, Frags& f) { load_frags<T, BKM>(a_st, b_st, a_off, b_off, kk, f); };
   auto mfma = [&](const Frags& f) { mfma_frags<T>(f, acc); };
-#if MMM_PIPE_FRAGS
-  // Fragments double-buffered in registers: step kk+1's reads are issued before step kk's
-  // MFMAs (scheduling barriers keep that order), so LDS latency hides under MFMA work.
-  Frags f[2];
-  load(0, f[0]);
-  after_first_reads();
-#pragma unroll
-  for (int kk = 0; kk < T::KSTEPS; ++kk) {
-    if (kk + 1 < T::KSTEPS) load(kk + 1, f[(kk + 1) & 1]);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma(f[kk & 1]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#else
 #pragma unroll
   for (int kk = 0; kk < T::KSTEPS; ++kk) {
     Frags f;
@@ -242,7 +209,6 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
     if (kk == 0) after_first_reads();
     mfma(f);
   }
-#endif
 }
 
 struct NoHook {
@@ -392,7 +358,6 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         issue(t, stage);
     };
 
-#if MMM_XSTAGE
     // Ring of S slots, tile u in slot u % S.  Cross-stage pipeline: during the last K-step of
     // tile t, this wave waits for its own loads of tile t+1, then the barrier (a) publishes
     // tile t+1 -- every wave's loads of it have landed -- and (b) retires slot t % S: every
@@ -418,16 +383,9 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
         load_frags<T, false>(st, st + T::A_BYTES, a_off, b_off, kk + 1, f[(kk + 1) & 1]);
         mfma_frags<T>(f[kk & 1], acc);
-        if constexpr (MMM_XSCHED == 1) {
-          __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);  // the step's LDS reads
-          __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);      // then its MFMAs
-        } else if constexpr (MMM_XSCHED == 2) {
-#pragma unroll
-          for (int i = 0; i < T::FM * T::FN; ++i) {
-            if (i < T::FM + 2 * T::FN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          }
-        }
+        // keep the next step's LDS reads ahead of this step's MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);
       }
     };
     // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
@@ -436,7 +394,6 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       const int issued = t + S < KT ? t + S : KT;  // tiles 0 .. issued-1 are issued
       int ahead = issued - (t + 2);                // of those, after t+1 (may stay in flight)
       if (tail_regs && issued == KT && ahead > 0) --ahead;
-      if constexpr (MMM_XFENCE) __builtin_amdgcn_sched_barrier(0);
       wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(ahead);
       block_sync();
       const int nslot = cur + 1 == S ? 0 : cur + 1;
@@ -464,45 +421,6 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     }
     tile_body();
     mfma_frags<T>(f[1], acc);
-#else
-    // Ring of STAGES slots, P = STAGES-1 tiles in flight ahead of the one computed.  At the
-    // top of iteration t: wait until tile t has landed (this wave's loads complete in order,
-    // so at most (P-1) tiles' loads may stay outstanding), barrier (every wave's part of tile
-    // t is in LDS, and every wave has finished reading slot (t-1) % STAGES), then refill that
-    // slot with tile t+P while computing tile t.
-    constexpr int P = T::STAGES - 1;
-    constexpr int LPT = T::RA + T::RB;
-    for (int s = 0; s < P; ++s)
-      if (s < KT) issue_tile(s, s);
-    int cur = 0, nxt = P;  // ring slots of tile t and tile t+P
-    int t = 0;
-    // steady state: the tile refilled (t+P) is never the last one, so this loop holds only
-    // DMA issue, LDS reads and MFMAs
-    for (; t + P < KT - 1; ++t) {
-      wait_vmcnt<(P - 1) * LPT>();
-      block_sync();
-      const char LDS_AS* st = lds_base + cur * T::STAGE;
-      compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue(t + P, nxt); });
-      cur = cur + 1 == T::STAGES ? 0 : cur + 1;
-      nxt = nxt + 1 == T::STAGES ? 0 : nxt + 1;
-    }
-    if (t + P == KT - 1) {  // the iteration that refills the last tile (possibly gathered)
-      // A gathered last tile leaves no DMA outstanding, so the next wait must drain the ring.
-      wait_vmcnt<(P - 1) * LPT>();
-      block_sync();
-      const char LDS_AS* st = lds_base + cur * T::STAGE;
-      compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue_tile(t + P, nxt); });
-      cur = cur + 1 == T::STAGES ? 0 : cur + 1;
-      ++t;
-    }
-    for (; t < KT; ++t) {
-      wait_dma();
-      block_sync();
-      const char LDS_AS* st = lds_base + cur * T::STAGE;
-      compute_stage<T, false>(st, st + T::A_BYTES, a_off, b_off, acc, NoHook{});
-      cur = cur + 1 == T::STAGES ? 0 : cur + 1;
-    }
-#endif
   } else {
     static_assert(!GENERIC || T::STAGES == 2, "the register-staged path double-buffers");
     (void)t_begin;
