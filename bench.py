@@ -199,7 +199,21 @@ def cpu_baseline(W, budget_s: float = 12.0):
         "kind": "port",
         "sample": f"{rows}x{N}x{K} (rows 0..{rows - 1} of the {M}x{N}x{K} workload, same seeded inputs), "
                   f"best of {len(times)} passes in {sum(times):.1f} s after a {probe_rows}-row warm-up",
+        "cpu": _cpu_model(),
+        "host_cpus": os.cpu_count(),
     }
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baseline's record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness):
