@@ -38,6 +38,10 @@
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
 
+#ifndef MMM_XINTERLEAVE
+#define MMM_XINTERLEAVE 1  // interleave the steady-state refill loads with the last K-step's MFMAs
+#endif
+
 namespace mmm {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -296,22 +300,37 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     int64_t a_left = ((int64_t)(M - 1 - m0) * lda + K - (int64_t)t_begin * T::BK) * 2;
     int64_t b_left = ((int64_t)(K - 1 - t_begin * T::BK) * ldb + N - n0) * 2;
     const int64_t b_step = (int64_t)T::BK * ldb * 2;
-    auto issue = [&](int t, int stage) {
+    // A K tile's loads: descriptors and bases (prep; advances the running state), then the
+    // LPT loads, j = 0 .. RA-1 for A and RA .. LPT-1 for B (dma_one).
+    struct TileDma {
+      i32x4 ra, rb;
+      uint32_t a_dst, b_dst, a_base;
+    };
+    auto prep = [&](int t, int stage) {
       const int k0 = (t_begin + t) * T::BK;
-      const i32x4 ra = make_rsrc(a_ptr, clip_records(a_left));
-      const i32x4 rb = make_rsrc(b_ptr, clip_records(b_left));
+      TileDma d;
+      d.ra = make_rsrc(a_ptr, clip_records(a_left));
+      d.rb = make_rsrc(b_ptr, clip_records(b_left));
       a_ptr += T::BK * 2, a_left -= T::BK * 2;
       b_ptr += b_step, b_left -= b_step;
-      const uint32_t a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
-      const uint32_t b_dst = a_dst + T::A_BYTES;
+      d.a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
+      d.b_dst = d.a_dst + T::A_BYTES;
       // K tail: a chunk at or past K gets kOobOffset added, which puts it beyond the
       // descriptor's range so it reads as zero (no select: keeps the loads branch-free).
       const uint32_t a_dead = (uint32_t)(K - 1 - (k0 + a_kc)) >> 31;
-      const uint32_t a_base = a_goff + a_dead * kOobOffset;
+      d.a_base = a_goff + a_dead * kOobOffset;
+      return d;
+    };
+    auto dma_one = [&](const TileDma& d, int j) {
+      if (j < T::RA)
+        dma_b128(d.a_dst + j * T::NT * 16, d.ra, d.a_base + j * a_rstep);
+      else
+        dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, d.rb, b_goff + (j - T::RA) * b_rstep);
+    };
+    auto issue = [&](int t, int stage) {
+      const TileDma d = prep(t, stage);
 #pragma unroll
-      for (int r = 0; r < T::RA; ++r) dma_b128(a_dst + r * T::NT * 16, ra, a_base + r * a_rstep);
-#pragma unroll
-      for (int r = 0; r < T::RB; ++r) dma_b128(b_dst + r * T::NT * 16, rb, b_goff + r * b_rstep);
+      for (int j = 0; j < T::LPT; ++j) dma_one(d, j);
     };
 
     // The last K tile of an unaligned problem (K or N not a multiple of 8, or rows not
@@ -403,12 +422,35 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       mfma_frags<T>(f[1], acc);
       cur = nslot;
     };
+    // Steady state: the refill's loads are interleaved one to one with the last K-step's MFMAs
+    // (scheduling fences keep the order), so no burst of load issue leaves the matrix pipe idle.
+    auto tile_next_interleaved = [&](int t) {
+      wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(S - 2);  // steady state: S-2 tiles after t+1 in flight
+      block_sync();
+      const int nslot = cur + 1 == S ? 0 : cur + 1;
+      const char LDS_AS* ns = lds_base + nslot * T::STAGE;
+      load_frags<T, false>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
+      const TileDma d = prep(t + S, cur);
+#pragma unroll
+      for (int i = 0; i < T::FM * T::FN; ++i) {
+        const int mb = i / T::FN, nb = i % T::FN;
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[1].b[nb], f[1].a[mb], acc[mb][nb], 0, 0, 0);
+        if (i < T::LPT) dma_one(d, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int j = T::FM * T::FN; j < T::LPT; ++j) dma_one(d, j);
+      cur = nslot;
+    };
     // steady state refills by DMA only; the refill of the last tile (possibly gathered
     // through VGPRs) is peeled so the loop carries no gather registers
     int t = 0;
     for (; t + S < KT - 1; ++t) {
       tile_body();
-      tile_next(t, [&] { issue(t + S, cur); });
+      if constexpr (MMM_XINTERLEAVE)
+        tile_next_interleaved(t);
+      else
+        tile_next(t, [&] { issue(t + S, cur); });
     }
     if (t + S == KT - 1) {
       tile_body();
