@@ -984,7 +984,8 @@ int gemm_nn_splits(const GemmProblem& p, int tile_id) {
 
 hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream) {
   GemmProblem p = p0;
-  p.c_vec4 = ((uintptr_t)p.C % 16 == 0) && (p.ldc % 4 == 0);
+  // 16-byte stores of C need only 4-byte alignment on gfx950 (rows of an odd ldc included)
+  p.c_vec4 = (uintptr_t)p.C % 4 == 0;
   p.tail_regs = !tail_aligned(p);
   p.k_splits = 1;
   p.partials = nullptr;

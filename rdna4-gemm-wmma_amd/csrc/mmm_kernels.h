@@ -15,7 +15,7 @@ struct GemmProblem {
   float* C;
   int M, N, K;
   int64_t lda, ldb, ldc;
-  bool c_vec4;     // set by the launcher: C 16-byte aligned and ldc % 4 == 0
+  bool c_vec4;     // set by the launcher: C 4-byte aligned (16-byte stores of C rows allowed)
   bool tail_regs;  // set by the launcher: gather the last K tile through VGPRs
   int k_splits;    // tile kernel: K ranges computed by separate workgroups (<= 1: none)
   float* partials; // k_splits > 1: [tile][split][BM][BN] fp32 partial tiles

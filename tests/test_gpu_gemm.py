@@ -344,6 +344,22 @@ def test_exact_large_grids(mm, cuda, case):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
+@pytest.mark.parametrize("pad", [1, 2, 3])
+@pytest.mark.parametrize("case", [((1000, 1999, 777), None), ((4097, 1000, 520), "256x256"),
+                                  ((513, 700, 1032), "128x256"), ((700, 300, 4000), None)],
+                         ids=lambda c: "x".join(map(str, c[0])) + f"-{c[1]}")
+def test_exact_c_row_alignment(mm, cuda, case, pad):
+    """C rows only 4-byte aligned (ldc = N + pad): 16-byte stores of unaligned rows, on the
+    tile epilogue and the split reduction; nothing outside the [M][N] window is written."""
+    (M, N, K), tile = case
+    A, B, truth = _exact_case(np.random.default_rng(M + N + K + pad), M, N, K)
+    Cw = cuda.full((M, N + pad), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cw[:, :N], tile=tile)
+    C = Cw.cpu().numpy()
+    assert np.array_equal(C[:, :N], truth), f"{int((C[:, :N] != truth).sum())} mismatches"
+    assert np.isnan(C[:, N:]).all(), "wrote outside the [M][N] window"
+
+
 def test_tile_split_deterministic_and_graph(mm, cuda, orc):
     """A split launch is bitwise reproducible, and a captured graph's replays match it."""
     A = to_dev(cuda, orc.uniform_f16((1024, 8192), 9, 0))
