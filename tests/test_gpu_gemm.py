@@ -380,6 +380,41 @@ def test_tile_split_deterministic_and_graph(mm, cuda, orc):
         assert bool((d <= 1e-3 * S).all()), f"replay {i}"
 
 
+def test_concurrent_host_threads(mm, cuda):
+    """Four host threads, each with its own stream, issue split launches (tile K split and the
+    streaming split) at the same time: each stream gets its own workspace, results exact."""
+    import threading
+
+    rng = np.random.default_rng(12)
+    cases = [_exact_case(rng, *shp) for shp in [(16, 8192, 2048), (1024, 512, 4096), (8, 4096, 4096), (300, 264, 2048)]]
+    dev = [(to_dev(cuda, A), to_dev(cuda, B), truth) for A, B, truth in cases]
+    results, errors = {}, []
+
+    def worker(i):
+        try:
+            A, B, _ = dev[i]
+            s = cuda.cuda.Stream()
+            outs = []
+            with cuda.cuda.stream(s):
+                for _ in range(3):
+                    outs.append(mm.gemm(A, B))
+            s.synchronize()
+            results[i] = [o.cpu().numpy() for o in outs]
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    cuda.cuda.synchronize()
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(dev))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i, (_, _, truth) in enumerate(dev):
+        for o in results[i]:
+            assert np.array_equal(o, truth)
+
+
 def test_skinny_deterministic(mm, cuda, orc):
     A = to_dev(cuda, orc.uniform_f16((16, 8192), 4, 0))
     B = to_dev(cuda, orc.uniform_f16((8192, 8192), 4, 1))
