@@ -202,11 +202,11 @@ struct GemmPlan {
 static GemmPlan plan_gemm(const GemmProblem& p) {
   if (p.M == 0 || p.N == 0) return {MMM_KERNEL_NONE, -1, 0};
   if (p.K == 0) return {MMM_KERNEL_ZERO, -1, 0};
-  if (skinny_ok(p)) return {MMM_KERNEL_STREAM, -1, 0};  // M <= 16: HBM-bound streaming kernel
+  if (skinny_ok(p)) return {MMM_KERNEL_STREAM, -1, 0};  // M <= 64: HBM-bound streaming kernel
   // A few rows past a whole number of 256-row tiles (4097 = 16*256 + 1) would cost a full
   // extra round of tiles; those rows go to the streaming kernel instead when that saves a round.
   const int rem = p.M % 256;
-  if (p.M > 256 && rem > 0 && rem <= 16) {
+  if (p.M > 256 && rem > 0 && rem <= kStreamMaxRows) {
     const int Mm = p.M - rem;
     const int64_t tn = (p.N + 255) / 256;
     const int64_t rounds_full = ((int64_t)((p.M + 255) / 256) * tn + 255) / 256;

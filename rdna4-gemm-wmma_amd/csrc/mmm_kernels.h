@@ -43,7 +43,13 @@ int gemm_nn_splits(const GemmProblem& p, int tile_id);          // K splits the 
 constexpr size_t kStreamWorkspaceBytes = (size_t)32 << 20;
 float* stream_workspace(hipStream_t stream);
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
-bool skinny_ok(const GemmProblem& p);  // M <= 16 and aligned operands
+// Rows of C up to which the streaming kernels take a GEMM (the kernels handle up to 64).
+#ifndef MMM_STREAM_MAX_ROWS
+#define MMM_STREAM_MAX_ROWS 64
+#endif
+constexpr int kStreamMaxRows = MMM_STREAM_MAX_ROWS;
+static_assert(kStreamMaxRows >= 16 && kStreamMaxRows <= 64, "streaming kernels take 16 to 64 rows");
+bool skinny_ok(const GemmProblem& p);  // M <= kStreamMaxRows and operands within 32-bit offsets
 hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);
 int skinny_workgroups(const GemmProblem& p);
 int skinny_splits(const GemmProblem& p);  // K ranges reduced across workgroups (0: within one)

@@ -271,31 +271,24 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
   }
 }
 
-// C[16][strip * 128 + c] = sum over q = 0 .. splits-1 (in that order) of the strip's partials;
-// one thread per element of the 16 x 128 strip tiles.
+// C[row][strip * 128 + c] = sum over q = 0 .. splits-1 (in that order) of the strip's
+// partials; one thread per element of the ROWS x 128 strip tiles.
+template <int ROWS>
 __global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int strips, int splits,
                                                             const float* partials) {
+  constexpr int TILE = ROWS * 128;
   const int idx = blockIdx.x * 256 + threadIdx.x;
-  const int strip = idx >> 11, e = idx & 2047, row = e >> 7, col = strip * 128 + (e & 127);
+  const int strip = idx / TILE, e = idx % TILE, row = e >> 7, col = strip * 128 + (e & 127);
   if (strip >= strips) return;
-  const float* base = partials + (int64_t)strip * splits * 2048 + e;
+  const float* base = partials + (int64_t)strip * splits * TILE + e;
   float sum = base[0];
-  for (int q = 1; q < splits; ++q) sum += base[q * 2048];
+  for (int q = 1; q < splits; ++q) sum += base[q * TILE];
   if (row < p.M && col < p.N) p.C[(int64_t)row * p.ldc + col] = sum;
 }
 
-bool skinny_ok(const GemmProblem& p) {
-  const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
-  if (p.M > 16 || p.M < 1) return false;
-  if ((a & 1) || (b & 1)) return false;
-  if ((int64_t)16 * p.lda * 2 >= (int64_t)kOobOffset) return false;
-  // B offsets are taken from the strip base: the whole operand must fit a 32-bit offset
-  if (((int64_t)p.K * p.ldb + kNS) * 2 >= (int64_t)kOobOffset) return false;
-  return true;
-}
 
 // ------------------------------------------------------------------------------------
-// Split streaming kernel (M <= 16, enough K): one workgroup per 128-column strip and K range
+// Split streaming kernel (M <= 64, enough K): one workgroup per 128-column strip and K range
 // q of `splits`.  Each wave streams the whole strip -- 256 contiguous bytes of every B row --
 // over its own quarter of the workgroup's K range, through a private LDS ring (no barrier in
 // the loop); the four K partials are summed through LDS in wave order.  With splits == 1 the
@@ -303,30 +296,36 @@ bool skinny_ok(const GemmProblem& p) {
 // same stream, sums the splits of every strip in split order (fixed orders throughout:
 // deterministic; the kernel boundary orders the partial stores before their reads).  B slots
 // [KS][128] use the tile kernel's row swizzle (chunk c of row k at c ^ {0,6,10,12}[k & 3]) so
-// the transposing reads of four 256-byte rows hit distinct banks.
+// the transposing reads of four 256-byte rows hit distinct banks.  MR 16-row groups of A
+// (MR = 1, 2, 4 for up to 16, 32, 64 rows) share every B fragment: MR MFMAs per B read.
 // ------------------------------------------------------------------------------------
-#ifndef MMM_WIDE_KS
-#define MMM_WIDE_KS 64
-#endif
-#ifndef MMM_WIDE_SLOTS
-#define MMM_WIDE_SLOTS 2
-#endif
-namespace wide {
-constexpr int NS = 128, KS = MMM_WIDE_KS, SLOTS = MMM_WIDE_SLOTS;
-constexpr int ABYTES = 16 * KS * 2, BBYTES = KS * NS * 2, SLOT = ABYTES + BBYTES;
-constexpr int NA = ABYTES / 1024, NB = BBYTES / 1024, LOADS = NA + NB;
-constexpr int NT = NS / 16, CPR = NS / 8, RPI = 64 / CPR;  // 8 tiles, 16 chunks per row, 4 rows
-constexpr int CA = KS / 8, RPI_A = 64 / CA;
-static_assert(KS == 32 || KS == 64, "K rows per slot");
-static_assert(kWaves * SLOTS * SLOT <= 160 * 1024, "rings must fit the LDS");
-__device__ __forceinline__ int wswz_a(int row) { return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
-__device__ __forceinline__ int wswz_b(int k) { return (0xCA60 >> (4 * (k & 3))) & 15; }
-}  // namespace wide
+template <int MR>
+struct Wide {
+  static constexpr int NS = 128;
+  static constexpr int ROWS = 16 * MR;
+  static constexpr int KS = MR == 4 ? 32 : 64;     // K rows per slot
+  static constexpr int SLOTS = MR == 4 ? 3 : 2;    // ring slots per wave
+  static constexpr int ABYTES = ROWS * KS * 2, BBYTES = KS * NS * 2, SLOT = ABYTES + BBYTES;
+  static constexpr int NA = ABYTES / 1024, NB = BBYTES / 1024, LOADS = NA + NB;
+  static constexpr int NT = NS / 16, CPR = NS / 8, RPI = 64 / CPR;  // 8 tiles, 16 chunks per row, 4 rows
+  static constexpr int CA = KS / 8, RPI_A = 64 / CA;
+  static constexpr int RING_BYTES = kWaves * SLOTS * SLOT;
+  static constexpr int PART_BYTES = kWaves * ROWS * NS * 4;  // [wave][ROWS][128] fp32
+  static constexpr int LDS_BYTES = RING_BYTES > PART_BYTES ? RING_BYTES : PART_BYTES;
+  static_assert(KS == 32 || KS == 64, "K rows per slot");
+  static_assert(LDS_BYTES <= 160 * 1024, "rings and partials must fit the LDS");
+  __device__ static __forceinline__ int swz_a(int row) { return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
+  __device__ static __forceinline__ int swz_b(int k) { return (0xCA60 >> (4 * (k & 3))) & 15; }
+};
 
+template <int MR>
 __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p, int strips, int splits,
                                                                   float* partials) {
-  using namespace wide;
-  __shared__ __attribute__((aligned(1024))) char lds[kWaves * SLOTS * SLOT];
+  using W = Wide<MR>;
+  constexpr int NS = W::NS, ROWS = W::ROWS, KS = W::KS, SLOTS = W::SLOTS, ABYTES = W::ABYTES, SLOT = W::SLOT;
+  constexpr int NA = W::NA, NB = W::NB, LOADS = W::LOADS, NT = W::NT, CPR = W::CPR, RPI = W::RPI;
+  constexpr int CA = W::CA, RPI_A = W::RPI_A;
+  __shared__ __attribute__((aligned(1024))) char lds[W::LDS_BYTES];
   const int b = blockIdx.x;
   const int strip = b % strips, q = b / strips;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -343,20 +342,21 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
   char LDS_AS* ring = (char LDS_AS*)lds + w * SLOTS * SLOT;
   const uint32_t ring_addr = (uint32_t)(uintptr_t)ring;
 
-  // DMA map.  A [16][KS]: lane -> row lane/CA (+ RPI_A per instruction), slot chunk lane%CA
-  // holding logical chunk (lane%CA) ^ wswz_a(row).  B [KS][128]: lane -> row lane/CPR (+ RPI
-  // per instruction), slot chunk lane%CPR holding logical chunk (lane%CPR) ^ wswz_b(row).
+  // DMA map.  A [ROWS][KS]: lane -> row lane/CA (+ RPI_A per instruction), slot chunk lane%CA
+  // holding logical chunk (lane%CA) ^ swz_a(row).  B [KS][128]: lane -> row lane/CPR (+ RPI
+  // per instruction), slot chunk lane%CPR holding logical chunk (lane%CPR) ^ swz_b(row).
+  // Rows of A at or past M lie past the A descriptor's range (lda >= K) and read as zero.
   const int a_row = lane / CA;
   uint32_t a_goff[NA];
   int a_kc[NA];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
     const int row = a_row + i * RPI_A;
-    a_kc[i] = 8 * ((lane % CA) ^ wswz_a(row));
+    a_kc[i] = 8 * ((lane % CA) ^ W::swz_a(row));
     a_goff[i] = (uint32_t)((row * lda + a_kc[i]) * 2);
   }
   const int b_row = lane / CPR;
-  const int b_nc = 8 * ((lane % CPR) ^ wswz_b(b_row));  // swz_b depends on row % 4 = b_row (RPI = 4)
+  const int b_nc = 8 * ((lane % CPR) ^ W::swz_b(b_row));  // swz_b depends on row % 4 = b_row (RPI = 4)
   const uint32_t b_goff = (uint32_t)((b_row * ldb + b_nc) * 2);
   const uint32_t b_rstep = (uint32_t)(RPI * ldb * 2);
   const i32x4 rb_full = make_rsrc(p.B + n0, clip_records(((int64_t)(K - 1) * ldb + N - n0) * 2));
@@ -411,22 +411,26 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
       issue(s, slot);
   };
 
-  // fragments: A row fr, k 8*fg..; B column 16*j + fr, k rows 8*fg + (fr>>2) (+4)
+  // fragments: A row 16*g + fr, k 8*fg..; B column 16*j + fr, k rows 8*fg + (fr>>2) (+4)
   const int fr = lane & 15, fg = lane >> 4;
   constexpr int KQ = KS / 32;
   uint32_t a_off[KQ];
 #pragma unroll
-  for (int qq = 0; qq < KQ; ++qq) a_off[qq] = fr * (KS * 2) + (((4 * qq + fg) ^ wswz_a(fr)) * 16);
+  for (int qq = 0; qq < KQ; ++qq) a_off[qq] = fr * (KS * 2) + (((4 * qq + fg) ^ W::swz_a(fr)) * 16);
   const int bk_row = 8 * fg + (fr >> 2);
-  const int bsw = wswz_b(bk_row);  // same for the +4 row
-  f32x4 acc[NT];
+  const int bsw = W::swz_b(bk_row);  // same for the +4 row
+  f32x4 acc[MR][NT];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = f32x4{};
+  for (int g = 0; g < MR; ++g)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[g][j] = f32x4{};
   auto compute = [&](int slot) {
     const char LDS_AS* sl = ring + slot * SLOT;
 #pragma unroll
     for (int qq = 0; qq < KQ; ++qq) {
-      const half8 af = *(const half8 LDS_AS*)(sl + a_off[qq]);
+      half8 af[MR];
+#pragma unroll
+      for (int g = 0; g < MR; ++g) af[g] = *(const half8 LDS_AS*)(sl + g * 16 * KS * 2 + a_off[qq]);
       const char LDS_AS* brow = sl + ABYTES + (32 * qq + bk_row) * (NS * 2);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
@@ -436,7 +440,8 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
         fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)(bp + 4 * NS * 2));
         const half8 bf = __builtin_shufflevector(__builtin_bit_cast(half4, lo), __builtin_bit_cast(half4, hi), 0, 1,
                                                  2, 3, 4, 5, 6, 7);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < MR; ++g) acc[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[g], bf, acc[g][j], 0, 0, 0);
       }
     }
   };
@@ -470,19 +475,21 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
 
   // four K partials -> LDS, summed in wave order, to C (one split) or the workspace
   __syncthreads();
-  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][16][128]
+  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][ROWS][128]
 #pragma unroll
-  for (int j = 0; j < NT; ++j)
+  for (int g = 0; g < MR; ++g)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) part[(w * 16 + 4 * fg + v) * NS + 16 * j + fr] = acc[j][v];
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) part[(w * ROWS + 16 * g + 4 * fg + v) * NS + 16 * j + fr] = acc[g][j][v];
   __syncthreads();
-  float* mine = splits > 1 ? partials + (int64_t)(strip * splits + q) * (16 * NS) : nullptr;
+  float* mine = splits > 1 ? partials + (int64_t)(strip * splits + q) * (ROWS * NS) : nullptr;
 #pragma unroll
-  for (int e = 0; e < 16 * NS / 256; ++e) {
+  for (int e = 0; e < ROWS * NS / 256; ++e) {
     const int idx = tid + 256 * e, row = idx / NS, col = idx % NS;
-    const float sum = ((part[(0 * 16 + row) * NS + col] + part[(1 * 16 + row) * NS + col]) +
-                       part[(2 * 16 + row) * NS + col]) +
-                      part[(3 * 16 + row) * NS + col];
+    const float sum = ((part[(0 * ROWS + row) * NS + col] + part[(1 * ROWS + row) * NS + col]) +
+                       part[(2 * ROWS + row) * NS + col]) +
+                      part[(3 * ROWS + row) * NS + col];
     if (mine)
       mine[idx] = sum;
     else if (row < M && n0 + col < N)
@@ -490,27 +497,35 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
   }
 }
 
-// ---- launch shape.  Split kernel: 128-column strips x `splits` K ranges, aiming at one
-// workgroup per CU (256), at least four 64-deep K steps per split, and at most kWsTiles
-// partial tiles in the workspace.  A split count of 1 needs no workspace; it is used when the
-// strips alone fill the chip.  Otherwise the wave-split kernel (32-column strips) runs.
-constexpr int kWsTiles = 512;  // 16 x 128 fp32 partial tiles (4 MiB of the stream workspace)
-static_assert((size_t)kWsTiles * 16 * 128 * 4 <= kStreamWorkspaceBytes, "partials must fit the workspace");
+// ---- launch shape.  Split kernel: 128-column strips x `splits` K ranges.  Every variant
+// holds one workgroup per CU (LDS), so the grid is kept to one round of 256 workgroups:
+// splits = the most that fit (at most 16, at least four 64-deep K steps each).  A second,
+// partly filled round costs more than the extra parallelism gains (measured: 112 strips run
+// 1.2-1.4x faster at 2 splits than at 3).  A split count of 1 needs no workspace.  For
+// M <= 16 with one split and fewer than 128 strips the wave-split kernel (32-column strips,
+// four times the workgroups) runs instead; for 16 < M <= 64 the split kernel runs with one
+// split when no workspace is to be had.
+constexpr int kWsTiles = 512;  // partial tiles of up to 64 x 128 fp32 (16 MiB of the stream workspace)
+static_assert((size_t)kWsTiles * 64 * 128 * 4 <= kStreamWorkspaceBytes, "partials must fit the workspace");
 
 struct StreamShape {
+  int mr;              // 16-row groups of the split kernel (1, 2, 4)
   int strips, splits;  // split kernel: grid strips * splits; splits == 0: wave-split kernel
 };
 
+static int stream_mr(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
+
 static StreamShape stream_shape(const GemmProblem& p) {
+  const int mr = stream_mr(p.M);
   const int strips = (p.N + 127) / 128;
   const int nst_all = (p.K + 63) / 64;  // 64-deep K steps
-  int splits = (256 + strips - 1) / strips;
+  int splits = 256 / strips;
   splits = splits < 16 ? splits : 16;
   splits = splits < nst_all / 4 ? splits : nst_all / 4;
   if (splits > kWsTiles / strips) splits = kWsTiles / strips;
   if (splits < 1) splits = 1;
-  if (splits == 1 && strips < 256) return {strips, 0};
-  return {strips, splits};
+  if (splits == 1 && strips < 128 && mr == 1) return {mr, strips, 0};
+  return {mr, strips, splits};
 }
 
 int skinny_splits(const GemmProblem& p) { return stream_shape(p).splits; }
@@ -520,22 +535,46 @@ int skinny_workgroups(const GemmProblem& p) {
   return sh.splits ? sh.strips * sh.splits : (p.N + kNS - 1) / kNS;
 }
 
+bool skinny_ok(const GemmProblem& p) {
+  const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
+  if (p.M > kStreamMaxRows || p.M < 1) return false;
+  if ((a & 1) || (b & 1)) return false;
+  if ((int64_t)16 * stream_mr(p.M) * p.lda * 2 >= (int64_t)kOobOffset) return false;
+  // B offsets are taken from the strip base: the whole operand must fit a 32-bit offset
+  if (((int64_t)p.K * p.ldb + 128) * 2 >= (int64_t)kOobOffset) return false;
+  return true;
+}
+
+template <int MR>
+static hipError_t launch_wide(const GemmProblem& p, int strips, int splits, float* ws, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm_stream_wide_kernel<MR>, dim3(strips * splits), dim3(256), 0, stream, p, strips, splits, ws);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  constexpr int ROWS = 16 * MR;
+  hipLaunchKernelGGL(reduce_splits_kernel<ROWS>, dim3(strips * (ROWS * 128 / 256)), dim3(256), 0, stream, p, strips,
+                     splits, (const float*)ws);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
   GemmProblem p = p0;
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   p.tail_regs = (a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8;
-  const StreamShape sh = stream_shape(p);
+  StreamShape sh = stream_shape(p);
   float* ws = sh.splits > 1 ? stream_workspace(stream) : nullptr;
+  if (sh.splits > 1 && !ws && sh.mr > 1) sh.splits = 1;  // no workspace: one split
   if (sh.splits == 1 || ws) {
-    hipLaunchKernelGGL(gemm_stream_wide_kernel, dim3(sh.strips * sh.splits), dim3(256), 0, stream, p, sh.strips,
-                       sh.splits, ws);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || sh.splits == 1) return e;
-    hipLaunchKernelGGL(reduce_splits_kernel, dim3(sh.strips * 8), dim3(256), 0, stream, p, sh.strips, sh.splits,
-                       (const float*)ws);
-    return hipGetLastError();
+    switch (sh.mr) {
+      case 1:
+        return launch_wide<1>(p, sh.strips, sh.splits, ws, stream);
+      case 2:
+        return launch_wide<2>(p, sh.strips, sh.splits, ws, stream);
+      default:
+        return launch_wide<4>(p, sh.strips, sh.splits, ws, stream);
+    }
   }
-  // wave-split kernel: no workspace (also the path under stream capture before a workspace exists)
+  // wave-split kernel (M <= 16): no workspace (also the path under stream capture before a
+  // workspace exists)
   const int strips = (p.N + kNS - 1) / kNS;
   hipLaunchKernelGGL(gemm_skinny_kernel, dim3(strips), dim3(256), 0, stream, p, strips);
   return hipGetLastError();

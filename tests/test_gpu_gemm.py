@@ -192,7 +192,7 @@ def test_exact_unaligned_rows(mm, cuda, shape):
 @pytest.mark.parametrize("shape", [(16, 8192, 8192), (5, 1000, 2000), (16, 96, 72), (1, 64, 8), (11, 520, 4104)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_exact_skinny(mm, cuda, shape):
-    """M <= 16 runs on the streaming kernel (K split over four waves, fixed-order reduction)."""
+    """M <= 16 runs on the 16-row streaming kernel (fixed-order reductions)."""
     M, N, K = shape
     rng = np.random.default_rng(M * 13 + N + K)
     A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
@@ -219,11 +219,14 @@ def test_exact_skinny_unaligned(mm, cuda, shape):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
-@pytest.mark.parametrize("shape", [(16 * 256 + 1, 1024, 520), (8 * 256 + 16, 4096, 264), (2 * 256 + 7, 300, 1001)],
+@pytest.mark.parametrize("shape", [(16 * 256 + 1, 4096, 264), (16 * 256 + 40, 4096, 264), (16 * 256 + 64, 4096, 1000),
+                                   (16 * 256 + 17, 4095, 523)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_exact_row_remainder_split(mm, cuda, shape):
-    """M = 256*k + r (r <= 16): the r rows run on the streaming kernel, the rest on the tile kernel."""
+    """M = 256*k + r (r <= 64): the r rows run on the streaming kernel, the rest on the tile kernel."""
     M, N, K = shape
+    plan = mm.gemm_plan(M, N, K)
+    assert plan["kernel"] == "tile+stream" and plan["stream_rows"] == M % 256
     rng = np.random.default_rng(M + N + K)
     A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
     B = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
@@ -253,6 +256,26 @@ def test_exact_stream_splits(mm, cuda, case):
     (M, N, K), splits = case
     assert mm.gemm_plan(M, N, K)["stream_splits"] == splits
     A, B, truth = _exact_case(np.random.default_rng(M * 7 + N + K), M, N, K)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)
+    C = Cd.cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
+# 17 <= M <= 64: 32- and 64-row variants of the split streaming kernel -> K splits
+STREAM_ROWS = [((17, 8192, 8192), 4), ((24, 14336, 4096), 2), ((32, 4095, 4111), 8), ((33, 1000, 3000), 11),
+               ((48, 130, 9000), 16), ((64, 8192, 1024), 4), ((63, 28672, 512), 1), ((40, 128, 64), 1),
+               ((64, 264, 200), 1), ((57, 777, 1031), 4)]
+
+
+@pytest.mark.parametrize("case", STREAM_ROWS, ids=lambda c: "x".join(map(str, c[0])) + f"-s{c[1]}")
+def test_exact_stream_rows(mm, cuda, case):
+    """Up to 64 rows on the streaming kernel (two or four 16-row groups sharing every B
+    fragment), split and unsplit, aligned and gathered tails: exact against int64."""
+    (M, N, K), splits = case
+    plan = mm.gemm_plan(M, N, K)
+    assert plan["kernel"] == "stream" and plan["stream_splits"] == splits
+    A, B, truth = _exact_case(np.random.default_rng(M * 5 + N + 3 * K), M, N, K)
     Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
     mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)
     C = Cd.cpu().numpy()
@@ -291,13 +314,15 @@ def test_stream_split_concurrent_streams(mm, cuda):
         assert np.array_equal(C2.cpu().numpy(), t2)
 
 
-def test_stream_graph_capture(mm, cuda):
+@pytest.mark.parametrize("rows", [16, 40])
+def test_stream_graph_capture(mm, cuda, rows):
     """Captured into a HIP graph (no allocation during capture: a stream without a workspace
-    takes the in-workgroup kernel); every replay, with eager work in between, matches eager."""
+    takes the in-workgroup kernel for 16 rows, one K range per workgroup for 40); every
+    replay, with eager work in between, matches eager."""
     rng = np.random.default_rng(8)
-    A, B, truth = _exact_case(rng, 16, 8192, 2048)
+    A, B, truth = _exact_case(rng, rows, 8192, 2048)
     A, B = to_dev(cuda, A), to_dev(cuda, B)
-    C = cuda.full((16, 8192), float("nan"), dtype=cuda.float32, device="cuda")
+    C = cuda.full((rows, 8192), float("nan"), dtype=cuda.float32, device="cuda")
     g = cuda.cuda.CUDAGraph()
     with cuda.cuda.graph(g):
         mm.gemm(A, B, C)
@@ -310,7 +335,7 @@ def test_stream_graph_capture(mm, cuda):
 
 
 # (M, N, K, tile or None) -> K splits of the tile kernel
-TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((64, 4096, 4096, None), 8), ((300, 264, 2048, None), 4),
+TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((65, 4096, 4096, None), 8), ((300, 264, 2048, None), 4),
                ((100, 200, 1001, None), 2), ((256, 512, 4096, "256x256"), 8), ((256, 512, 2048, "256x128"), 4),
                ((200, 300, 3000, "128x256"), 5), ((2000, 2000, 512, None), 1)]
 

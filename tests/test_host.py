@@ -191,13 +191,21 @@ def test_gemm_plan(mm):
     # too little K to split: 32-column strips, K split among each workgroup's waves
     p = mm.gemm_plan(16, 8192, 128)
     assert p["stream_splits"] == 0 and p["stream_workgroups"] == 8192 // 32
+    # the split grid stays within one round of 256 workgroups: 112 strips x 2, not x 3
+    p = mm.gemm_plan(64, 14336, 4096)
+    assert p["kernel"] == "stream" and p["stream_splits"] == 2 and p["stream_workgroups"] == 224
+    p = mm.gemm_plan(32, 28672, 8192)  # 224 strips fill the chip unsplit
+    assert p["stream_splits"] == 1 and p["stream_workgroups"] == 224
+    assert mm.gemm_plan(65, 8192, 8192)["kernel"] == "tile"
+    p = mm.gemm_plan(16 * 256 + 40, 4096, 264)  # 40 rows past 16 tile rows stream
+    assert p["kernel"] == "tile+stream" and p["tile_rows"] == 4096 and p["stream_rows"] == 40
     assert mm.gemm_plan(5, 5, 0)["kernel"] == "zero"
     assert mm.gemm_plan(0, 5, 5)["kernel"] == "none"
     # odd addresses cannot use the direct-to-LDS loads or the streaming kernel
     p = mm.gemm_plan(300, 264, 200, A=3)
     assert p["kernel"] == "tile" and p["direct_to_lds"] == 0
     assert mm.gemm_plan(8, 64, 64, A=3)["kernel"] == "tile"
-    for shape in [(256, 256, 256), (1000, 3000, 70), (8192, 2048, 2048), (17, 4096, 4096), (6000, 200, 50)]:
+    for shape in [(256, 256, 256), (1000, 3000, 70), (8192, 2048, 2048), (65, 4096, 4096), (6000, 200, 50)]:
         p = mm.gemm_plan(*shape)
         assert (p["wave_m"], p["wave_n"], p["waves_i"], p["waves_j"]) in mm.TILES.values()
         assert p["block_m"] == p["waves_i"] * p["wave_m"] * 32 and p["block_n"] == p["waves_j"] * p["wave_n"] * 32
