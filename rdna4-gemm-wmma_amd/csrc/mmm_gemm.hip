@@ -34,6 +34,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "mmm.h"
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
@@ -59,14 +61,18 @@ constexpr int kRsrcWord3 = 0x00020000;
 constexpr uint32_t kOobOffset = 0x7ffffff0u;
 
 // Block tile BM x BN, K step BK (32 or 64), WGM x WGN waves, STAGES-deep LDS ring, OCC
-// workgroups per CU targeted by the launch bounds (OCC > 1 caps registers accordingly).
-template <int BM_, int BN_, int WGM_, int WGN_, int BK_, int STAGES_, int OCC_ = 1>
+// workgroups per CU targeted by the launch bounds (OCC > 1 caps registers accordingly), MFMA
+// shape MF: 32 = v_mfma_f32_32x32x16_f16, 16 = v_mfma_f32_16x16x32_f16 (same MACs per LDS byte;
+// a quarter of the accumulator bytes per instruction for half the MACs).
+template <int BM_, int BN_, int WGM_, int WGN_, int BK_, int STAGES_, int OCC_ = 1, int MF_ = 32>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_, STAGES = STAGES_, OCC = OCC_;
+  static constexpr int MF = MF_;
   static constexpr int NT = 64 * WGM * WGN;
   static constexpr int TM = BM / WGM, TN = BN / WGN;
-  static constexpr int FM = TM / 32, FN = TN / 32;
-  static constexpr int KSTEPS = BK / 16;  // MFMA K-steps per stage
+  static constexpr int FM = TM / MF, FN = TN / MF;
+  static constexpr int KK = MF == 32 ? 16 : 32;  // K per MFMA
+  static constexpr int KSTEPS = BK / KK;         // MFMA K-steps per stage
   static constexpr int CA = BK / 8;       // 16-byte chunks per A row
   static constexpr int CB = BN / 8;       // 16-byte chunks per B row
   static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
@@ -74,25 +80,45 @@ struct Tile {
   static constexpr int RA = BM * CA / NT;  // A chunks per thread per stage
   static constexpr int RB = BK * CB / NT;  // B chunks per thread per stage
   static constexpr int LPT = RA + RB;      // direct-to-LDS loads per thread per stage
-  // A-row swizzle (chunk c of row m stored at c ^ swz_a(m)).  Rows of 128 B (BK = 64):
-  // 8 consecutive rows take 8 distinct chunk slots and 16 consecutive rows 16 distinct
-  // 16-byte bank groups of the 256-byte bank window.  Rows of 64 B (BK = 32): four rows share
-  // a 256-byte window, so the swizzle uses row bits 1..3.  Both are conflict-free for
-  // ds_read_b128 whether the LDS serves 8 or 16 lanes per cycle.
+  // A-row swizzle (chunk c of row m stored at c ^ swz_a(m)).  32x32 fragments, rows of 128 B
+  // (BK = 64): 8 consecutive rows take 8 distinct chunk slots and 16 consecutive rows 16
+  // distinct 16-byte bank groups of the 256-byte bank window.  Rows of 64 B (BK = 32): four
+  // rows share a 256-byte window, so the swizzle uses row bits 1..3.  Both are conflict-free
+  // for the 32x32 fragment reads (measured).
+  // 16x16 fragments (BK = 64): each ds_read_b128 reads 16 consecutive rows at four logical
+  // chunks; row bits 1..3 as the chunk swizzle make it conflict-free (measured with
+  // SQ_LDS_BANK_CONFLICT on MI355X: the 32x32 swizzle costs this pattern a 2-way conflict).
   static __device__ __forceinline__ int swz_a(int m) {
-    if constexpr (BK == 64) return (m & 7) ^ ((m >> 3) & 3);
+    if constexpr (MF == 16) return (m >> 1) & 7;
+    else if constexpr (BK == 64) return (m & 7) ^ ((m >> 3) & 3);
     else return ((m >> 1) & 3) ^ ((m >> 3) & 1);
   }
-  static constexpr int SWZ_A_ROWS = BK == 64 ? 32 : 16;  // swz_a depends on m % SWZ_A_ROWS
+  static constexpr int SWZ_A_ROWS = MF == 16 ? 16 : BK == 64 ? 32 : 16;  // swz_a depends on m % SWZ_A_ROWS
+  // A fragment offsets per K-step: 16-row fragments alternate between two swizzle phases when
+  // the swizzle spans 32 rows; fragment mb sits (mb / APAR) * AROWS rows past phase mb % APAR.
+  static constexpr int APAR = (MF == 16 && SWZ_A_ROWS == 32) ? 2 : 1;
+  static constexpr int AROWS = APAR * MF;
+  // B-row swizzle (chunk c of row k stored at c ^ swz_bk(k)).  32x32 fragments: {0, 6, 10, 12}
+  // by k % 4 (the 4 rows x 4 chunks that 32 lanes of one ds_read_b64_tr_b16 touch land in 16
+  // distinct bank groups).  16x16 fragments: those 32 lanes read rows k .. k+3 and k+8 .. k+11
+  // (2 chunks each), so rows with bit 3 set also flip chunk bit 1 ({2, 4, 8, 14}).
+  static __device__ __forceinline__ int swz_bk(int k) {
+    const int s = (0xCA60 >> (4 * (k & 3))) & 15;
+    if constexpr (MF == 16) return s ^ (((k >> 3) & 1) << 1);
+    else return s;
+  }
+  static constexpr int SWZ_B_ROWS = MF == 16 ? 16 : 4;  // swz_bk depends on k % SWZ_B_ROWS
+  static_assert(MF == 32 || (MF == 16 && BK == 64), "MFMA shape (16x16 fragments with 64-deep stages)");
   static_assert(BK == 32 || BK == 64, "K step must be 32 or 64");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32x32");
-  static_assert(FN <= 4, "at most 4 B fragments per wave");
+  static_assert(FN <= 4 && KSTEPS * APAR <= 4, "at most 4 B fragments and 4 A offsets per wave");
   static_assert(CB >= 16, "B swizzle needs rows of at least 16 chunks (BN >= 128)");
   static_assert((BM * CA) % NT == 0 && (BK * CB) % NT == 0, "chunks must divide evenly over threads");
   static_assert(STAGES >= 2 && OCC * STAGES * STAGE <= 160 * 1024, "LDS rings must fit the 160 KB LDS");
 };
 
-// B-row swizzle (chunk c of row k stored at c ^ swz_b(k)), {0, 6, 10, 12} by k % 4.
+// B-row swizzle of the 32x32 layouts (chunk c of row k stored at c ^ swz_b(k)), {0, 6, 10, 12}
+// by k % 4.
 __device__ __forceinline__ int swz_b(int k) { return (0xCA60 >> (4 * (k & 3))) & 15; }
 
 __device__ __forceinline__ half8 lds_read_a(const char LDS_AS* p) { return *(const half8 LDS_AS*)p; }
@@ -174,35 +200,51 @@ struct Frags {
   half8 a[T::FM], b[T::FN];
 };
 
+// Accumulator of one MF x MF output block (C^T: lane l owns row m = l % MF).
+template <class T>
+using AccT = typename std::conditional<T::MF == 32, f32x16, f32x4>::type;
+
 // Fragment reads of K-step kk from an LDS stage (layouts as for compute_stage below).
+// a_off[kk * APAR + phase]: A fragment offsets; b_off[nb] (N-contiguous B) or b_off[kk]
+// (K-major B, 32x32 only).
 template <class T, bool BKM>
-__device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char LDS_AS* b_st,
-                                           const uint32_t (&a_off)[T::KSTEPS], const uint32_t (&b_off)[4], int kk,
-                                           Frags<T>& f) {
+__device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char LDS_AS* b_st, const uint32_t (&a_off)[4],
+                                           const uint32_t (&b_off)[4], int kk, Frags<T>& f) {
+  static_assert(!BKM || T::MF == 32, "K-major B stages use 32x32 fragments");
 #pragma unroll
-  for (int mb = 0; mb < T::FM; ++mb) f.a[mb] = lds_read_a(a_st + a_off[kk] + mb * 32 * T::BK * 2);
+  for (int mb = 0; mb < T::FM; ++mb)
+    f.a[mb] = lds_read_a(a_st + a_off[kk * T::APAR + mb % T::APAR] + (mb / T::APAR) * T::AROWS * T::BK * 2);
 #pragma unroll
   for (int nb = 0; nb < T::FN; ++nb) {
     if constexpr (BKM)
       f.b[nb] = lds_read_a(b_st + b_off[kk] + nb * 32 * T::BK * 2);
     else
-      f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * 16) * T::BN * 2, b_st + b_off[nb] + (kk * 16 + 4) * T::BN * 2);
+      f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * T::KK) * T::BN * 2,
+                              b_st + b_off[nb] + (kk * T::KK + 4) * T::BN * 2);
   }
 }
 
+// One MFMA of the tile's shape, operands swapped (B fragment as src A): acc holds C^T.
 template <class T>
-__device__ __forceinline__ void mfma_frags(const Frags<T>& f, f32x16 (&acc)[T::FM][T::FN]) {
+__device__ __forceinline__ void mfma_one(const half8& b, const half8& a, AccT<T>& acc) {
+  if constexpr (T::MF == 32)
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, acc, 0, 0, 0);
+  else
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, a, acc, 0, 0, 0);
+}
+
+template <class T>
+__device__ __forceinline__ void mfma_frags(const Frags<T>& f, AccT<T> (&acc)[T::FM][T::FN]) {
 #pragma unroll
   for (int mb = 0; mb < T::FM; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < T::FN; ++nb)
-      acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[nb], f.a[mb], acc[mb][nb], 0, 0, 0);
+    for (int nb = 0; nb < T::FN; ++nb) mfma_one<T>(f.b[nb], f.a[mb], acc[mb][nb]);
 }
 
 template <class T, bool BKM, class Hook>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const char LDS_AS* b_st,
-                                              const uint32_t (&a_off)[T::KSTEPS], const uint32_t (&b_off)[4],
-                                              f32x16 (&acc)[T::FM][T::FN], Hook&& after_first_reads) {
+                                              const uint32_t (&a_off)[4], const uint32_t (&b_off)[4],
+                                              AccT<T> (&acc)[T::FM][T::FN], Hook&& after_first_reads) {
   using Frags = mmm::Frags<T>;
   auto load = [&](int kk, Frags& f) { load_frags<T, BKM>(a_st, b_st, a_off, b_off, kk, f); };
   auto mfma = [&](const Frags& f) { mfma_frags<T>(f, acc); };
@@ -249,34 +291,42 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   // and RPB = NT/CB rows of B, so slot rows are row0 + r*RP; RPA is a multiple of the rows
   // the A swizzle depends on and RPB of 4, so the logical chunk is the same every round.
   constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
-  static_assert(RPA % T::SWZ_A_ROWS == 0 && RPB % 4 == 0, "round strides must preserve the swizzle");
+  static_assert(RPA % T::SWZ_A_ROWS == 0 && RPB % T::SWZ_B_ROWS == 0, "round strides must preserve the swizzle");
   const int a_row0 = w * (64 / T::CA) + lane / T::CA;
   const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
   const int b_row0 = w * (64 / T::CB) + lane / T::CB;
-  const int b_nc = 8 * ((lane % T::CB) ^ swz_b(b_row0));
+  const int b_nc = 8 * ((lane % T::CB) ^ T::swz_bk(b_row0));
 
-  // ---- fragment read offsets (bytes within a stage)
-  uint32_t a_off[T::KSTEPS];
-  {
-    const int m = wm * T::TM + (lane & 31);
+  // ---- fragment read offsets (bytes within a stage).  MF = 32: lane l reads row l % 32 of
+  // A, k chunk l / 32 of each 16-deep step; B rows 8*(l/32) + (l/4)%4 (+4), columns
+  // 16*((l/16)%2) + 4*(l%4) of each 32-column fragment.  MF = 16: row l % 16 of A, k chunk
+  // l / 16 of each 32-deep step; B rows 8*(l/16) + (l/4)%4 (+4), columns 4*(l%4) of each
+  // 16-column fragment.
+  uint32_t a_off[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int kk = 0; kk < T::KSTEPS; ++kk) a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(m)) * 16;
-  }
+  for (int kk = 0; kk < T::KSTEPS; ++kk)
+#pragma unroll
+    for (int ph = 0; ph < T::APAR; ++ph) {
+      const int m = wm * T::TM + ph * T::MF + (lane % T::MF);
+      const int chunk = (T::KK / 8) * kk + lane / T::MF;
+      a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
+    }
   uint32_t b_off[4] = {0, 0, 0, 0};
   {
-    const int k = 8 * (lane >> 5) + ((lane >> 2) & 3);
+    const int k = 8 * (lane / T::MF) + ((lane >> 2) & 3);
 #pragma unroll
     for (int nb = 0; nb < T::FN; ++nb) {
-      const int n = wn * T::TN + 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-      b_off[nb] = k * T::BN * 2 + (((n >> 3) ^ swz_b(k)) * 16) + (n & 7) * 2;
+      const int n = T::MF == 32 ? wn * T::TN + 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)
+                                : wn * T::TN + 16 * nb + 4 * (lane & 3);
+      b_off[nb] = k * T::BN * 2 + (((n >> 3) ^ T::swz_bk(k)) * 16) + (n & 7) * 2;
     }
   }
 
-  f32x16 acc[T::FM][T::FN];
+  AccT<T> acc[T::FM][T::FN];
 #pragma unroll
   for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < T::FN; ++j) acc[i][j] = AccT<T>{};
 
   const int KT_all = (K + T::BK - 1) / T::BK;
   const int t_begin = __builtin_amdgcn_readfirstlane((q * KT_all) / nsplit);
@@ -434,7 +484,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
 #pragma unroll
       for (int i = 0; i < T::FM * T::FN; ++i) {
         const int mb = i / T::FN, nb = i % T::FN;
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[1].b[nb], f[1].a[mb], acc[mb][nb], 0, 0, 0);
+        mfma_one<T>(f[1].b[nb], f[1].a[mb], acc[mb][nb]);
         if (i < T::LPT) dma_one(d, i);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -523,18 +573,24 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     }
   }
 
-  // ---- epilogue: lane owns row m, columns n..n+3 for each (mb, nb, q).
+  // ---- epilogue: lane owns row m, columns n..n+3 for each (mb, nb, q).  MF = 32: m = l % 32,
+  // n = 32*nb + 8*q + 4*(l/32) (q = 0..3); MF = 16: m = l % 16, n = 16*nb + 4*(l/16) (q = 0).
+  constexpr int NQ = T::MF == 32 ? 4 : 1;  // float4 groups per accumulator
+  static_assert(NQ * 4 == sizeof(AccT<T>) / 4, "accumulator groups");
+  auto col_of = [&](int nb, int qq) {
+    return T::MF == 32 ? 32 * nb + 8 * qq + 4 * (lane >> 5) : 16 * nb + 4 * (lane >> 4);
+  };
   if (nsplit > 1) {  // K split: the whole tile (rows/columns past M/N included) to the partials
     float* part = p.partials + ((int64_t)(tm * tiles_n + tn) * nsplit + q) * (T::BM * T::BN);
 #pragma unroll
     for (int mb = 0; mb < T::FM; ++mb) {
-      float* prow = part + (wm * T::TM + 32 * mb + (lane & 31)) * T::BN + wn * T::TN + 4 * (lane >> 5);
+      float* prow = part + (wm * T::TM + T::MF * mb + (lane % T::MF)) * T::BN + wn * T::TN;
 #pragma unroll
       for (int nb = 0; nb < T::FN; ++nb)
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq)
-          *(f32x4*)(prow + 32 * nb + 8 * qq) = f32x4{acc[mb][nb][4 * qq + 0], acc[mb][nb][4 * qq + 1],
-                                                      acc[mb][nb][4 * qq + 2], acc[mb][nb][4 * qq + 3]};
+        for (int qq = 0; qq < NQ; ++qq)
+          *(f32x4*)(prow + col_of(nb, qq)) = f32x4{acc[mb][nb][4 * qq + 0], acc[mb][nb][4 * qq + 1],
+                                                   acc[mb][nb][4 * qq + 2], acc[mb][nb][4 * qq + 3]};
     }
     return;
   }
@@ -543,14 +599,14 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   const bool vec_ok = p.c_vec4;
 #pragma unroll
   for (int mb = 0; mb < T::FM; ++mb) {
-    const int m = m0 + wm * T::TM + 32 * mb + (lane & 31);
+    const int m = m0 + wm * T::TM + T::MF * mb + (lane % T::MF);
     if (m >= M) continue;
     float* crow = C + (int64_t)m * ldc;
 #pragma unroll
     for (int nb = 0; nb < T::FN; ++nb) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * T::TN + 32 * nb + 8 * q + 4 * (lane >> 5);
+      for (int q = 0; q < NQ; ++q) {
+        const int n = n0 + wn * T::TN + col_of(nb, q);
         f32x4 v = {acc[mb][nb][4 * q + 0], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2], acc[mb][nb][4 * q + 3]};
         if (vec_ok && n + 3 < N) {
           *(f32x4*)(crow + n) = v;
@@ -580,6 +636,7 @@ __device__ __forceinline__ int64_t fold_off(int i, int lo, int64_t s_hi, int64_t
 
 template <class T, bool BKM>
 __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int tiles_m, int tiles_n) {
+  static_assert(T::MF == 32, "the folded kernels use 32x32 fragments");
   __shared__ __attribute__((aligned(1024))) char lds[2 * T::STAGE];
   static_assert(T::STAGES == 2 && T::BK == 64, "the folded path double-buffers 64-deep stages");
   static_assert(!BKM || T::BN * 8 % T::NT == 0, "K-major B chunks must divide over threads");
@@ -621,7 +678,7 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
     }
   }
 
-  uint32_t a_off[T::KSTEPS];
+  uint32_t a_off[4] = {0, 0, 0, 0};
   {
     const int m = wm * T::TM + (lane & 31);
 #pragma unroll
@@ -641,7 +698,7 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
     }
   }
 
-  f32x16 acc[T::FM][T::FN];
+  AccT<T> acc[T::FM][T::FN];
 #pragma unroll
   for (int i = 0; i < T::FM; ++i)
 #pragma unroll
@@ -747,6 +804,7 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
 template <class T>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProblem p, int tiles_m, int tiles_n,
                                                                       uint32_t a_bytes, uint32_t b_bytes) {
+  static_assert(T::MF == 32, "the folded kernels use 32x32 fragments");
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
   static_assert(T::BN * T::CA % T::NT == 0, "K-major B chunks must divide over threads");
   constexpr int RBK = T::BN * T::CA / T::NT;  // K-major B chunks per thread
@@ -775,7 +833,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
     b_voff[r] = n < N ? (uint32_t)((fold_off(n, p.n_lo, p.bn[0], p.bn[1]) + kc) * 2) : kOobOffset;
   }
 
-  uint32_t a_off[T::KSTEPS], b_off[4] = {0, 0, 0, 0};
+  uint32_t a_off[4] = {0, 0, 0, 0}, b_off[4] = {0, 0, 0, 0};
   {
     const int m = wm * T::TM + (lane & 31), n = wn * T::TN + (lane & 31);
 #pragma unroll
@@ -785,7 +843,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
     }
   }
 
-  f32x16 acc[T::FM][T::FN];
+  AccT<T> acc[T::FM][T::FN];
 #pragma unroll
   for (int i = 0; i < T::FM; ++i)
 #pragma unroll
@@ -907,6 +965,12 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
 #ifndef MMM_DMA_WGN
 #define MMM_DMA_WGN 4
 #endif
+// MFMA shape of the 256x256 tile (measured at 8192^3 under sustained load: 16x16x32 runs at a
+// 16% higher power-limited clock than 32x32x16 -- a quarter of the accumulator traffic per
+// instruction -- and is 2-9% faster across 4096^3 .. 16384^2 x 4096)
+#ifndef MMM_DMA_MF
+#define MMM_DMA_MF 16
+#endif
 // 256x128 / 128x256 tiles: 4 waves; K step, ring depth and workgroups per CU
 // (measured at 8192^3: 32 x 3 stages with two workgroups per CU 1031-1064 TFLOP/s vs
 // 64 x 2 with one 868-908; two independent workgroups per CU desynchronise their barriers)
@@ -925,7 +989,7 @@ struct DmaCfg {  // 128x128
 };
 template <>
 struct DmaCfg<256, 256> {
-  using T = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1>;
+  using T = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1, MMM_DMA_MF>;
 };
 template <>
 struct DmaCfg<256, 128> {
@@ -937,6 +1001,8 @@ struct DmaCfg<128, 256> {
 };
 template <int BM, int BN>
 using DmaTile = typename DmaCfg<BM, BN>::T;
+// The folded direct-to-LDS kernel: the 256x256 tile's waves and ring with 32x32 fragments.
+using FoldDmaTile = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1, 32>;
 // Register-staged path: 64-deep stages, double-buffered.
 template <int BM, int BN>
 using RegTile = Tile<BM, BN, 2, 2, 64, 2>;
@@ -1022,7 +1088,7 @@ static int64_t fold_extent(int64_t e_hi, int64_t e_lo, int64_t s_hi, int64_t s_l
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream) {
   // direct-to-LDS fold path: K contiguous in both operands, K tiles inside one k_hi block,
   // 16-byte-aligned chunks, offsets within 32 bits
-  using TD = DmaTile<256, 256>;
+  using TD = FoldDmaTile;
   const int m_hi = (p.M + p.m_lo - 1) / p.m_lo, n_hi = (p.N + p.n_lo - 1) / p.n_lo, k_hi = p.K / p.k_lo;
   const int64_t a_ext = fold_extent(m_hi, p.m_lo, p.am[0], p.am[1], k_hi, p.k_lo, p.ak[0], p.ak[1]);
   const int64_t b_ext = fold_extent(n_hi, p.n_lo, p.bn[0], p.bn[1], k_hi, p.k_lo, p.bk[0], p.bk[1]);
