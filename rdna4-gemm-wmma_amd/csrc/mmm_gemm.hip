@@ -43,6 +43,12 @@
 #ifndef MMM_XINTERLEAVE
 #define MMM_XINTERLEAVE 1  // interleave the steady-state refill loads with the last K-step's MFMAs
 #endif
+#ifndef MMM_SPREAD_READS
+#define MMM_SPREAD_READS 1  // spread the next tile's first fragment reads over the last K-step's MFMAs
+#endif
+#ifndef MMM_PIN_BODY
+#define MMM_PIN_BODY 1  // keep a tile's body MFMAs ahead of the next tile's load wait and barrier
+#endif
 
 namespace mmm {
 
@@ -221,6 +227,20 @@ __device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char L
     else
       f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * T::KK) * T::BN * 2,
                               b_st + b_off[nb] + (kk * T::KK + 4) * T::BN * 2);
+  }
+}
+
+// Fragment read unit u of K-step kk (N-contiguous B): u < FM reads A fragment u, otherwise B
+// fragment u - FM (two transposing reads).
+template <class T>
+__device__ __forceinline__ void load_frag_unit(const char LDS_AS* a_st, const char LDS_AS* b_st,
+                                               const uint32_t (&a_off)[4], const uint32_t (&b_off)[4], int kk, int u,
+                                               Frags<T>& f) {
+  if (u < T::FM) {
+    f.a[u] = lds_read_a(a_st + a_off[kk * T::APAR + u % T::APAR] + (u / T::APAR) * T::AROWS * T::BK * 2);
+  } else {
+    const int nb = u - T::FM;
+    f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * T::KK) * T::BN * 2, b_st + b_off[nb] + (kk * T::KK + 4) * T::BN * 2);
   }
 }
 
@@ -460,6 +480,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
     // retired slot (`refill` loads tile t+S into slot `cur`), then the MFMAs.
     auto tile_next = [&](int t, auto&& refill) {
+      if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
       const int issued = t + S < KT ? t + S : KT;  // tiles 0 .. issued-1 are issued
       int ahead = issued - (t + 2);                // of those, after t+1 (may stay in flight)
       if (tail_regs && issued == KT && ahead > 0) --ahead;
@@ -472,24 +493,31 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       mfma_frags<T>(f[1], acc);
       cur = nslot;
     };
-    // Steady state: the refill's loads are interleaved one to one with the last K-step's MFMAs
-    // (scheduling fences keep the order), so no burst of load issue leaves the matrix pipe idle.
+    // Steady state: after the barrier the next tile's first fragment reads and the refill's
+    // loads are interleaved with the last K-step's MFMAs (scheduling fences keep the order), so
+    // neither a burst of LDS reads nor a burst of load issue leaves the matrix pipe idle.
+    // MFMA i carries fragment read i (i < FM + FN) when MMM_SPREAD_READS is set, and the DMA
+    // loads go on the MFMAs after the reads when there are enough of them.
     auto tile_next_interleaved = [&](int t) {
+      if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
       wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(S - 2);  // steady state: S-2 tiles after t+1 in flight
       block_sync();
       const int nslot = cur + 1 == S ? 0 : cur + 1;
       const char LDS_AS* ns = lds_base + nslot * T::STAGE;
-      load_frags<T, false>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
+      constexpr int NM = T::FM * T::FN, NU = MMM_SPREAD_READS ? T::FM + T::FN : 0;
+      constexpr int D0 = NM - T::LPT >= NU ? NU : (NM > T::LPT ? NM - T::LPT : 0);
+      if constexpr (!MMM_SPREAD_READS) load_frags<T, false>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
       const TileDma d = prep(t + S, cur);
 #pragma unroll
-      for (int i = 0; i < T::FM * T::FN; ++i) {
+      for (int i = 0; i < NM; ++i) {
         const int mb = i / T::FN, nb = i % T::FN;
         mfma_one<T>(f[1].b[nb], f[1].a[mb], acc[mb][nb]);
-        if (i < T::LPT) dma_one(d, i);
+        if (i < NU) load_frag_unit<T>(ns, ns + T::A_BYTES, a_off, b_off, 0, i, f[0]);
+        if (i >= D0 && i - D0 < T::LPT) dma_one(d, i - D0);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int j = T::FM * T::FN; j < T::LPT; ++j) dma_one(d, j);
+      for (int j = NM - D0; j < T::LPT; ++j) dma_one(d, j);
       cur = nslot;
     };
     // steady state refills by DMA only; the refill of the last tile (possibly gathered
