@@ -210,29 +210,11 @@ struct Frags {
 template <class T>
 using AccT = typename std::conditional<T::MF == 32, f32x16, f32x4>::type;
 
-// Fragment reads of K-step kk from an LDS stage (layouts as for compute_stage below).
-// a_off[kk * APAR + phase]: A fragment offsets; b_off[nb] (N-contiguous B) or b_off[kk]
-// (K-major B, 32x32 only).
+// Fragment read unit u of K-step kk: u < FM reads A fragment u; otherwise B fragment u - FM,
+// by one ds_read_b128 from a K-major B stage (BKM) or two transposing reads from an
+// N-contiguous one.  a_off[kk * APAR + phase]: A fragment offsets; b_off[nb] (N-contiguous
+// B) or b_off[kk * APAR + phase] (K-major B, laid out and swizzled like A).
 template <class T, bool BKM>
-__device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char LDS_AS* b_st, const uint32_t (&a_off)[4],
-                                           const uint32_t (&b_off)[4], int kk, Frags<T>& f) {
-  static_assert(!BKM || T::MF == 32, "K-major B stages use 32x32 fragments");
-#pragma unroll
-  for (int mb = 0; mb < T::FM; ++mb)
-    f.a[mb] = lds_read_a(a_st + a_off[kk * T::APAR + mb % T::APAR] + (mb / T::APAR) * T::AROWS * T::BK * 2);
-#pragma unroll
-  for (int nb = 0; nb < T::FN; ++nb) {
-    if constexpr (BKM)
-      f.b[nb] = lds_read_a(b_st + b_off[kk] + nb * 32 * T::BK * 2);
-    else
-      f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * T::KK) * T::BN * 2,
-                              b_st + b_off[nb] + (kk * T::KK + 4) * T::BN * 2);
-  }
-}
-
-// Fragment read unit u of K-step kk (N-contiguous B): u < FM reads A fragment u, otherwise B
-// fragment u - FM (two transposing reads).
-template <class T>
 __device__ __forceinline__ void load_frag_unit(const char LDS_AS* a_st, const char LDS_AS* b_st,
                                                const uint32_t (&a_off)[4], const uint32_t (&b_off)[4], int kk, int u,
                                                Frags<T>& f) {
@@ -240,8 +222,20 @@ __device__ __forceinline__ void load_frag_unit(const char LDS_AS* a_st, const ch
     f.a[u] = lds_read_a(a_st + a_off[kk * T::APAR + u % T::APAR] + (u / T::APAR) * T::AROWS * T::BK * 2);
   } else {
     const int nb = u - T::FM;
-    f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * T::KK) * T::BN * 2, b_st + b_off[nb] + (kk * T::KK + 4) * T::BN * 2);
+    if constexpr (BKM)
+      f.b[nb] = lds_read_a(b_st + b_off[kk * T::APAR + nb % T::APAR] + (nb / T::APAR) * T::AROWS * T::BK * 2);
+    else
+      f.b[nb] = lds_read_b_tr(b_st + b_off[nb] + (kk * T::KK) * T::BN * 2,
+                              b_st + b_off[nb] + (kk * T::KK + 4) * T::BN * 2);
   }
+}
+
+// All fragment reads of K-step kk from an LDS stage.
+template <class T, bool BKM>
+__device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char LDS_AS* b_st, const uint32_t (&a_off)[4],
+                                           const uint32_t (&b_off)[4], int kk, Frags<T>& f) {
+#pragma unroll
+  for (int u = 0; u < T::FM + T::FN; ++u) load_frag_unit<T, BKM>(a_st, b_st, a_off, b_off, kk, u, f);
 }
 
 // One MFMA of the tile's shape, operands swapped (B fragment as src A): acc holds C^T.
@@ -277,11 +271,123 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
   }
 }
 
+__device__ __forceinline__ void block_sync() { __syncthreads(); }
+
+// Cross-stage K loop over KT K tiles (the direct-to-LDS kernels).  The caller supplies the
+// loads: prep(t, slot) builds the per-tile load state of K tile t for ring slot `slot` (and
+// advances any running state: tiles are prepared in order), dma_one(d, j) issues load j of
+// T::LPT, and issue_tile(t, slot) fills slot `slot` with tile t by whatever means (the last
+// tile of an unaligned problem is gathered through VGPRs when tail_regs is set, which leaves
+// no loads in flight for it).
+template <class T, bool BKM, class Prep, class DmaOne, class IssueTile>
+__device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool tail_regs, const uint32_t (&a_off)[4],
+                                            const uint32_t (&b_off)[4], AccT<T> (&acc)[T::FM][T::FN], Prep&& prep,
+                                            DmaOne&& dma_one, IssueTile&& issue_tile) {
+  auto issue = [&](int t, int stage) {
+    const auto d = prep(t, stage);
+#pragma unroll
+    for (int j = 0; j < T::LPT; ++j) dma_one(d, j);
+  };
+  // Ring of S slots, tile u in slot u % S.  Cross-stage pipeline: during the last K-step of
+  // tile t, this wave waits for its own loads of tile t+1, then the barrier (a) publishes
+  // tile t+1 -- every wave's loads of it have landed -- and (b) retires slot t % S: every
+  // wave has completed its reads of tile t, since a barrier waits for outstanding LDS reads
+  // and tile t's last fragments were read before it.  After the barrier the wave reads
+  // tile t+1's first fragments and refills slot t % S with tile t+S, and only then issues
+  // tile t's last MFMAs, which cover the barrier and the first reads' latency.
+  constexpr int S = T::STAGES;
+  static_assert(T::KSTEPS % 2 == 0, "fragment double buffer alternates per K-step");
+  const int first = KT < S ? KT : S;
+  for (int s = 0; s < first; ++s) issue_tile(s, s);
+  // tile 0 must land; later tiles may stay in flight (a gathered last tile has no loads)
+  wait_tiles<T::LPT, S - 1>(first - 1 - ((tail_regs && first == KT) ? 1 : 0));
+  block_sync();
+  Frags<T> f[2];
+  load_frags<T, BKM>(lds_base, lds_base + T::A_BYTES, a_off, b_off, 0, f[0]);
+  int cur = 0;
+  // K-steps 0 .. KSTEPS-2 of the tile in slot `cur` (each step's MFMAs run while the next
+  // step's fragments are read).
+  auto tile_body = [&] {
+    const char LDS_AS* st = lds_base + cur * T::STAGE;
+#pragma unroll
+    for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
+      load_frags<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, f[(kk + 1) & 1]);
+      mfma_frags<T>(f[kk & 1], acc);
+      // keep the next step's LDS reads ahead of this step's MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);
+    }
+  };
+  // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
+  // retired slot (`refill` loads tile t+S into slot `cur`), then the MFMAs.
+  auto tile_next = [&](int t, auto&& refill) {
+    if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
+    const int issued = t + S < KT ? t + S : KT;  // tiles 0 .. issued-1 are issued
+    int ahead = issued - (t + 2);                // of those, after t+1 (may stay in flight)
+    if (tail_regs && issued == KT && ahead > 0) --ahead;
+    wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(ahead);
+    block_sync();
+    const int nslot = cur + 1 == S ? 0 : cur + 1;
+    const char LDS_AS* ns = lds_base + nslot * T::STAGE;
+    load_frags<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
+    refill();
+    mfma_frags<T>(f[1], acc);
+    cur = nslot;
+  };
+  // Steady state: after the barrier the next tile's first fragment reads and the refill's
+  // loads are interleaved with the last K-step's MFMAs (scheduling fences keep the order), so
+  // neither a burst of LDS reads nor a burst of load issue leaves the matrix pipe idle.
+  // MFMA i carries fragment read i (i < FM + FN) when MMM_SPREAD_READS is set, and the DMA
+  // loads go on the MFMAs after the reads when there are enough of them.
+  auto tile_next_interleaved = [&](int t) {
+    if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
+    wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(S - 2);  // steady state: S-2 tiles after t+1 in flight
+    block_sync();
+    const int nslot = cur + 1 == S ? 0 : cur + 1;
+    const char LDS_AS* ns = lds_base + nslot * T::STAGE;
+    constexpr int NM = T::FM * T::FN, NU = MMM_SPREAD_READS ? T::FM + T::FN : 0;
+    constexpr int D0 = NM - T::LPT >= NU ? NU : (NM > T::LPT ? NM - T::LPT : 0);
+    if constexpr (!MMM_SPREAD_READS) load_frags<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
+    const auto d = prep(t + S, cur);
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      const int mb = i / T::FN, nb = i % T::FN;
+      mfma_one<T>(f[1].b[nb], f[1].a[mb], acc[mb][nb]);
+      if (i < NU) load_frag_unit<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, i, f[0]);
+      if (i >= D0 && i - D0 < T::LPT) dma_one(d, i - D0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = NM - D0; j < T::LPT; ++j) dma_one(d, j);
+    cur = nslot;
+  };
+  // steady state refills by DMA only; the refill of the last tile (possibly gathered
+  // through VGPRs) is peeled so the loop carries no gather registers
+  int t = 0;
+  for (; t + S < KT - 1; ++t) {
+    tile_body();
+    if constexpr (MMM_XINTERLEAVE)
+      tile_next_interleaved(t);
+    else
+      tile_next(t, [&] { issue(t + S, cur); });
+  }
+  if (t + S == KT - 1) {
+    tile_body();
+    tile_next(t, [&] { issue_tile(t + S, cur); });
+    ++t;
+  }
+  for (; t + 1 < KT; ++t) {
+    tile_body();
+    tile_next(t, [] {});
+  }
+  tile_body();
+  mfma_frags<T>(f[1], acc);
+}
+
 struct NoHook {
   __device__ __forceinline__ void operator()() const {}
 };
 
-__device__ __forceinline__ void block_sync() { __syncthreads(); }
 
 // GENERIC = false: direct-to-LDS buffer loads; needs lda, ldb, K, N multiples of 8 and
 //                  16-byte-aligned A and B (checked by the host).
@@ -447,100 +553,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         issue(t, stage);
     };
 
-    // Ring of S slots, tile u in slot u % S.  Cross-stage pipeline: during the last K-step of
-    // tile t, this wave waits for its own loads of tile t+1, then the barrier (a) publishes
-    // tile t+1 -- every wave's loads of it have landed -- and (b) retires slot t % S: every
-    // wave has completed its reads of tile t, since a barrier waits for outstanding LDS reads
-    // and tile t's last fragments were read before it.  After the barrier the wave reads
-    // tile t+1's first fragments and refills slot t % S with tile t+S, and only then issues
-    // tile t's last MFMAs, which cover the barrier and the first reads' latency.
-    constexpr int S = T::STAGES;
-    static_assert(T::KSTEPS % 2 == 0, "fragment double buffer alternates per K-step");
-    const int first = KT < S ? KT : S;
-    for (int s = 0; s < first; ++s) issue_tile(s, s);
-    // tile 0 must land; later tiles may stay in flight (a gathered last tile has no loads)
-    wait_tiles<T::LPT, S - 1>(first - 1 - ((tail_regs && first == KT) ? 1 : 0));
-    block_sync();
-    Frags<T> f[2];
-    load_frags<T, false>(lds_base, lds_base + T::A_BYTES, a_off, b_off, 0, f[0]);
-    int cur = 0;
-    // K-steps 0 .. KSTEPS-2 of the tile in slot `cur` (each step's MFMAs run while the next
-    // step's fragments are read).
-    auto tile_body = [&] {
-      const char LDS_AS* st = lds_base + cur * T::STAGE;
-#pragma unroll
-      for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
-        load_frags<T, false>(st, st + T::A_BYTES, a_off, b_off, kk + 1, f[(kk + 1) & 1]);
-        mfma_frags<T>(f[kk & 1], acc);
-        // keep the next step's LDS reads ahead of this step's MFMAs
-        __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);
-      }
-    };
-    // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
-    // retired slot (`refill` loads tile t+S into slot `cur`), then the MFMAs.
-    auto tile_next = [&](int t, auto&& refill) {
-      if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
-      const int issued = t + S < KT ? t + S : KT;  // tiles 0 .. issued-1 are issued
-      int ahead = issued - (t + 2);                // of those, after t+1 (may stay in flight)
-      if (tail_regs && issued == KT && ahead > 0) --ahead;
-      wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(ahead);
-      block_sync();
-      const int nslot = cur + 1 == S ? 0 : cur + 1;
-      const char LDS_AS* ns = lds_base + nslot * T::STAGE;
-      load_frags<T, false>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
-      refill();
-      mfma_frags<T>(f[1], acc);
-      cur = nslot;
-    };
-    // Steady state: after the barrier the next tile's first fragment reads and the refill's
-    // loads are interleaved with the last K-step's MFMAs (scheduling fences keep the order), so
-    // neither a burst of LDS reads nor a burst of load issue leaves the matrix pipe idle.
-    // MFMA i carries fragment read i (i < FM + FN) when MMM_SPREAD_READS is set, and the DMA
-    // loads go on the MFMAs after the reads when there are enough of them.
-    auto tile_next_interleaved = [&](int t) {
-      if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
-      wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(S - 2);  // steady state: S-2 tiles after t+1 in flight
-      block_sync();
-      const int nslot = cur + 1 == S ? 0 : cur + 1;
-      const char LDS_AS* ns = lds_base + nslot * T::STAGE;
-      constexpr int NM = T::FM * T::FN, NU = MMM_SPREAD_READS ? T::FM + T::FN : 0;
-      constexpr int D0 = NM - T::LPT >= NU ? NU : (NM > T::LPT ? NM - T::LPT : 0);
-      if constexpr (!MMM_SPREAD_READS) load_frags<T, false>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
-      const TileDma d = prep(t + S, cur);
-#pragma unroll
-      for (int i = 0; i < NM; ++i) {
-        const int mb = i / T::FN, nb = i % T::FN;
-        mfma_one<T>(f[1].b[nb], f[1].a[mb], acc[mb][nb]);
-        if (i < NU) load_frag_unit<T>(ns, ns + T::A_BYTES, a_off, b_off, 0, i, f[0]);
-        if (i >= D0 && i - D0 < T::LPT) dma_one(d, i - D0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int j = NM - D0; j < T::LPT; ++j) dma_one(d, j);
-      cur = nslot;
-    };
-    // steady state refills by DMA only; the refill of the last tile (possibly gathered
-    // through VGPRs) is peeled so the loop carries no gather registers
-    int t = 0;
-    for (; t + S < KT - 1; ++t) {
-      tile_body();
-      if constexpr (MMM_XINTERLEAVE)
-        tile_next_interleaved(t);
-      else
-        tile_next(t, [&] { issue(t + S, cur); });
-    }
-    if (t + S == KT - 1) {
-      tile_body();
-      tile_next(t, [&] { issue_tile(t + S, cur); });
-      ++t;
-    }
-    for (; t + 1 < KT; ++t) {
-      tile_body();
-      tile_next(t, [] {});
-    }
-    tile_body();
-    mfma_frags<T>(f[1], acc);
+    cross_stage<T, false>(lds_base, KT, tail_regs, a_off, b_off, acc, prep, dma_one, issue_tile);
   } else {
     static_assert(!GENERIC || T::STAGES == 2, "the register-staged path double-buffers");
     (void)t_begin;
@@ -832,11 +845,11 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
 template <class T>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProblem p, int tiles_m, int tiles_n,
                                                                       uint32_t a_bytes, uint32_t b_bytes) {
-  static_assert(T::MF == 32, "the folded kernels use 32x32 fragments");
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
   static_assert(T::BN * T::CA % T::NT == 0, "K-major B chunks must divide over threads");
   constexpr int RBK = T::BN * T::CA / T::NT;  // K-major B chunks per thread
-  constexpr int RPA = T::NT / T::CA;          // rows per round (A and B alike)
+  static_assert(RBK == T::RB, "the K-major B stage holds as many chunks as the N-contiguous one");
+  constexpr int RPA = T::NT / T::CA;  // rows per round (A and B alike)
   static_assert(RPA % T::SWZ_A_ROWS == 0, "round strides must preserve the swizzle");
 
   int tm, tn;
@@ -861,73 +874,74 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
     b_voff[r] = n < N ? (uint32_t)((fold_off(n, p.n_lo, p.bn[0], p.bn[1]) + kc) * 2) : kOobOffset;
   }
 
+  // fragment read offsets: A rows and K-major B columns share the layout (lane l reads row
+  // l % MF, k chunk l / MF of each K-step)
   uint32_t a_off[4] = {0, 0, 0, 0}, b_off[4] = {0, 0, 0, 0};
-  {
-    const int m = wm * T::TM + (lane & 31), n = wn * T::TN + (lane & 31);
 #pragma unroll
-    for (int kk = 0; kk < T::KSTEPS; ++kk) {
-      a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(m)) * 16;
-      b_off[kk] = n * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(n)) * 16;
+  for (int kk = 0; kk < T::KSTEPS; ++kk)
+#pragma unroll
+    for (int ph = 0; ph < T::APAR; ++ph) {
+      const int m = wm * T::TM + ph * T::MF + (lane % T::MF), n = wn * T::TN + ph * T::MF + (lane % T::MF);
+      const int chunk = (T::KK / 8) * kk + lane / T::MF;
+      a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
+      b_off[kk * T::APAR + ph] = n * T::BK * 2 + (chunk ^ T::swz_a(n)) * 16;
     }
-  }
 
   AccT<T> acc[T::FM][T::FN];
 #pragma unroll
   for (int i = 0; i < T::FM; ++i)
 #pragma unroll
-    for (int j = 0; j < T::FN; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < T::FN; ++j) acc[i][j] = AccT<T>{};
 
   char LDS_AS* lds_base = (char LDS_AS*)lds;
   const i32x4 ra = make_rsrc(p.A, a_bytes);
   const i32x4 rb = make_rsrc(p.B, b_bytes);
-  auto issue = [&](int t, int stage) {
-    const int k0 = t * T::BK;
-    const uint32_t ka = (uint32_t)(((k0 / p.k_lo) * p.ak[0] + k0 % p.k_lo) * 2);
-    const uint32_t kb = (uint32_t)(((k0 / p.k_lo) * p.bk[0] + k0 % p.k_lo) * 2);
-    const uint32_t a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
-    const uint32_t b_dst = a_dst + T::A_BYTES;
-#pragma unroll
-    for (int r = 0; r < T::RA; ++r) dma_b128(a_dst + r * T::NT * 16, ra, a_voff[r] + ka);
-#pragma unroll
-    for (int r = 0; r < RBK; ++r) dma_b128(b_dst + r * T::NT * 16, rb, b_voff[r] + kb);
+  // K tile t starts at k0 = t * BK = (k_hi, k_rem): uniform offsets k_hi * ak0 + k_rem (A) and
+  // k_hi * bk0 + k_rem (B), advanced per tile (tiles are prepared in order).
+  struct FoldDma {
+    uint32_t a_dst, b_dst, ka, kb;
   };
+  int k_hi = 0, k_rem = 0;
+  auto prep = [&](int t, int stage) {
+    FoldDma d;
+    d.ka = (uint32_t)(((int64_t)k_hi * p.ak[0] + k_rem) * 2);
+    d.kb = (uint32_t)(((int64_t)k_hi * p.bk[0] + k_rem) * 2);
+    k_rem += T::BK;
+    if (k_rem == p.k_lo) k_rem = 0, ++k_hi;
+    d.a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
+    d.b_dst = d.a_dst + T::A_BYTES;
+    return d;
+  };
+  auto dma_one = [&](const FoldDma& d, int j) {
+    if (j < T::RA)
+      dma_b128(d.a_dst + j * T::NT * 16, ra, a_voff[j] + d.ka);
+    else
+      dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, rb, b_voff[j - T::RA] + d.kb);
+  };
+  auto issue_tile = [&](int t, int stage) {
+    const FoldDma d = prep(t, stage);
+#pragma unroll
+    for (int j = 0; j < T::LPT; ++j) dma_one(d, j);
+  };
+  cross_stage<T, true>(lds_base, K / T::BK, false, a_off, b_off, acc, prep, dma_one, issue_tile);
 
-  const int KT = K / T::BK;
-  constexpr int P = T::STAGES - 1;
-  constexpr int LPT = T::RA + RBK;
-  for (int s = 0; s < P; ++s)
-    if (s < KT) issue(s, s);
-  int cur = 0, nxt = P;
-  int t = 0;
-  for (; t + P < KT; ++t) {
-    wait_vmcnt<(P - 1) * LPT>();
-    block_sync();
-    const char LDS_AS* st = lds_base + cur * T::STAGE;
-    compute_stage<T, true>(st, st + T::A_BYTES, a_off, b_off, acc, [&] { issue(t + P, nxt); });
-    cur = cur + 1 == T::STAGES ? 0 : cur + 1;
-    nxt = nxt + 1 == T::STAGES ? 0 : nxt + 1;
-  }
-  for (; t < KT; ++t) {
-    wait_dma();
-    block_sync();
-    const char LDS_AS* st = lds_base + cur * T::STAGE;
-    compute_stage<T, true>(st, st + T::A_BYTES, a_off, b_off, acc, NoHook{});
-    cur = cur + 1 == T::STAGES ? 0 : cur + 1;
-  }
-
+  // epilogue: lane owns row m and columns n .. n+3 of each accumulator group, scattered
+  // through the C strides (MF = 32: m = l % 32, n = 32*nb + 8*q + 4*(l/32); MF = 16:
+  // m = l % 16, n = 16*nb + 4*(l/16))
+  constexpr int NQ = T::MF == 32 ? 4 : 1;
   float* C = p.C;
 #pragma unroll
   for (int mb = 0; mb < T::FM; ++mb) {
-    const int m = m0 + wm * T::TM + 32 * mb + (lane & 31);
+    const int m = m0 + wm * T::TM + T::MF * mb + (lane % T::MF);
     if (m >= M) continue;
     const int64_t crow = fold_off(m, p.m_lo, p.cm[0], p.cm[1]);
 #pragma unroll
     for (int nb = 0; nb < T::FN; ++nb)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < NQ; ++q)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int n = n0 + wn * T::TN + 32 * nb + 8 * q + 4 * (lane >> 5) + e;
+          const int n = n0 + wn * T::TN + (T::MF == 32 ? 32 * nb + 8 * q + 4 * (lane >> 5) : 16 * nb + 4 * (lane >> 4)) + e;
           if (n < N) C[crow + fold_off(n, p.n_lo, p.cn[0], p.cn[1])] = acc[mb][nb][4 * q + e];
         }
   }
@@ -1029,8 +1043,11 @@ struct DmaCfg<128, 256> {
 };
 template <int BM, int BN>
 using DmaTile = typename DmaCfg<BM, BN>::T;
-// The folded direct-to-LDS kernel: the 256x256 tile's waves and ring with 32x32 fragments.
-using FoldDmaTile = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1, 32>;
+// The folded direct-to-LDS kernel: the 256x256 tile's waves and ring.
+#ifndef MMM_FOLD_MF
+#define MMM_FOLD_MF 16
+#endif
+using FoldDmaTile = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1, MMM_FOLD_MF>;
 // Register-staged path: 64-deep stages, double-buffered.
 template <int BM, int BN>
 using RegTile = Tile<BM, BN, 2, 2, 64, 2>;
