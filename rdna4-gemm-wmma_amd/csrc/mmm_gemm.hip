@@ -1025,9 +1025,15 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
 #ifndef MMM_T2_OCC
 #define MMM_T2_OCC 2
 #endif
+// MFMA shape of the 128x128 tile: 32x32x16 (16x16x32 measured 2-7% slower at the 1024..3072
+// sizes this tile serves; its short K loops and two workgroups per CU gain less from the
+// higher clock than they lose to the doubled MFMA issue count)
+#ifndef MMM_T1_MF
+#define MMM_T1_MF 32
+#endif
 template <int BM, int BN>
 struct DmaCfg {  // 128x128
-  using T = Tile<BM, BN, 2, 2, 64, 2, 2>;
+  using T = Tile<BM, BN, 2, 2, 64, 2, 2, MMM_T1_MF>;
 };
 template <>
 struct DmaCfg<256, 256> {
