@@ -1026,8 +1026,7 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
 #define MMM_T2_OCC 2
 #endif
 // MFMA shape of the 128x128 tile: 32x32x16 (16x16x32 measured 2-7% slower at the 1024..3072
-// sizes this tile serves; its short K loops and two workgroups per CU gain less from the
-// higher clock than they lose to the doubled MFMA issue count)
+// sizes this tile serves, faster only at 8192^3, where the 256x256 tile runs)
 #ifndef MMM_T1_MF
 #define MMM_T1_MF 32
 #endif
