@@ -72,7 +72,7 @@ hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C,
 #define MMM_KERNEL_NONE 0        /* M == 0 or N == 0: nothing */
 #define MMM_KERNEL_ZERO 1        /* K == 0: C = 0 */
 #define MMM_KERNEL_TILE 2        /* matrix-core tile kernel over all of C */
-#define MMM_KERNEL_STREAM 3      /* M <= 16: HBM-streaming kernel */
+#define MMM_KERNEL_STREAM 3      /* M <= 64: HBM-streaming kernel */
 #define MMM_KERNEL_TILE_STREAM 4 /* tile kernel on the first tile_rows rows, streaming kernel on the rest */
 
 typedef struct mmm_gemm_plan {

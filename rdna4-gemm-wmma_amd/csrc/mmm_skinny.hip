@@ -1,12 +1,12 @@
-// Streaming GEMM for M <= 16 (decode-shaped, e.g. 16 x 8192 x 8192): HBM-bound, so the design
+// Streaming GEMM for M <= 64 (decode-shaped, e.g. 16 x 8192 x 8192): HBM-bound, so the design
 // goal is to stream B once at full bandwidth with the MFMA work hidden underneath.  Two kernels:
 //
-//  * gemm_stream_wide_kernel (the default when a workspace is available): one workgroup per
-//    128-column strip and K range; every wave streams the strip's full 256-byte rows of B
-//    over its quarter of the range; K partials summed through LDS, K ranges across
-//    workgroups summed by reduce_splits_kernel in a fixed order.
-//  * gemm_skinny_kernel (no workspace, e.g. under graph capture): one workgroup per 32-column
-//    strip, XCD-contiguous; the four waves split K; partials summed through LDS.
+//  * gemm_stream_wide_kernel<MR> (MR = 1, 2, 4 groups of 16 rows): one workgroup per 128-column
+//    strip and K range; every wave streams the strip's full 256-byte rows of B over its quarter
+//    of the range; K partials summed through LDS, K ranges across workgroups summed by
+//    reduce_splits_kernel in a fixed order.
+//  * gemm_skinny_kernel (M <= 16 with no workspace, e.g. under graph capture): one workgroup per
+//    32-column strip, XCD-contiguous; the four waves split K; partials summed through LDS.
 //
 // Common to both: each wave streams through its own LDS ring with direct-to-LDS buffer loads
 // and only reads what it loaded itself, so the loop has no workgroup barrier (a wave waits on

@@ -192,7 +192,7 @@ def test_exact_unaligned_rows(mm, cuda, shape):
 @pytest.mark.parametrize("shape", [(16, 8192, 8192), (5, 1000, 2000), (16, 96, 72), (1, 64, 8), (11, 520, 4104)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_exact_skinny(mm, cuda, shape):
-    """M <= 16 runs on the 16-row streaming kernel (fixed-order reductions)."""
+    """M <= 16 runs on the streaming kernel's 16-row variant (fixed-order reductions)."""
     M, N, K = shape
     rng = np.random.default_rng(M * 13 + N + K)
     A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
