@@ -16,7 +16,7 @@
  *  - Pointers are device pointers owned by the caller.  No entry point synchronises the host
  *    or exits the process.  The only device memory the library allocates is the workspace
  *    of its K splits (launches that would leave most of the chip idle split K across
- *    workgroups and sum the partials in a fixed order): 32 MiB per (device, stream), on the
+ *    workgroups and sum the partials in a fixed order): 64 MiB per (device, stream), on the
  *    first split call on that stream, kept until the process exits.  A call made while its
  *    stream is being captured into a graph never allocates: without a workspace it runs
  *    unsplit (the streaming kernel's variant gives the same results bit for bit).
@@ -86,6 +86,9 @@ typedef struct mmm_gemm_plan {
                                               workgroups (0: split among one workgroup's waves) */
     int tile_splits;                       /* K ranges of the tile kernel (1: no split); a split
                                               launch is followed by an ordered reduction kernel */
+    int tile_split_tiles;                  /* tiles that run as tile_splits K ranges: the last,
+                                              partly filled round of 256 workgroups (all tiles
+                                              when the grid is one small round); 0: none */
 } mmm_gemm_plan;
 
 /*

@@ -156,23 +156,29 @@ hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream) {
 // ---------------------------------------------------------------- tile selection
 // Estimated time of a tile launch, in seconds: rounds of 256 concurrent workgroups (one per
 // CU) times the MFMA time of one tile's K range at the tile's relative efficiency (measured
-// at 8192^3, each tile forced: 256x256 1.0, 128x256 0.84, 256x128 0.80, 128x128 0.78), a
-// fixed per-round cost (prologue, epilogue), and, for a K split, the reduction's traffic and
-// launch.
+// at 8192^3, each tile forced: 256x256 1.0, 128x256 0.84, 256x128 0.80, 128x128 0.78) plus a
+// fixed per-round cost (prologue, epilogue).  With a K split (gemm_nn_split) the split tiles'
+// round runs K / splits, and the reduction's traffic and launch are added.
 static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
   static const struct {
     int bm, bn;
     double eff;
   } shape[4] = {{256, 256, 1.0}, {128, 256, 0.84}, {256, 128, 0.80}, {128, 128, 0.78}};
   const int bm = shape[tile].bm, bn = shape[tile].bn;
-  const int splits = gemm_nn_splits(p, tile);
+  const TileSplit sp = gemm_nn_split(p, tile);
   const double tiles = (double)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
-  const double rounds = std::ceil(tiles * splits / 256.0);
-  const double k = std::ceil((double)p.K / splits / 64.0) * 64.0;
   const double per_cu_flops = 4.8e12;  // sustained MFMA rate of one CU under load (256x256 at 8192^3)
-  double t = rounds * (2.0 * bm * bn * k / (per_cu_flops * shape[tile].eff) + 3e-6);
-  if (splits > 1) t += tiles * bm * bn * 4.0 * (splits + 1) / 4e12 + 3e-6;
-  *splits_out = splits;
+  auto round = [&](double k) { return 2.0 * bm * bn * k / (per_cu_flops * shape[tile].eff) + 3e-6; };
+  const double k_full = std::ceil((double)p.K / 64.0) * 64.0;
+  double t;
+  if (sp.splits > 1) {
+    const double whole_rounds = std::ceil((tiles - sp.tiles) / 256.0);
+    t = whole_rounds * round(k_full) + round(std::ceil((double)p.K / sp.splits / 64.0) * 64.0) +
+        (double)sp.tiles * bm * bn * 4.0 * (2.0 * sp.splits + 1) / 4e12 + 3e-6;
+  } else {
+    t = std::ceil(tiles / 256.0) * round(k_full);
+  }
+  *splits_out = sp.splits;
   return t;
 }
 
@@ -356,7 +362,9 @@ hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const floa
     GemmProblem pm = p;
     pm.M = pl.tile_rows;
     plan->direct_to_lds = gemm_nn_direct_to_lds(pm, pl.tile) ? 1 : 0;
-    plan->tile_splits = gemm_nn_splits(pm, pl.tile);
+    const TileSplit sp = gemm_nn_split(pm, pl.tile);
+    plan->tile_splits = sp.splits;
+    plan->tile_split_tiles = sp.splits > 1 ? sp.tiles : 0;
   }
   if (pl.kind == MMM_KERNEL_STREAM || pl.kind == MMM_KERNEL_TILE_STREAM) {
     GemmProblem pr = p;

@@ -396,13 +396,25 @@ template <class T, bool GENERIC>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
 
-  // K split (direct-to-LDS path only): blocks [q * tiles, (q+1) * tiles) compute K range q of
-  // every tile; each split layer walks the tiles in the same XCD-aware order.
-  const int nsplit = (!GENERIC && p.k_splits > 1) ? p.k_splits : 1;
+  // K split (direct-to-LDS path only).  Blocks [0, whole) compute tiles 0 .. whole-1 of the
+  // XCD-aware order over their full K range; the last split_tiles tiles of that order are split:
+  // block whole + q * split_tiles + j computes K range q of tile whole + j (each split layer
+  // walks those tiles in the same order).
   const int ntiles = tiles_m * tiles_n;
-  const int q = __builtin_amdgcn_readfirstlane((int)blockIdx.x / ntiles);
+  const int ksplit = (!GENERIC && p.k_splits > 1) ? p.k_splits : 1;
+  const int whole = ksplit > 1 ? ntiles - p.split_tiles : ntiles;
+  const bool split_block = (int)blockIdx.x >= whole;
+  const int nsplit = split_block ? ksplit : 1;
+  int q = 0, j = 0, bt = (int)blockIdx.x;
+  if (split_block) {
+    const int b2 = (int)blockIdx.x - whole;
+    q = b2 / p.split_tiles;
+    j = b2 - q * p.split_tiles;
+    bt = whole + j;
+  }
+  q = __builtin_amdgcn_readfirstlane(q);
   int tm, tn;
-  tile_of_block((int)blockIdx.x - q * ntiles, tiles_m, tiles_n, 4, &tm, &tn);
+  tile_of_block(bt, tiles_m, tiles_n, 4, &tm, &tn);
   // The tile origin is uniform; readfirstlane keeps it (and everything derived from it, such
   // as the buffer descriptors) in SGPRs -- the integer divisions above are expanded on the VALU.
   const int m0 = __builtin_amdgcn_readfirstlane(tm * T::BM), n0 = __builtin_amdgcn_readfirstlane(tn * T::BN);
@@ -622,7 +634,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     return T::MF == 32 ? 32 * nb + 8 * qq + 4 * (lane >> 5) : 16 * nb + 4 * (lane >> 4);
   };
   if (nsplit > 1) {  // K split: the whole tile (rows/columns past M/N included) to the partials
-    float* part = p.partials + ((int64_t)(tm * tiles_n + tn) * nsplit + q) * (T::BM * T::BN);
+    float* part = p.partials + ((int64_t)j * nsplit + q) * (T::BM * T::BN);
 #pragma unroll
     for (int mb = 0; mb < T::FM; ++mb) {
       float* prow = part + (wm * T::TM + T::MF * mb + (lane % T::MF)) * T::BN + wn * T::TN;
@@ -951,16 +963,20 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
 // Host-side launch
 // ------------------------------------------------------------------------------------
 // C tile = sum over the K splits, in split order (fixed order: deterministic), of the partial
-// tiles written by gemm_nn_kernel; one thread per 4 consecutive columns.
+// tiles written by gemm_nn_kernel for split tile j (tile `first + j` of the XCD-aware order);
+// one thread per 4 consecutive columns.
 template <int BM, int BN>
-__global__ __launch_bounds__(256) void reduce_tiles_kernel(GemmProblem p, int tiles_n, int splits) {
+__global__ __launch_bounds__(256) void reduce_tiles_kernel(GemmProblem p, int tiles_m, int tiles_n, int first,
+                                                           int splits) {
   constexpr int F4 = BM * BN / 4;  // float4s per tile
   const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int tile = (int)(g / F4), e = (int)(g % F4);
+  const int j = (int)(g / F4), e = (int)(g % F4);
+  int tm, tn;
+  tile_of_block(first + j, tiles_m, tiles_n, 4, &tm, &tn);
   const int r = e / (BN / 4), c = 4 * (e % (BN / 4));
-  const int m = (tile / tiles_n) * BM + r, n = (tile % tiles_n) * BN + c;
+  const int m = tm * BM + r, n = tn * BN + c;
   if (m >= p.M || n >= p.N) return;
-  const f32x4* src = (const f32x4*)(p.partials + (int64_t)tile * splits * (BM * BN)) + e;
+  const f32x4* src = (const f32x4*)(p.partials + (int64_t)j * splits * (BM * BN)) + e;
   f32x4 sum = src[0];
   for (int s = 1; s < splits; ++s) sum += src[(int64_t)s * F4];
   float* crow = p.C + (int64_t)m * p.ldc;
@@ -979,14 +995,17 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
   const int tiles_n = (p.N + T::BN - 1) / T::BN;
   const int64_t tiles = (int64_t)tiles_m * tiles_n;
   const int splits = p.k_splits > 1 ? p.k_splits : 1;
-  if (tiles * splits > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_nn_kernel<T, GENERIC>), dim3((unsigned)(tiles * splits)), dim3(T::NT), 0, stream, p,
-                     tiles_m, tiles_n);
+  const int64_t split_tiles = splits > 1 ? p.split_tiles : 0;
+  if (split_tiles < 0 || split_tiles > tiles) return hipErrorInvalidValue;
+  const int64_t blocks = tiles - split_tiles + split_tiles * splits;
+  if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_nn_kernel<T, GENERIC>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
+                     tiles_n);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   const int64_t per_tile = T::BM * T::BN / 4 / 256;  // blocks of 256 float4s per tile
-  hipLaunchKernelGGL((reduce_tiles_kernel<T::BM, T::BN>), dim3((unsigned)(tiles * per_tile)), dim3(256), 0, stream,
-                     p, tiles_n, splits);
+  hipLaunchKernelGGL((reduce_tiles_kernel<T::BM, T::BN>), dim3((unsigned)(split_tiles * per_tile)), dim3(256), 0,
+                     stream, p, tiles_m, tiles_n, (int)(tiles - split_tiles), splits);
   return hipGetLastError();
 }
 
@@ -1080,23 +1099,36 @@ bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id) {
   return dma_ok(p, tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128);
 }
 
-// K splits for a tile launch that leaves most of the chip idle: enough layers to reach about
-// one workgroup per CU (256), at least 8 K tiles per split, at most 16 splits, and the partial
-// tiles within the stream workspace.  Direct-to-LDS path only.
-int gemm_nn_splits(const GemmProblem& p, int tile_id) {
-  if (!gemm_nn_direct_to_lds(p, tile_id)) return 1;
+// K split for a tile launch whose last round of 256 workgroups (one per CU) is less than half
+// full -- the whole grid when it is one small round: the last round's tiles each run as
+// `splits` K ranges, enough to refill about one workgroup per CU (at least 8 64-deep K tiles
+// each, at most 16, partial tiles within the stream workspace).  Taken only when the round
+// time it saves exceeds the reduction's traffic (each split writes its partial tile; the
+// reduction reads them and writes C) and launch.  Direct-to-LDS path only.
+TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
+  if (!gemm_nn_direct_to_lds(p, tile_id)) return {1, 0};
   const int bm = tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128;
   const int bn = tile_id == kTile256x256 || tile_id == kTile128x256 ? 256 : 128;
   const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
-  if (tiles >= 128) return 1;
+  const int64_t last = tiles - (tiles - 1) / 256 * 256;  // tiles in the last round (1 .. 256)
+  if (last >= 128) return {1, 0};
   const int kt = (p.K + 63) / 64;  // 64-deep K tiles (the 32-deep tiles have twice as many)
-  int64_t splits = 256 / tiles;
+  int64_t splits = 256 / last;
   if (splits > kt / 8) splits = kt / 8;
   if (splits > 16) splits = 16;
-  const int64_t cap = (int64_t)(kStreamWorkspaceBytes / ((size_t)bm * bn * 4)) / tiles;
+  const int64_t cap = (int64_t)(kStreamWorkspaceBytes / ((size_t)bm * bn * 4)) / last;
   if (splits > cap) splits = cap;
-  return splits >= 2 ? (int)splits : 1;
+  if (splits < 2) return {1, 0};
+  // one tile's round at 4.8 TFLOP/s per CU (the 256x256 tile at 8192^3; smaller tiles run
+  // slower, so this underestimates the saving); reduction at 4 TB/s plus 3 us
+  const double round = 2.0 * bm * bn * (kt * 64.0) / 4.8e12;
+  const double saved = round * (1.0 - 1.0 / (double)splits);
+  const double cost = (double)last * bm * bn * 4.0 * (2.0 * splits + 1.0) / 4e12 + 3e-6;
+  if (saved <= cost) return {1, 0};
+  return {(int)splits, (int)last};
 }
+
+int gemm_nn_splits(const GemmProblem& p, int tile_id) { return gemm_nn_split(p, tile_id).splits; }
 
 hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream) {
   GemmProblem p = p0;
@@ -1104,11 +1136,12 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
   p.c_vec4 = (uintptr_t)p.C % 4 == 0;
   p.tail_regs = !tail_aligned(p);
   p.k_splits = 1;
+  p.split_tiles = 0;
   p.partials = nullptr;
-  const int splits = gemm_nn_splits(p, tile_id);
-  if (splits > 1) {
+  const TileSplit sp = gemm_nn_split(p, tile_id);
+  if (sp.splits > 1) {
     float* ws = stream_workspace(stream);  // none under stream capture: no split then
-    if (ws) p.k_splits = splits, p.partials = ws;
+    if (ws) p.k_splits = sp.splits, p.split_tiles = sp.tiles, p.partials = ws;
   }
   switch (tile_id) {
     case kTile256x256:

@@ -18,7 +18,8 @@ struct GemmProblem {
   bool c_vec4;     // set by the launcher: C 4-byte aligned (16-byte stores of C rows allowed)
   bool tail_regs;  // set by the launcher: gather the last K tile through VGPRs
   int k_splits;    // tile kernel: K ranges computed by separate workgroups (<= 1: none)
-  float* partials; // k_splits > 1: [tile][split][BM][BN] fp32 partial tiles
+  int split_tiles; // k_splits > 1: the last split_tiles tiles in dispatch order are split
+  float* partials; // k_splits > 1: [split tile][split][BM][BN] fp32 partial tiles
 };
 
 // Folded problem (the 5-D contraction descriptor, see mmm.h), with int32 extents.
@@ -37,10 +38,17 @@ enum TileId { kTile256x256 = 0, kTile128x256 = 1, kTile256x128 = 2, kTile128x128
 
 hipError_t launch_gemm_nn(const GemmProblem& p, int tile_id, hipStream_t stream);
 bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id);  // else the register-staged path
-int gemm_nn_splits(const GemmProblem& p, int tile_id);          // K splits the tile launch would use
+// K split of a tile launch: the last `tiles` tiles in dispatch order (the last, partly filled
+// round of 256 workgroups, or the whole grid when it is one small round) each run as `splits`
+// K ranges; splits == 1: none.
+struct TileSplit {
+  int splits, tiles;
+};
+TileSplit gemm_nn_split(const GemmProblem& p, int tile_id);
+int gemm_nn_splits(const GemmProblem& p, int tile_id);  // gemm_nn_split(...).splits
 // Per-(device, stream) scratch for split reductions (partial tiles), allocated on first use
 // outside stream capture; null when unavailable.  kStreamWorkspaceBytes long.
-constexpr size_t kStreamWorkspaceBytes = (size_t)32 << 20;
+constexpr size_t kStreamWorkspaceBytes = (size_t)64 << 20;
 float* stream_workspace(hipStream_t stream);
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
 // Rows of C up to which the streaming kernels take a GEMM (the kernels handle up to 64).

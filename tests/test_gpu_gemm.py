@@ -334,6 +334,33 @@ def test_stream_graph_capture(mm, cuda, rows):
         assert np.array_equal(mm.gemm(A, B).cpu().numpy(), truth)
 
 
+# (M, N, K) -> (tile, K splits, split tiles): the last round of 256 workgroups is less than half
+# full, so its tiles run as K ranges while the rest run over all of K (0 split tiles: declined,
+# the reduction would cost more than the round it saves)
+TAIL_SPLITS = [((6144, 6144, 2048), ("256x256", 4, 64)), ((3072, 3072, 3072), ("128x256", 6, 32)),
+               ((4608, 4608, 8192), ("256x256", 3, 68)), ((7168, 7168, 7168), ("256x256", 14, 16)),
+               ((4357, 4095, 4111), ("256x256", 8, 32)), ((2304, 2304, 8192), ("128x128", 3, 68)),
+               ((6150, 6144, 1030), ("256x256", 1, 0))]
+
+
+@pytest.mark.parametrize("case", TAIL_SPLITS, ids=lambda c: "x".join(map(str, c[0])))
+def test_exact_tail_split(mm, cuda, case):
+    """Whole tiles and K-split last-round tiles in one launch, then the ordered reduction: exact
+    against the on-device fp64 truth (integer inputs; every partial sum is exact), twice."""
+    (M, N, K), (tile, splits, split_tiles) = case
+    plan = mm.gemm_plan(M, N, K)
+    assert plan["kernel"] == "tile" and f"{plan['block_m']}x{plan['block_n']}" == tile
+    assert (plan["tile_splits"], plan["tile_split_tiles"]) == (splits, split_tiles)
+    g = cuda.Generator(device="cuda").manual_seed(M + N + K)
+    A = cuda.randint(-4, 5, (M, K), device="cuda", generator=g).half()
+    B = cuda.randint(-4, 5, (K, N), device="cuda", generator=g).half()
+    T, _ = mm.gemm_truth(A, B, with_scale=False)
+    for _ in range(2):
+        C = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+        mm.gemm(A, B, C)
+        assert cuda.equal(C.double(), T), f"{int((C.double() != T).sum())} mismatches"
+
+
 # (M, N, K, tile or None) -> K splits of the tile kernel
 TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((65, 4096, 4096, None), 8), ((300, 264, 2048, None), 4),
                ((100, 200, 1001, None), 2), ((256, 512, 4096, "256x256"), 8), ((256, 512, 2048, "256x128"), 4),
