@@ -197,6 +197,11 @@ def test_gemm_plan(mm):
     p = mm.gemm_plan(32, 28672, 8192)  # 224 strips fill the chip unsplit
     assert p["stream_splits"] == 1 and p["stream_workgroups"] == 224
     assert mm.gemm_plan(65, 8192, 8192)["kernel"] == "tile"
+    # under-filled last round: 576 tiles = 2 rounds + 64; those 64 run as 4 K ranges each
+    p = mm.gemm_plan(6144, 6144, 6144)
+    assert (p["block_m"], p["tile_splits"], p["tile_split_tiles"], p["tile_workgroups"]) == (256, 4, 64, 576)
+    p = mm.gemm_plan(6150, 6144, 1030)  # short K: the reduction would cost more than it saves
+    assert (p["tile_splits"], p["tile_split_tiles"]) == (1, 0)
     p = mm.gemm_plan(16 * 256 + 40, 4096, 264)  # 40 rows past 16 tile rows stream
     assert p["kernel"] == "tile+stream" and p["tile_rows"] == 4096 and p["stream_rows"] == 40
     assert mm.gemm_plan(5, 5, 0)["kernel"] == "zero"
