@@ -89,6 +89,8 @@ typedef struct mmm_gemm_plan {
     int tile_split_tiles;                  /* tiles that run as tile_splits K ranges: the last,
                                               partly filled round of 256 workgroups (all tiles
                                               when the grid is one small round); 0: none */
+    int tile_persistent;                   /* 1: 256 workgroups each loop over tiles (whole
+                                              interior tiles over several rounds) */
 } mmm_gemm_plan;
 
 /*

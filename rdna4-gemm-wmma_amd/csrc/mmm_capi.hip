@@ -365,6 +365,7 @@ hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const floa
     const TileSplit sp = gemm_nn_split(pm, pl.tile);
     plan->tile_splits = sp.splits;
     plan->tile_split_tiles = sp.splits > 1 ? sp.tiles : 0;
+    plan->tile_persistent = plan->direct_to_lds && gemm_nn_persistent(pm, pl.tile) ? 1 : 0;
   }
   if (pl.kind == MMM_KERNEL_STREAM || pl.kind == MMM_KERNEL_TILE_STREAM) {
     GemmProblem pr = p;

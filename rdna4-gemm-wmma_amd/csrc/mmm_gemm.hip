@@ -167,7 +167,9 @@ __device__ __forceinline__ void dma_b128(uint32_t lds_addr, i32x4 rsrc, uint32_t
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass checks "I" against its own (narrower) range
   asm volatile("s_waitcnt vmcnt(%0)" ::"I"(N) : "memory");
+#endif
 }
 __device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
 
@@ -279,10 +281,15 @@ __device__ __forceinline__ void block_sync() { __syncthreads(); }
 // T::LPT, and issue_tile(t, slot) fills slot `slot` with tile t by whatever means (the last
 // tile of an unaligned problem is gathered through VGPRs when tail_regs is set, which leaves
 // no loads in flight for it).
-template <class T, bool BKM, class Prep, class DmaOne, class IssueTile>
+//
+// pre = 0: the loop issues the first tiles itself.  pre = 1: the caller has issued tiles
+// 0 .. S-1 already (KT >= S).  pre = 2: as 1, and NST further vector-memory operations (the
+// previous tile's C stores) were issued after them; the first wait lets those stay
+// outstanding (vmcnt retires in issue order).
+template <class T, bool BKM, int NST = 0, class Prep, class DmaOne, class IssueTile>
 __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool tail_regs, const uint32_t (&a_off)[4],
                                             const uint32_t (&b_off)[4], AccT<T> (&acc)[T::FM][T::FN], Prep&& prep,
-                                            DmaOne&& dma_one, IssueTile&& issue_tile) {
+                                            DmaOne&& dma_one, IssueTile&& issue_tile, int pre = 0) {
   auto issue = [&](int t, int stage) {
     const auto d = prep(t, stage);
 #pragma unroll
@@ -298,9 +305,15 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
   constexpr int S = T::STAGES;
   static_assert(T::KSTEPS % 2 == 0, "fragment double buffer alternates per K-step");
   const int first = KT < S ? KT : S;
-  for (int s = 0; s < first; ++s) issue_tile(s, s);
+  if (pre == 0)
+    for (int s = 0; s < first; ++s) issue_tile(s, s);
   // tile 0 must land; later tiles may stay in flight (a gathered last tile has no loads)
-  wait_tiles<T::LPT, S - 1>(first - 1 - ((tail_regs && first == KT) ? 1 : 0));
+  if (pre == 2) {
+    static_assert((S - 1) * T::LPT + NST <= 63, "vmcnt range");
+    wait_vmcnt<(S - 1) * T::LPT + NST>();
+  } else {
+    wait_tiles<T::LPT, S - 1>(first - 1 - ((tail_regs && first == KT) ? 1 : 0));
+  }
   block_sync();
   Frags<T> f[2];
   load_frags<T, BKM>(lds_base, lds_base + T::A_BYTES, a_off, b_off, 0, f[0]);
@@ -670,6 +683,151 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         }
       }
     }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// Persistent direct-to-LDS tile kernel, for grids of whole interior tiles (M and N multiples
+// of the tile, aligned operands and C, no K split) over more than one round: grid =
+// min(tiles, 256) workgroups; workgroup b computes tiles b, b + grid, b + 2*grid, ... of the
+// XCD-aware order (grid % 8 == 0 keeps it on one XCD, walking that XCD's tile patches in
+// order).  Between two tiles it waits for every wave to finish reading the ring, issues the
+// next tile's first S K tiles, and only then stores the finished tile's C: the stores drain
+// while those loads are in flight, and the next tile's first wait lets the NST stores
+// (issued after the loads) stay outstanding, since vector-memory operations retire in issue
+// order.
+// ------------------------------------------------------------------------------------
+template <class T>
+__global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmProblem p, int tiles_m, int tiles_n) {
+  __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
+  constexpr int S = T::STAGES;
+  constexpr int NQ = T::MF == 32 ? 4 : 1;       // float4 groups per accumulator
+  constexpr int NST = T::FM * T::FN * NQ;       // C stores per thread per tile
+  const int ntiles = tiles_m * tiles_n;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / T::WGN, wn = w % T::WGN;
+  const int K = p.K;
+  const int64_t lda = p.lda, ldb = p.ldb;
+
+  // staging map and fragment offsets: as gemm_nn_kernel
+  constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
+  static_assert(RPA % T::SWZ_A_ROWS == 0 && RPB % T::SWZ_B_ROWS == 0, "round strides must preserve the swizzle");
+  const int a_row0 = w * (64 / T::CA) + lane / T::CA;
+  const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
+  const int b_row0 = w * (64 / T::CB) + lane / T::CB;
+  const int b_nc = 8 * ((lane % T::CB) ^ T::swz_bk(b_row0));
+  uint32_t a_off[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int kk = 0; kk < T::KSTEPS; ++kk)
+#pragma unroll
+    for (int ph = 0; ph < T::APAR; ++ph) {
+      const int m = wm * T::TM + ph * T::MF + (lane % T::MF);
+      const int chunk = (T::KK / 8) * kk + lane / T::MF;
+      a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
+    }
+  uint32_t b_off[4] = {0, 0, 0, 0};
+  {
+    const int k = 8 * (lane / T::MF) + ((lane >> 2) & 3);
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb) {
+      const int n = T::MF == 32 ? wn * T::TN + 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)
+                                : wn * T::TN + 16 * nb + 4 * (lane & 3);
+      b_off[nb] = k * T::BN * 2 + (((n >> 3) ^ T::swz_bk(k)) * 16) + (n & 7) * 2;
+    }
+  }
+
+  const int KT = (K + T::BK - 1) / T::BK;
+  char LDS_AS* lds_base = (char LDS_AS*)lds;
+  int a_kc_t = a_kc;  // a_kc for the K-tail test, made opaque per tile like the offset bases
+  uint32_t a_goff = (uint32_t)((a_row0 * lda + a_kc) * 2);
+  uint32_t b_goff = (uint32_t)((b_row0 * ldb + b_nc) * 2);
+  const uint32_t a_rstep = (uint32_t)(RPA * lda * 2), b_rstep = (uint32_t)(RPB * ldb * 2);
+  const int64_t b_step = (int64_t)T::BK * ldb * 2;
+  // per-tile running load state (K tiles are prepared in order from 0)
+  const char* a_ptr;
+  const char* b_ptr;
+  int64_t a_left, b_left;
+  auto start_tile = [&](int tm0, int tn0) {
+    // The per-lane offset bases pass through an empty asm each tile, so the offsets of a tile's
+    // first loads are recomputed from them rather than kept live across the K loop (which
+    // runs at the register limit).
+    asm volatile("" : "+v"(a_goff), "+v"(b_goff), "+v"(a_kc_t));
+    a_ptr = (const char*)(p.A + (int64_t)tm0 * lda);
+    b_ptr = (const char*)(p.B + tn0);
+    a_left = ((int64_t)(p.M - 1 - tm0) * lda + K) * 2;
+    b_left = ((int64_t)(K - 1) * ldb + p.N - tn0) * 2;
+  };
+  struct TileDma {
+    i32x4 ra, rb;
+    uint32_t a_dst, b_dst, a_base;
+  };
+  auto prep = [&](int t, int stage) {
+    const int k0 = t * T::BK;
+    TileDma d;
+    d.ra = make_rsrc(a_ptr, clip_records(a_left));
+    d.rb = make_rsrc(b_ptr, clip_records(b_left));
+    a_ptr += T::BK * 2, a_left -= T::BK * 2;
+    b_ptr += b_step, b_left -= b_step;
+    d.a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
+    d.b_dst = d.a_dst + T::A_BYTES;
+    const uint32_t a_dead = (uint32_t)(K - 1 - (k0 + a_kc_t)) >> 31;
+    d.a_base = a_goff + a_dead * kOobOffset;
+    return d;
+  };
+  auto dma_one = [&](const TileDma& d, int j) {
+    if (j < T::RA)
+      dma_b128(d.a_dst + j * T::NT * 16, d.ra, d.a_base + j * a_rstep);
+    else
+      dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, d.rb, b_goff + (j - T::RA) * b_rstep);
+  };
+  auto issue = [&](int t, int stage) {
+    const TileDma d = prep(t, stage);
+#pragma unroll
+    for (int j = 0; j < T::LPT; ++j) dma_one(d, j);
+  };
+
+  int b = blockIdx.x;
+  int tm, tn;
+  tile_of_block(b, tiles_m, tiles_n, 4, &tm, &tn);
+  int m0 = __builtin_amdgcn_readfirstlane(tm * T::BM), n0 = __builtin_amdgcn_readfirstlane(tn * T::BN);
+  start_tile(m0, n0);
+#pragma unroll
+  for (int s = 0; s < S; ++s) issue(s, s);
+  int pre = 1;
+  AccT<T> acc[T::FM][T::FN];
+  while (true) {
+#pragma unroll
+    for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < T::FN; ++jj) acc[i][jj] = AccT<T>{};
+    cross_stage<T, false, NST>(lds_base, KT, false, a_off, b_off, acc, prep, dma_one, issue, pre);
+    const int nb = b + (int)gridDim.x;
+    int nm0 = 0, nn0 = 0;
+    if (nb < ntiles) {
+      block_sync();  // every wave has read its last fragments of the ring
+      tile_of_block(nb, tiles_m, tiles_n, 4, &tm, &tn);
+      nm0 = __builtin_amdgcn_readfirstlane(tm * T::BM), nn0 = __builtin_amdgcn_readfirstlane(tn * T::BN);
+      start_tile(nm0, nn0);
+#pragma unroll
+      for (int s = 0; s < S; ++s) issue(s, s);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before the stores below
+    }
+    // epilogue: interior tile, NST 16-byte stores per thread
+#pragma unroll
+    for (int mb = 0; mb < T::FM; ++mb) {
+      float* crow = p.C + (int64_t)(m0 + wm * T::TM + T::MF * mb + (lane % T::MF)) * p.ldc + n0 + wn * T::TN;
+#pragma unroll
+      for (int nb2 = 0; nb2 < T::FN; ++nb2)
+#pragma unroll
+        for (int qq = 0; qq < NQ; ++qq) {
+          const int n = T::MF == 32 ? 32 * nb2 + 8 * qq + 4 * (lane >> 5) : 16 * nb2 + 4 * (lane >> 4);
+          *(f32x4*)(crow + n) = f32x4{acc[mb][nb2][4 * qq + 0], acc[mb][nb2][4 * qq + 1], acc[mb][nb2][4 * qq + 2],
+                                      acc[mb][nb2][4 * qq + 3]};
+        }
+    }
+    if (nb >= ntiles) break;
+    b = nb, m0 = nm0, n0 = nn0, pre = 2;
   }
 }
 
@@ -1130,6 +1288,30 @@ TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
 
 int gemm_nn_splits(const GemmProblem& p, int tile_id) { return gemm_nn_split(p, tile_id).splits; }
 
+// The persistent kernel's conditions: whole interior 256x256 tiles over more than one round of
+// 256 workgroups, aligned operands (no gathered K tile), 4-byte-aligned C, no K split, and at
+// least S + 1 K tiles.  Measured against one workgroup per tile (same box): 8192^3 +1%,
+// 8192^2 x 2048 +3.7%, 16384 x 8192 x 1024 +3.8%.
+#ifndef MMM_PERSIST
+#define MMM_PERSIST 1
+#endif
+static bool persistent_ok(const GemmProblem& p) {
+  using TP = DmaTile<256, 256>;
+  if (!dma_ok(p, 256) || p.tail_regs || !p.c_vec4 || p.k_splits > 1) return false;
+  if (p.M % TP::BM || p.N % TP::BN) return false;
+  if ((int64_t)(p.M / TP::BM) * (p.N / TP::BN) <= 256) return false;
+  return (p.K + TP::BK - 1) / TP::BK >= TP::STAGES + 1;
+}
+
+bool gemm_nn_persistent(const GemmProblem& p0, int tile_id) {
+  if (!MMM_PERSIST || tile_id != kTile256x256) return false;
+  GemmProblem p = p0;
+  p.c_vec4 = (uintptr_t)p.C % 4 == 0;
+  p.tail_regs = !tail_aligned(p);
+  p.k_splits = gemm_nn_split(p, tile_id).splits;
+  return persistent_ok(p);
+}
+
 hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream) {
   GemmProblem p = p0;
   // 16-byte stores of C need only 4-byte alignment on gfx950 (rows of an odd ldc included)
@@ -1145,6 +1327,12 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
   }
   switch (tile_id) {
     case kTile256x256:
+      if (MMM_PERSIST && persistent_ok(p)) {
+        using TP = DmaTile<256, 256>;
+        hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP>), dim3(256), dim3(TP::NT), 0, stream, p, p.M / TP::BM,
+                           p.N / TP::BN);
+        return hipGetLastError();
+      }
       return dma_ok(p, 256) ? launch_nn<DmaTile<256, 256>, false>(p, stream)
                             : launch_nn<RegTile<256, 256>, true>(p, stream);
     case kTile128x256:

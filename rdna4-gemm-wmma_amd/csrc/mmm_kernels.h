@@ -46,6 +46,7 @@ struct TileSplit {
 };
 TileSplit gemm_nn_split(const GemmProblem& p, int tile_id);
 int gemm_nn_splits(const GemmProblem& p, int tile_id);  // gemm_nn_split(...).splits
+bool gemm_nn_persistent(const GemmProblem& p, int tile_id);  // launch as the persistent kernel
 // Per-(device, stream) scratch for split reductions (partial tiles), allocated on first use
 // outside stream capture; null when unavailable.  kStreamWorkspaceBytes long.
 constexpr size_t kStreamWorkspaceBytes = (size_t)64 << 20;

@@ -334,6 +334,32 @@ def test_stream_graph_capture(mm, cuda, rows):
         assert np.array_equal(mm.gemm(A, B).cpu().numpy(), truth)
 
 
+# (M, N, K, C row padding): whole interior 256x256 tiles over several rounds run on the persistent
+# kernel (256 workgroups looping over tiles, next tile's loads issued before this tile's stores)
+PERSISTENT = [(8192, 8192, 8192, 0), (8192, 8192, 2048, 0), (4608, 4096, 192, 0), (2560, 16384, 1024, 0),
+              (4608, 4096, 576, 3)]
+
+
+@pytest.mark.parametrize("case", PERSISTENT, ids=lambda c: "x".join(map(str, c[:3])) + f"-pad{c[3]}")
+def test_exact_persistent(mm, cuda, case):
+    """The persistent tile kernel: exact against the on-device fp64 truth (integer inputs), three
+    calls in a row, with a padded C row stride in one case."""
+    M, N, K, pad = case
+    plan = mm.gemm_plan(M, N, K, ldc=N + pad)
+    assert plan["kernel"] == "tile" and plan["tile_persistent"] == 1
+    g = cuda.Generator(device="cuda").manual_seed(M + N + K + pad)
+    A = cuda.randint(-4, 5, (M, K), device="cuda", generator=g).half()
+    B = cuda.randint(-4, 5, (K, N), device="cuda", generator=g).half()
+    T, _ = mm.gemm_truth(A, B, with_scale=False)
+    for _ in range(3):
+        Cbuf = cuda.full((M, N + pad), float("nan"), dtype=cuda.float32, device="cuda")
+        C = Cbuf[:, :N]
+        mm.gemm(A, B, C)
+        assert cuda.equal(C.double(), T), f"{int((C.double() != T).sum())} mismatches"
+        if pad:
+            assert bool(cuda.isnan(Cbuf[:, N:]).all()), "wrote past the row"
+
+
 # (M, N, K) -> (tile, K splits, split tiles): the last round of 256 workgroups is less than half
 # full, so its tiles run as K ranges while the rest run over all of K (0 split tiles: declined,
 # the reduction would cost more than the round it saves)

@@ -180,6 +180,8 @@ def test_gemm_plan(mm):
     """The launch the library chooses, queried without a GPU (mmm_gemm_plan_f16f32)."""
     p = mm.gemm_plan(8192, 8192, 8192)
     assert p["kernel"] == "tile" and (p["block_m"], p["block_n"]) == (256, 256)
+    assert p["tile_persistent"] == 1  # 1024 whole tiles: 256 workgroups loop over 4 each
+    assert mm.gemm_plan(4096, 4096, 4096)["tile_persistent"] == 0  # one round
     assert p["direct_to_lds"] == 1 and p["tile_workgroups"] == 32 * 32 and p["stream_rows"] == 0
     p = mm.gemm_plan(4097, 4095, 4111)  # one row past 16 tile rows: that row streams
     assert p["kernel"] == "tile+stream" and p["tile_rows"] == 4096 and p["stream_rows"] == 1
