@@ -13,13 +13,13 @@
  *
  * Conventions (all entry points):
  *  - fp16 tensors are passed as pointers to IEEE binary16 bit patterns (mmm_half).
- *  - Pointers are device pointers owned by the caller.  No entry point synchronises the host
- *    or exits the process.  The only device memory the library allocates is the workspace
- *    of its K splits (launches that would leave most of the chip idle split K across
- *    workgroups and sum the partials in a fixed order): 64 MiB per (device, stream), on the
- *    first split call on that stream, kept until the process exits.  A call made while its
- *    stream is being captured into a graph never allocates: without a workspace it runs
- *    unsplit (the streaming kernel's variant gives the same results bit for bit).
+ *  - Pointers are device pointers owned by the caller.  No entry point synchronises the host,
+ *    exits the process or allocates memory.  Launches that would leave most of the chip idle
+ *    split K across workgroups and sum the partials in a fixed order; the partials go to a
+ *    workspace the caller passes to the _ws entry points (size from mmm_gemm_workspace_f16f32
+ *    or mmm_contract5d_workspace_f16f32, at most 64 MiB).  Without one (the entry points
+ *    without _ws, a null or too small workspace) the unsplit kernels run; results agree
+ *    within rounding (the summation order differs).  Each choice is deterministic.
  *  - C is overwritten (alpha = 1, beta = 0, as mmm.cpp:1512-1513 and the kernel's store at
  *    mmm.cpp:1370); C is never read.
  *  - Errors: hipErrorInvalidValue for null pointers, negative sizes or leading dimensions
@@ -27,13 +27,14 @@
  *    M == 0 or N == 0 is a no-op; K == 0 writes zeros to C.
  *  - Work is enqueued on `stream` (0 = the null stream, as the reference) and is
  *    asynchronous, as the reference's launches are (the caller synchronises, mmm.cpp:1491).
- *  - Thread safety: the only mutable global state is the workspace table, guarded by a
- *    mutex.  Calls on one stream are ordered and share its workspace; different streams
- *    never share one.
+ *  - Thread safety: the library has no mutable global state.  A workspace serves one call at
+ *    a time: calls on one stream may share one (they are ordered); concurrent calls on
+ *    different streams need their own.
  */
 #ifndef MMM_H
 #define MMM_H
 
+#include <stddef.h>
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
@@ -55,6 +56,25 @@ hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M
                            int64_t ldb, int64_t ldc, hipStream_t stream);
 
 /*
+ * As mmm_gemm_f16f32, with a caller-provided workspace for the K-split partial sums
+ * (16-byte aligned; NULL allowed).  When workspace_bytes is at least what
+ * mmm_gemm_workspace_f16f32 reports, shapes that would leave most of the chip idle (M <= 64,
+ * small grids, an under-filled last round of tiles) split K across workgroups; otherwise they
+ * run unsplit.  No reference counterpart: the reference's kernel never splits K and
+ * allocates nothing (mmm.cpp:1214-1374).
+ */
+hipError_t mmm_gemm_f16f32_ws(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                              int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Workspace bytes mmm_gemm_f16f32_ws needs for these arguments (0: it would not split).
+ * Host only, no GPU call; A, B, C only for their alignment and may be NULL (taken as
+ * 256-byte aligned).  No reference counterpart (see mmm_gemm_f16f32_ws).
+ */
+hipError_t mmm_gemm_workspace_f16f32(const mmm_half* A, const mmm_half* B, const float* C, int M, int N, int K,
+                                     int64_t lda, int64_t ldb, int64_t ldc, size_t* bytes);
+
+/*
  * As mmm_gemm_f16f32, with the tile shape chosen by the caller through the reference's
  * template parameters (mmm.cpp:694-695, 1462-1465), reinterpreted for wave64 MFMA:
  *   WAVE_M, WAVE_N   -- 32x32 MFMA tiles per wave along M and N (the reference counts
@@ -62,11 +82,12 @@ hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M
  *   WAVES_I, WAVES_J -- waves per workgroup along M and N.
  * Block tile = (WAVES_I*WAVE_M*32) x (WAVES_J*WAVE_N*32), K step 64.
  * Instantiated shapes (WAVE_M,WAVE_N,WAVES_I,WAVES_J): (4,4,2,2) 256x256, (2,4,2,2) 128x256,
- * (4,2,2,2) 256x128, (2,2,2,2) 128x128.  Others return hipErrorInvalidValue.
+ * (4,2,2,2) 256x128, (2,2,2,2) 128x128.  Others return hipErrorInvalidValue.  The workspace
+ * (NULL allowed) serves the tile's K split as in mmm_gemm_f16f32_ws.
  */
 hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
                                  int64_t lda, int64_t ldb, int64_t ldc, int wave_m, int wave_n, int waves_i,
-                                 int waves_j, hipStream_t stream);
+                                 int waves_j, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Kernels mmm_gemm_f16f32 can launch (mmm_gemm_plan.kernel). */
 #define MMM_KERNEL_NONE 0        /* M == 0 or N == 0: nothing */
@@ -91,6 +112,8 @@ typedef struct mmm_gemm_plan {
                                               when the grid is one small round); 0: none */
     int tile_persistent;                   /* 1: 256 workgroups each loop over tiles (whole
                                               interior tiles over several rounds) */
+    int64_t workspace_bytes;               /* workspace the splits need (mmm_gemm_f16f32_ws);
+                                              the split counts above assume it is given */
 } mmm_gemm_plan;
 
 /*
@@ -143,6 +166,17 @@ hipError_t mmm_contract_desc_reference(mmm_contract_desc* d, int mt, int bt, int
  */
 hipError_t mmm_contract5d_f16f32(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
                                  hipStream_t stream);
+
+/*
+ * As mmm_contract5d_f16f32, with a caller-provided workspace (as mmm_gemm_f16f32_ws; a fold
+ * that is a plain row-major GEMM runs on the GEMM kernels and may split K), and the bytes it
+ * needs (host only; pointers only for alignment, may be NULL).  No reference counterpart
+ * (the reference's tensor kernel never splits K, mmmTensor.cpp:44-257).
+ */
+hipError_t mmm_contract5d_f16f32_ws(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
+                                    void* workspace, size_t workspace_bytes, hipStream_t stream);
+hipError_t mmm_contract5d_workspace_f16f32(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B,
+                                           const float* C, size_t* bytes);
 
 /*
  * On-device cross-check: the reference's GEMM_Naive (mmm.cpp:52-62) with run-time sizes and

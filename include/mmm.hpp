@@ -26,15 +26,17 @@ inline hipError_t WMMA_Swizzled_Full(const mmm_half* A, const mmm_half* B, float
   constexpr int wm = BLOCK_M / 64, wn = BLOCK_N / 64;
   constexpr bool have = (BLOCK_M == 128 || BLOCK_M == 256) && (BLOCK_N == 128 || BLOCK_N == 256);
   if constexpr (have)
-    return mmm_gemm_f16f32_tiled(A, B, C, DIM_I, DIM_J, DIM_K, DIM_K, DIM_J, DIM_J, wm, wn, 2, 2, stream);
+    return mmm_gemm_f16f32_tiled(A, B, C, DIM_I, DIM_J, DIM_K, DIM_K, DIM_J, DIM_J, wm, wn, 2, 2, nullptr, 0, stream);
   else
     return mmm_gemm_f16f32(A, B, C, DIM_I, DIM_J, DIM_K, DIM_K, DIM_J, DIM_J, stream);
 }
 
-// Library-chosen tile (recommended: includes the M <= 16 streaming kernel).
+// Library-chosen kernel (recommended: includes the M <= 64 streaming kernel).  With a workspace
+// of mmm_gemm_workspace_f16f32's size, under-filled launches split K (mmm_gemm_f16f32_ws).
 inline hipError_t WMMA_Auto(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
-                            int64_t ldb, int64_t ldc, hipStream_t stream = nullptr) {
-  return mmm_gemm_f16f32(A, B, C, M, N, K, lda, ldb, ldc, stream);
+                            int64_t ldb, int64_t ldc, hipStream_t stream = nullptr, void* workspace = nullptr,
+                            size_t workspace_bytes = 0) {
+  return mmm_gemm_f16f32_ws(A, B, C, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, stream);
 }
 
 // The reference's tensor program (mmmTensor.cpp): Out[m][b][r] = sum_{n,l} G[r][n][m][l] *

@@ -4,43 +4,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <cmath>
-#include <map>
-#include <mutex>
-#include <utility>
 
 #include "mmm.h"
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
 
 namespace mmm {
-
-// ---------------------------------------------------------------- split-reduction workspace
-// One workspace per (device, stream), allocated on first use outside stream capture and kept
-// until the process exits.  Calls on one stream are ordered, so they share its workspace
-// safely (a split launch and its reduction finish before the next call's kernels start);
-// different streams never share one.  Nothing in it needs initialising: every partial a
-// reduction reads is written by the launch before it.
-static std::mutex g_ws_mu;
-static std::map<std::pair<int, uintptr_t>, float*> g_ws;
-
-float* stream_workspace(hipStream_t stream) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  const auto key = std::make_pair(dev, (uintptr_t)stream);
-  const auto it = g_ws.find(key);
-  if (it != g_ws.end()) return it->second;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-  void* mem = nullptr;
-  if (hipMalloc(&mem, kStreamWorkspaceBytes) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  g_ws[key] = (float*)mem;
-  return (float*)mem;
-}
 
 // ---------------------------------------------------------------- seeded input generator
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
@@ -304,6 +275,43 @@ static FoldProblem fold_of_gemm(const mmm_half* A, const mmm_half* B, float* C, 
   return p;
 }
 
+// Workspace bytes the planned launch's K splits need (0: none).  The tile and streaming
+// kernels of a tile+stream plan run one after the other on the stream, so they share it.
+static size_t plan_workspace_bytes(const GemmProblem& p, const GemmPlan& pl) {
+  size_t need = 0;
+  if (pl.kind == MMM_KERNEL_TILE || pl.kind == MMM_KERNEL_TILE_STREAM) {
+    GemmProblem pm = p;
+    pm.M = pl.tile_rows;
+    need = std::max(need, gemm_nn_workspace_bytes(pm, pl.tile));
+  }
+  if (pl.kind == MMM_KERNEL_STREAM || pl.kind == MMM_KERNEL_TILE_STREAM) {
+    GemmProblem pr = p;
+    pr.M = p.M - pl.tile_rows;
+    pr.A = p.A + (int64_t)pl.tile_rows * p.lda;
+    need = std::max(need, skinny_workspace_bytes(pr));
+  }
+  return need;
+}
+
+// A caller's workspace is optional (null: the unsplit kernels run) and 16-byte aligned (the
+// reductions read it as float4).
+static hipError_t check_workspace(const void* ws) {
+  return ((uintptr_t)ws & 15) ? hipErrorInvalidValue : hipSuccess;
+}
+
+// A fold that is a plain row-major GEMM (every pair of sub-indices collapses to one stride,
+// unit along K for A and along N for B and C): its leading dimensions.
+static bool plain_gemm(const mmm_contract_desc* d, int64_t K, int64_t N, int64_t* lda, int64_t* ldb, int64_t* ldc) {
+  int64_t ak, bn, cn;
+  return collapse(d->m_ext[0], d->m_ext[1], d->a_m_stride[0], d->a_m_stride[1], lda) &&
+         collapse(d->k_ext[0], d->k_ext[1], d->a_k_stride[0], d->a_k_stride[1], &ak) && ak == 1 &&
+         collapse(d->k_ext[0], d->k_ext[1], d->b_k_stride[0], d->b_k_stride[1], ldb) &&
+         collapse(d->n_ext[0], d->n_ext[1], d->b_n_stride[0], d->b_n_stride[1], &bn) && bn == 1 &&
+         collapse(d->m_ext[0], d->m_ext[1], d->c_m_stride[0], d->c_m_stride[1], ldc) &&
+         collapse(d->n_ext[0], d->n_ext[1], d->c_n_stride[0], d->c_n_stride[1], &cn) && cn == 1 && *lda >= K &&
+         *ldb >= N && *ldc >= N;
+}
+
 }  // namespace mmm
 
 using namespace mmm;
@@ -312,9 +320,17 @@ extern "C" {
 
 hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
                            int64_t ldb, int64_t ldc, hipStream_t stream) {
+  return mmm_gemm_f16f32_ws(A, B, C, M, N, K, lda, ldb, ldc, nullptr, 0, stream);
+}
+
+hipError_t mmm_gemm_f16f32_ws(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
+                              int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
   if (e != hipSuccess) return e;
-  const GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
+  if ((e = check_workspace(workspace)) != hipSuccess) return e;
+  GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
+  p.ws = (float*)workspace;
+  p.ws_bytes = workspace ? workspace_bytes : 0;
   const GemmPlan pl = plan_gemm(p);
   switch (pl.kind) {
     case MMM_KERNEL_NONE:
@@ -374,18 +390,31 @@ hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const floa
     plan->stream_workgroups = skinny_workgroups(pr);
     plan->stream_splits = skinny_splits(pr);
   }
+  plan->workspace_bytes = (int64_t)plan_workspace_bytes(p, pl);
   return hipSuccess;
+}
+
+hipError_t mmm_gemm_workspace_f16f32(const mmm_half* A, const mmm_half* B, const float* C, int M, int N, int K,
+                                     int64_t lda, int64_t ldb, int64_t ldc, size_t* bytes) {
+  if (!bytes) return hipErrorInvalidValue;
+  mmm_gemm_plan plan;
+  const hipError_t e = mmm_gemm_plan_f16f32(A, B, C, M, N, K, lda, ldb, ldc, &plan);
+  *bytes = e == hipSuccess ? (size_t)plan.workspace_bytes : 0;
+  return e;
 }
 
 hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
                                  int64_t lda, int64_t ldb, int64_t ldc, int wave_m, int wave_n, int waves_i,
-                                 int waves_j, hipStream_t stream) {
+                                 int waves_j, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const int tile = tile_from_params(wave_m, wave_n, waves_i, waves_j);
   if (tile < 0) return hipErrorInvalidValue;
   hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
   if (e != hipSuccess || M == 0 || N == 0) return e;
+  if ((e = check_workspace(workspace)) != hipSuccess) return e;
   if (K == 0) return launch_zero_f32(C, M, N, ldc, stream);
   GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
+  p.ws = (float*)workspace;
+  p.ws_bytes = workspace ? workspace_bytes : 0;
   return launch_gemm_nn(p, tile, stream);
 }
 
@@ -425,25 +454,39 @@ hipError_t mmm_contract_desc_reference(mmm_contract_desc* d, int mt, int bt, int
 
 hipError_t mmm_contract5d_f16f32(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
                                  hipStream_t stream) {
+  return mmm_contract5d_f16f32_ws(d, A, B, C, nullptr, 0, stream);
+}
+
+hipError_t mmm_contract5d_f16f32_ws(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
+                                    void* workspace, size_t workspace_bytes, hipStream_t stream) {
   FoldProblem p{};
   hipError_t e = fold_from_desc(d, A, B, C, &p);
   if (e != hipSuccess || p.M == 0 || p.N == 0) return e;
   if (!C) return hipErrorInvalidValue;
-  const int64_t M = p.M, N = p.N, K = p.K;
-
+  if ((e = check_workspace(workspace)) != hipSuccess) return e;
   // A fold that is a plain row-major GEMM runs on the GEMM kernels (the benchmark's
   // A[b,i,k,l] x B[k,l,j] -> C[b,i,j] is one: M = b*i, K = k*l, N = j).
-  int64_t am, ak, bk, bn, cm, cn;
-  const bool plain = collapse(d->m_ext[0], d->m_ext[1], d->a_m_stride[0], d->a_m_stride[1], &am) &&
-                     collapse(d->k_ext[0], d->k_ext[1], d->a_k_stride[0], d->a_k_stride[1], &ak) && ak == 1 &&
-                     collapse(d->k_ext[0], d->k_ext[1], d->b_k_stride[0], d->b_k_stride[1], &bk) &&
-                     collapse(d->n_ext[0], d->n_ext[1], d->b_n_stride[0], d->b_n_stride[1], &bn) && bn == 1 &&
-                     collapse(d->m_ext[0], d->m_ext[1], d->c_m_stride[0], d->c_m_stride[1], &cm) &&
-                     collapse(d->n_ext[0], d->n_ext[1], d->c_n_stride[0], d->c_n_stride[1], &cn) && cn == 1 &&
-                     am >= K && bk >= N && cm >= N;
-  if (plain) return mmm_gemm_f16f32(A, B, C, (int)M, (int)N, (int)K, am, bk, cm, stream);
-  if (K == 0) return launch_zero_fold(p, stream);
-  return launch_gemm_fold(p, stream);
+  int64_t lda, ldb, ldc;
+  if (plain_gemm(d, p.K, p.N, &lda, &ldb, &ldc))
+    return mmm_gemm_f16f32_ws(A, B, C, p.M, p.N, p.K, lda, ldb, ldc, workspace, workspace_bytes, stream);
+  if (p.K == 0) return launch_zero_fold(p, stream);
+  return launch_gemm_fold(p, stream);  // the folded kernels split nothing: no workspace
+}
+
+hipError_t mmm_contract5d_workspace_f16f32(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B,
+                                           const float* C, size_t* bytes) {
+  if (!bytes) return hipErrorInvalidValue;
+  *bytes = 0;
+  FoldProblem p{};
+  // only alignment matters here; null stands for a 256-byte-aligned buffer
+  const mmm_half* a = A ? A : (const mmm_half*)(uintptr_t)256;
+  const mmm_half* b = B ? B : (const mmm_half*)(uintptr_t)256;
+  float* c = C ? (float*)C : (float*)(uintptr_t)256;
+  hipError_t e = fold_from_desc(d, a, b, c, &p);
+  if (e != hipSuccess || p.M == 0 || p.N == 0) return e;
+  int64_t lda, ldb, ldc;
+  if (!plain_gemm(d, p.K, p.N, &lda, &ldb, &ldc)) return hipSuccess;
+  return mmm_gemm_workspace_f16f32(a, b, c, p.M, p.N, p.K, lda, ldb, ldc, bytes);
 }
 
 hipError_t mmm_gemm_naive_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,

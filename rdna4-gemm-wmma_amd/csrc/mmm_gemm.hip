@@ -1274,7 +1274,7 @@ TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
   int64_t splits = 256 / last;
   if (splits > kt / 8) splits = kt / 8;
   if (splits > 16) splits = 16;
-  const int64_t cap = (int64_t)(kStreamWorkspaceBytes / ((size_t)bm * bn * 4)) / last;
+  const int64_t cap = (int64_t)(kMaxWorkspaceBytes / ((size_t)bm * bn * 4)) / last;
   if (splits > cap) splits = cap;
   if (splits < 2) return {1, 0};
   // one tile's round at 4.8 TFLOP/s per CU (the 256x256 tile at 8192^3; smaller tiles run
@@ -1287,6 +1287,14 @@ TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
 }
 
 int gemm_nn_splits(const GemmProblem& p, int tile_id) { return gemm_nn_split(p, tile_id).splits; }
+
+size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id) {
+  const TileSplit sp = gemm_nn_split(p, tile_id);
+  if (sp.splits < 2) return 0;
+  const size_t bm = tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128;
+  const size_t bn = tile_id == kTile256x256 || tile_id == kTile128x256 ? 256 : 128;
+  return (size_t)sp.tiles * sp.splits * bm * bn * 4;
+}
 
 // The persistent kernel's conditions: whole interior 256x256 tiles over more than one round of
 // 256 workgroups, aligned operands (no gathered K tile), 4-byte-aligned C, no K split, and at
@@ -1321,10 +1329,8 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
   p.split_tiles = 0;
   p.partials = nullptr;
   const TileSplit sp = gemm_nn_split(p, tile_id);
-  if (sp.splits > 1) {
-    float* ws = stream_workspace(stream);  // none under stream capture: no split then
-    if (ws) p.k_splits = sp.splits, p.split_tiles = sp.tiles, p.partials = ws;
-  }
+  if (sp.splits > 1 && p.ws && p.ws_bytes >= gemm_nn_workspace_bytes(p, tile_id))
+    p.k_splits = sp.splits, p.split_tiles = sp.tiles, p.partials = p.ws;  // else unsplit
   switch (tile_id) {
     case kTile256x256:
       if (MMM_PERSIST && persistent_ok(p)) {

@@ -20,6 +20,8 @@ struct GemmProblem {
   int k_splits;    // tile kernel: K ranges computed by separate workgroups (<= 1: none)
   int split_tiles; // k_splits > 1: the last split_tiles tiles in dispatch order are split
   float* partials; // k_splits > 1: [split tile][split][BM][BN] fp32 partial tiles
+  float* ws;       // caller's workspace for K splits (16-byte aligned), or null: no split
+  size_t ws_bytes; // its size
 };
 
 // Folded problem (the 5-D contraction descriptor, see mmm.h), with int32 extents.
@@ -47,10 +49,11 @@ struct TileSplit {
 TileSplit gemm_nn_split(const GemmProblem& p, int tile_id);
 int gemm_nn_splits(const GemmProblem& p, int tile_id);  // gemm_nn_split(...).splits
 bool gemm_nn_persistent(const GemmProblem& p, int tile_id);  // launch as the persistent kernel
-// Per-(device, stream) scratch for split reductions (partial tiles), allocated on first use
-// outside stream capture; null when unavailable.  kStreamWorkspaceBytes long.
-constexpr size_t kStreamWorkspaceBytes = (size_t)64 << 20;
-float* stream_workspace(hipStream_t stream);
+// Workspace bytes a tile launch's K split needs (0: no split).  Launches split only when the
+// caller's workspace (GemmProblem::ws) holds that much; splits are planned within
+// kMaxWorkspaceBytes.
+size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id);
+constexpr size_t kMaxWorkspaceBytes = (size_t)64 << 20;
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
 // Rows of C up to which the streaming kernels take a GEMM (the kernels handle up to 64).
 #ifndef MMM_STREAM_MAX_ROWS
@@ -62,6 +65,7 @@ bool skinny_ok(const GemmProblem& p);  // M <= kStreamMaxRows and operands withi
 hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);
 int skinny_workgroups(const GemmProblem& p);
 int skinny_splits(const GemmProblem& p);  // K ranges reduced across workgroups (0: within one)
+size_t skinny_workspace_bytes(const GemmProblem& p);  // workspace its split needs (0: none)
 hipError_t launch_fill_uniform(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream);
 hipError_t launch_fill_normal(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, double scale,
                               hipStream_t stream);

@@ -5,7 +5,7 @@
 //    strip and K range; every wave streams the strip's full 256-byte rows of B over its quarter
 //    of the range; K partials summed through LDS, K ranges across workgroups summed by
 //    reduce_splits_kernel in a fixed order.
-//  * gemm_skinny_kernel (M <= 16 with no workspace, e.g. under graph capture): one workgroup per
+//  * gemm_skinny_kernel (M <= 16 without a caller workspace): one workgroup per
 //    32-column strip, XCD-contiguous; the four waves split K; partials summed through LDS.
 //
 // Common to both: each wave streams through its own LDS ring with direct-to-LDS buffer loads
@@ -505,8 +505,8 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
 // M <= 16 with one split and fewer than 128 strips the wave-split kernel (32-column strips,
 // four times the workgroups) runs instead; for 16 < M <= 64 the split kernel runs with one
 // split when no workspace is to be had.
-constexpr int kWsTiles = 512;  // partial tiles of up to 64 x 128 fp32 (16 MiB of the stream workspace)
-static_assert((size_t)kWsTiles * 64 * 128 * 4 <= kStreamWorkspaceBytes, "partials must fit the workspace");
+constexpr int kWsTiles = 512;  // partial tiles of up to 64 x 128 fp32 (16 MiB of workspace)
+static_assert((size_t)kWsTiles * 64 * 128 * 4 <= kMaxWorkspaceBytes, "partials must fit the workspace");
 
 struct StreamShape {
   int mr;              // 16-row groups of the split kernel (1, 2, 4)
@@ -529,6 +529,11 @@ static StreamShape stream_shape(const GemmProblem& p) {
 }
 
 int skinny_splits(const GemmProblem& p) { return stream_shape(p).splits; }
+
+size_t skinny_workspace_bytes(const GemmProblem& p) {
+  const StreamShape sh = stream_shape(p);
+  return sh.splits > 1 ? (size_t)sh.strips * sh.splits * (16 * sh.mr) * 128 * 4 : 0;
+}
 
 int skinny_workgroups(const GemmProblem& p) {
   const StreamShape sh = stream_shape(p);
@@ -561,7 +566,7 @@ hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   p.tail_regs = (a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8;
   StreamShape sh = stream_shape(p);
-  float* ws = sh.splits > 1 ? stream_workspace(stream) : nullptr;
+  float* ws = sh.splits > 1 && p.ws && p.ws_bytes >= skinny_workspace_bytes(p) ? p.ws : nullptr;
   if (sh.splits > 1 && !ws && sh.mr > 1) sh.splits = 1;  // no workspace: one split
   if (sh.splits == 1 || ws) {
     switch (sh.mr) {
@@ -573,8 +578,7 @@ hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
         return launch_wide<4>(p, sh.strips, sh.splits, ws, stream);
     }
   }
-  // wave-split kernel (M <= 16): no workspace (also the path under stream capture before a
-  // workspace exists)
+  // wave-split kernel (M <= 16): no caller workspace
   const int strips = (p.N + kNS - 1) / kNS;
   hipLaunchKernelGGL(gemm_skinny_kernel, dim3(strips), dim3(256), 0, stream, p, strips);
   return hipGetLastError();

@@ -12,6 +12,7 @@ tensor variant mmmTensor.cpp:44-45): device pointers, M/N/K, tile parameters.
 from __future__ import annotations
 
 import ctypes as C
+import threading
 import os
 import re
 
@@ -51,7 +52,7 @@ class GemmPlan(C.Structure):
                 ("waves_j", C.c_int), ("block_m", C.c_int), ("block_n", C.c_int), ("direct_to_lds", C.c_int),
                 ("tile_rows", C.c_int), ("stream_rows", C.c_int), ("tile_workgroups", C.c_int64),
                 ("stream_workgroups", C.c_int64), ("stream_splits", C.c_int), ("tile_splits", C.c_int),
-                ("tile_split_tiles", C.c_int), ("tile_persistent", C.c_int)]
+                ("tile_split_tiles", C.c_int), ("tile_persistent", C.c_int), ("workspace_bytes", C.c_int64)]
 
 
 class ContractDesc(C.Structure):
@@ -107,12 +108,16 @@ def lib() -> C.CDLL:
     except ImportError:
         pass
     L = C.CDLL(LIB_PATH)
-    p, i, i64, s = C.c_void_p, C.c_int, C.c_int64, C.c_void_p
+    p, i, i64, s, sz = C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_size_t
     L.mmm_gemm_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, s]
-    L.mmm_gemm_f16f32_tiled.argtypes = [p, p, p, i, i, i, i64, i64, i64, i, i, i, i, s]
+    L.mmm_gemm_f16f32_ws.argtypes = [p, p, p, i, i, i, i64, i64, i64, p, sz, s]
+    L.mmm_gemm_workspace_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, C.POINTER(sz)]
+    L.mmm_gemm_f16f32_tiled.argtypes = [p, p, p, i, i, i, i64, i64, i64, i, i, i, i, p, sz, s]
     L.mmm_contract_desc_baseline.argtypes = [C.POINTER(ContractDesc), i, i, i, i, i]
     L.mmm_contract_desc_reference.argtypes = [C.POINTER(ContractDesc), i, i, i, i, i]
     L.mmm_contract5d_f16f32.argtypes = [C.POINTER(ContractDesc), p, p, p, s]
+    L.mmm_contract5d_f16f32_ws.argtypes = [C.POINTER(ContractDesc), p, p, p, p, sz, s]
+    L.mmm_contract5d_workspace_f16f32.argtypes = [C.POINTER(ContractDesc), p, p, p, C.POINTER(sz)]
     L.mmm_fill_uniform_f16.argtypes = [p, i64, C.c_uint64, C.c_uint32, s]
     L.mmm_fill_normal_f16.argtypes = [p, i64, C.c_uint64, C.c_uint32, C.c_double, s]
     L.mmm_tile_of_block.argtypes = [i, i, i, C.POINTER(i), C.POINTER(i)]
@@ -120,8 +125,9 @@ def lib() -> C.CDLL:
     L.mmm_gemm_truth_f64.argtypes = [p, p, p, p, i, i, i, i64, i64, i64, s]
     L.mmm_contract5d_truth_f64.argtypes = [C.POINTER(ContractDesc), p, p, p, p, s]
     L.mmm_gemm_plan_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, C.POINTER(GemmPlan)]
-    for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_tiled", "mmm_contract_desc_baseline",
-                 "mmm_contract_desc_reference", "mmm_contract5d_f16f32", "mmm_fill_uniform_f16",
+    for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_ws", "mmm_gemm_workspace_f16f32", "mmm_gemm_f16f32_tiled",
+                 "mmm_contract_desc_baseline", "mmm_contract_desc_reference", "mmm_contract5d_f16f32",
+                 "mmm_contract5d_f16f32_ws", "mmm_contract5d_workspace_f16f32", "mmm_fill_uniform_f16",
                  "mmm_fill_normal_f16", "mmm_tile_of_block", "mmm_gemm_naive_f16f32", "mmm_gemm_truth_f64",
                  "mmm_contract5d_truth_f64", "mmm_gemm_plan_f16f32"):
         getattr(L, name).restype = C.c_int
@@ -158,12 +164,43 @@ def _check_f16(name: str, t) -> None:
 # Tile parameters (WAVE_M, WAVE_N, WAVES_I, WAVES_J) of the instantiated block tiles.
 TILES = {"256x256": (4, 4, 2, 2), "128x256": (2, 4, 2, 2), "256x128": (4, 2, 2, 2), "128x128": (2, 2, 2, 2)}
 
+# The most workspace any K split uses (the library plans its splits within this).
+MAX_WORKSPACE_BYTES = 64 << 20
 
-def gemm(A, B, C_out=None, tile=None, stream=None):
+# K-split workspaces the wrappers pass to the library: one per (device, stream), from torch's
+# allocator, grown on demand.  Calls on one stream are ordered, so they may share one.
+_ws_lock = threading.Lock()
+_ws_cache = {}
+
+
+def _workspace(device, st: C.c_void_p, nbytes: int):
+    import torch
+
+    key = (device.index if device.index is not None else torch.cuda.current_device(), st.value or 0)
+    with _ws_lock:
+        t = _ws_cache.get(key)
+        if t is None or t.numel() < nbytes:
+            t = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            _ws_cache[key] = t
+        return t
+
+
+def _ws_args(workspace, device, st, nbytes: int):
+    """(pointer, bytes) for a call needing nbytes: the caller's tensor, none (workspace=False),
+    or the per-stream cache."""
+    if workspace is False or nbytes == 0:
+        return None, 0
+    t = workspace if workspace is not None else _workspace(device, st, nbytes)
+    return C.c_void_p(t.data_ptr()), t.numel() * t.element_size()
+
+
+def gemm(A, B, C_out=None, tile=None, stream=None, workspace=None):
     """C = A @ B for fp16 A [M,K] and B [K,N] (row-major, any leading dimension via strides).
 
     Returns the fp32 C [M,N].  ``tile`` is None (library heuristic), a key of TILES, or a
-    (WAVE_M, WAVE_N, WAVES_I, WAVES_J) tuple.
+    (WAVE_M, WAVE_N, WAVES_I, WAVES_J) tuple.  ``workspace``: a CUDA tensor for the K-split
+    partials (mmm_gemm_f16f32_ws), None for a per-stream one from torch's allocator, or False
+    for none (the unsplit kernels).
     """
     import torch
 
@@ -185,11 +222,17 @@ def gemm(A, B, C_out=None, tile=None, stream=None):
     st = _stream(stream)
     L = lib()
     if tile is None:
-        _check("mmm_gemm_f16f32", L.mmm_gemm_f16f32(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, st))
+        need = C.c_size_t(0)
+        _check("mmm_gemm_workspace_f16f32",
+               L.mmm_gemm_workspace_f16f32(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, C.byref(need)))
+        wp, wb = _ws_args(workspace, A.device, st, need.value)
+        _check("mmm_gemm_f16f32_ws",
+               L.mmm_gemm_f16f32_ws(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, wp, wb, st))
     else:
         params = TILES[tile] if isinstance(tile, str) else tuple(tile)
+        wp, wb = _ws_args(workspace, A.device, st, MAX_WORKSPACE_BYTES)
         _check("mmm_gemm_f16f32_tiled",
-               L.mmm_gemm_f16f32_tiled(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, *params, st))
+               L.mmm_gemm_f16f32_tiled(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, *params, wp, wb, st))
     return C_out
 
 
@@ -280,16 +323,23 @@ def contract_desc_reference(mt: int, bt: int, rt: int, nt: int, rt_l: int) -> Co
     return d
 
 
-def contract(desc: ContractDesc, A, B, C_out, stream=None):
-    """Runs the 5-D contraction described by desc (A, B fp16; C fp32; caller-shaped tensors)."""
+def contract(desc: ContractDesc, A, B, C_out, stream=None, workspace=None):
+    """Runs the 5-D contraction described by desc (A, B fp16; C fp32; caller-shaped tensors).
+    ``workspace`` as for gemm (used when the fold is a plain GEMM that splits K)."""
     import torch
 
     _check_f16("A", A)
     _check_f16("B", B)
     if C_out.dtype != torch.float32 or not C_out.is_cuda:
         raise TypeError("C must be a CUDA float32 tensor")
-    _check("mmm_contract5d_f16f32",
-           lib().mmm_contract5d_f16f32(C.byref(desc), _ptr(A), _ptr(B), _ptr(C_out), _stream(stream)))
+    st = _stream(stream)
+    L = lib()
+    need = C.c_size_t(0)
+    _check("mmm_contract5d_workspace_f16f32",
+           L.mmm_contract5d_workspace_f16f32(C.byref(desc), _ptr(A), _ptr(B), _ptr(C_out), C.byref(need)))
+    wp, wb = _ws_args(workspace, A.device, st, need.value)
+    _check("mmm_contract5d_f16f32_ws",
+           L.mmm_contract5d_f16f32_ws(C.byref(desc), _ptr(A), _ptr(B), _ptr(C_out), wp, wb, st))
     return C_out
 
 

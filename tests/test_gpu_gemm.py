@@ -7,6 +7,8 @@ sum exact in any order, so those cases must match an int64 product bit for bit.
 At full size, outputs are checked on sampled rows/columns plus row and column checksums
 (C 1 = A (B 1), 1^T C = (1^T A) B, each within the summed tolerance).
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -315,23 +317,55 @@ def test_stream_split_concurrent_streams(mm, cuda):
 
 
 @pytest.mark.parametrize("rows", [16, 40])
-def test_stream_graph_capture(mm, cuda, rows):
-    """Captured into a HIP graph (no allocation during capture: a stream without a workspace
-    takes the in-workgroup kernel for 16 rows, one K range per workgroup for 40); every
-    replay, with eager work in between, matches eager."""
+@pytest.mark.parametrize("ws", [None, False], ids=["workspace", "no-workspace"])
+def test_stream_graph_capture(mm, cuda, rows, ws):
+    """Captured into a HIP graph, with the wrapper's per-stream workspace (the K split) or none
+    (the in-workgroup kernel for 16 rows, one K range per workgroup for 40); every replay, with
+    eager work in between, matches eager."""
     rng = np.random.default_rng(8)
     A, B, truth = _exact_case(rng, rows, 8192, 2048)
     A, B = to_dev(cuda, A), to_dev(cuda, B)
     C = cuda.full((rows, 8192), float("nan"), dtype=cuda.float32, device="cuda")
     g = cuda.cuda.CUDAGraph()
     with cuda.cuda.graph(g):
-        mm.gemm(A, B, C)
+        mm.gemm(A, B, C, workspace=ws)
     for i in range(3):
         C.fill_(float("nan"))
         g.replay()
         cuda.cuda.synchronize()
         assert np.array_equal(C.cpu().numpy(), truth), f"replay {i}"
         assert np.array_equal(mm.gemm(A, B).cpu().numpy(), truth)
+
+
+# shapes whose launch splits K: streaming (16 and 40 rows), one small round of tiles, a partly
+# filled last round (with a gathered K tail), and the 128x128 tile
+WS_SHAPES = [(16, 8192, 2048), (40, 4096, 4096), (1024, 1024, 8192), (4357, 4095, 4111), (300, 264, 2048)]
+
+
+@pytest.mark.parametrize("shape", WS_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_workspace_entry_point(mm, cuda, shape):
+    """mmm_gemm_f16f32_ws through the C ABI: a workspace of the queried size (K split), one
+    byte short and none (both unsplit) all give exact results, and nothing past the queried
+    size is written."""
+    M, N, K = shape
+    A, B, truth = _exact_case(np.random.default_rng(M + 2 * N + K), M, N, K)
+    A, B = to_dev(cuda, A), to_dev(cuda, B)
+    L = mm.lib()
+    st = C.c_void_p(cuda.cuda.current_stream().cuda_stream)
+    need = C.c_size_t(0)
+    Cd = cuda.empty((M, N), dtype=cuda.float32, device="cuda")
+    assert L.mmm_gemm_workspace_f16f32(A.data_ptr(), B.data_ptr(), Cd.data_ptr(), M, N, K, K, N, N,
+                                       C.byref(need)) == 0
+    assert need.value > 0
+    guard = 4096
+    ws = cuda.full((need.value + guard,), 0x5A, dtype=cuda.uint8, device="cuda")
+    for nbytes in (need.value, need.value - 1, 0):
+        Cd.fill_(float("nan"))
+        ptr = C.c_void_p(ws.data_ptr()) if nbytes else None
+        assert L.mmm_gemm_f16f32_ws(A.data_ptr(), B.data_ptr(), Cd.data_ptr(), M, N, K, K, N, N, ptr, nbytes, st) == 0
+        got = Cd.cpu().numpy()
+        assert np.array_equal(got, truth), f"workspace {nbytes} of {need.value}: {int((got != truth).sum())} mismatches"
+        assert bool((ws[need.value:] == 0x5A).all()), "wrote past the queried workspace size"
 
 
 # (M, N, K, C row padding): whole interior 256x256 tiles over several rounds run on the persistent
@@ -561,7 +595,7 @@ def test_invalid_arguments(mm, cuda):
     p = C.c_void_p(A.data_ptr())
     assert L.mmm_gemm_f16f32(p, p, C.c_void_p(Cd.data_ptr()), 4, 4, 4, 3, 4, 4, null) == mm.HIP_ERROR_INVALID_VALUE
     assert L.mmm_gemm_f16f32(p, p, C.c_void_p(Cd.data_ptr()), -1, 4, 4, 4, 4, 4, null) == mm.HIP_ERROR_INVALID_VALUE
-    assert L.mmm_gemm_f16f32_tiled(p, p, C.c_void_p(Cd.data_ptr()), 4, 4, 4, 4, 4, 4, 2, 2, 4, 4, null) == \
+    assert L.mmm_gemm_f16f32_tiled(p, p, C.c_void_p(Cd.data_ptr()), 4, 4, 4, 4, 4, 4, 2, 2, 4, 4, null, 0, null) == \
         mm.HIP_ERROR_INVALID_VALUE
 
 

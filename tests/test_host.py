@@ -97,11 +97,19 @@ def test_argument_validation_without_gpu(mm):
     assert L.mmm_gemm_f16f32(dummy, dummy, dummy, 8, 8, 8, 7, 8, 8, null) == HIP_INVALID  # lda < K
     assert L.mmm_gemm_f16f32(dummy, dummy, dummy, 8, 8, 8, 8, 7, 8, null) == HIP_INVALID  # ldb < N
     assert L.mmm_gemm_f16f32(dummy, dummy, dummy, 8, 8, 8, 8, 8, 7, null) == HIP_INVALID  # ldc < N
-    assert L.mmm_gemm_f16f32_tiled(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, 2, 2, 4, 4, null) == HIP_INVALID
-    assert L.mmm_gemm_f16f32_tiled(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, 3, 4, 2, 2, null) == HIP_INVALID
+    assert L.mmm_gemm_f16f32_tiled(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, 2, 2, 4, 4, null, 0, null) == HIP_INVALID
+    assert L.mmm_gemm_f16f32_tiled(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, 3, 4, 2, 2, null, 0, null) == HIP_INVALID
+    # a workspace must be 16-byte aligned (checked before any launch)
+    odd = C.c_void_p(0x1008)
+    assert L.mmm_gemm_f16f32_ws(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, odd, 1 << 20, null) == HIP_INVALID
+    assert L.mmm_gemm_f16f32_tiled(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, 2, 2, 2, 2, odd, 1 << 20, null) == HIP_INVALID
+    assert L.mmm_gemm_f16f32_ws(null, null, null, 8, 8, 8, 8, 8, 8, null, 0, null) == HIP_INVALID
+    assert L.mmm_gemm_workspace_f16f32(null, null, null, 8, 8, 8, 8, 8, 8, None) == HIP_INVALID
     d = mm.contract_desc_baseline(2, 3, 4, 5, 6)
     assert L.mmm_contract5d_f16f32(C.byref(d), null, null, null, null) == HIP_INVALID
     assert L.mmm_contract5d_f16f32(None, dummy, dummy, dummy, null) == HIP_INVALID
+    assert L.mmm_contract5d_f16f32_ws(C.byref(d), dummy, dummy, dummy, odd, 1 << 20, null) == HIP_INVALID
+    assert L.mmm_contract5d_workspace_f16f32(C.byref(d), null, null, null, None) == HIP_INVALID
     assert L.mmm_fill_uniform_f16(null, 10, 0, 0, null) == HIP_INVALID
     assert L.mmm_fill_uniform_f16(null, 0, 0, 0, null) == 0
     assert L.mmm_contract_desc_baseline(None, 1, 1, 1, 1, 1) == HIP_INVALID
@@ -181,6 +189,7 @@ def test_gemm_plan(mm):
     p = mm.gemm_plan(8192, 8192, 8192)
     assert p["kernel"] == "tile" and (p["block_m"], p["block_n"]) == (256, 256)
     assert p["tile_persistent"] == 1  # 1024 whole tiles: 256 workgroups loop over 4 each
+    assert p["workspace_bytes"] == 0  # no K split
     assert mm.gemm_plan(4096, 4096, 4096)["tile_persistent"] == 0  # one round
     assert p["direct_to_lds"] == 1 and p["tile_workgroups"] == 32 * 32 and p["stream_rows"] == 0
     p = mm.gemm_plan(4097, 4095, 4111)  # one row past 16 tile rows: that row streams
@@ -190,6 +199,10 @@ def test_gemm_plan(mm):
     p = mm.gemm_plan(16, 8192, 8192)
     assert p["kernel"] == "stream" and p["stream_rows"] == 16 and p["tile_workgroups"] == 0
     assert p["stream_splits"] == 4 and p["stream_workgroups"] == 64 * 4
+    assert p["workspace_bytes"] == 64 * 4 * 16 * 128 * 4  # [strip][split][16][128] fp32 partials
+    need = C.c_size_t(0)
+    assert mm.lib().mmm_gemm_workspace_f16f32(None, None, None, 16, 8192, 8192, 8192, 8192, 8192,
+                                              C.byref(need)) == 0 and need.value == p["workspace_bytes"]
     # too little K to split: 32-column strips, K split among each workgroup's waves
     p = mm.gemm_plan(16, 8192, 128)
     assert p["stream_splits"] == 0 and p["stream_workgroups"] == 8192 // 32
@@ -202,6 +215,7 @@ def test_gemm_plan(mm):
     # under-filled last round: 576 tiles = 2 rounds + 64; those 64 run as 4 K ranges each
     p = mm.gemm_plan(6144, 6144, 6144)
     assert (p["block_m"], p["tile_splits"], p["tile_split_tiles"], p["tile_workgroups"]) == (256, 4, 64, 576)
+    assert p["workspace_bytes"] == 64 * 4 * 256 * 256 * 4  # [split tile][split][256][256] fp32
     p = mm.gemm_plan(6150, 6144, 1030)  # short K: the reduction would cost more than it saves
     assert (p["tile_splits"], p["tile_split_tiles"]) == (1, 0)
     p = mm.gemm_plan(16 * 256 + 40, 4096, 264)  # 40 rows past 16 tile rows stream
