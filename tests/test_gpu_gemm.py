@@ -71,6 +71,27 @@ def test_config1_256_full(orc, mm, cuda):
     assert np.all(np.abs(C.astype(np.float64) - N32) <= TOL * S), "violations vs GEMM_Naive's fp32 math"
 
 
+def test_config1_golden_record(mm, cuda):
+    """C1's inputs from the on-device generator hash to the committed record, and the GEMM's
+    sample outputs are within tolerance of the committed fp64 values."""
+    import hashlib
+    import json
+    import os
+
+    rec = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "c1_256.json")))
+    A = cuda.empty((256, 256), dtype=cuda.float16, device="cuda")
+    B = cuda.empty((256, 256), dtype=cuda.float16, device="cuda")
+    mm.fill_uniform(A, 0, 0)
+    mm.fill_uniform(B, 0, 1)
+    h = lambda t: hashlib.sha256(t.cpu().numpy().view(np.uint16).tobytes()).hexdigest()
+    assert h(A) == rec["sha256"]["A_f16_bits"] and h(B) == rec["sha256"]["B_f16_bits"]
+    C = mm.gemm(A, B).cpu().numpy()
+    _, S = mm.gemm_truth(A, B)
+    S = S.cpu().numpy()
+    for (i, j), key in [((0, 0), "C[0][0]"), ((255, 255), "C[255][255]"), ((17, 200), "C[17][200]")]:
+        assert abs(float(C[i, j]) - rec["samples"][key]) <= TOL * S[i, j], key
+
+
 def test_config2_8192_sampled(orc, mm, cuda):
     """C2: 8192^3, U[-1,1], seed 1; sampled rows/cols vs fp64, plus row/column checksums."""
     n = 8192

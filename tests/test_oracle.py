@@ -107,6 +107,23 @@ def test_gemm_golden_small(orc):
     assert np.array_equal(C, g["C"]) and np.array_equal(S, g["S"])
 
 
+def test_c1_golden_record(orc):
+    """Configuration C1 (256^3, seed 0): the seeded inputs and the fp64 result match the
+    committed hashes and sample values."""
+    import hashlib
+
+    rec = json.load(open(os.path.join(GOLDEN, "c1_256.json")))
+    A = orc.uniform_f16((256, 256), 0, 0)
+    B = orc.uniform_f16((256, 256), 0, 1)
+    C, S = orc.gemm_f64(A, B)
+    h = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    assert h(A.view(np.uint16)) == rec["sha256"]["A_f16_bits"]
+    assert h(B.view(np.uint16)) == rec["sha256"]["B_f16_bits"]
+    assert h(C) == rec["sha256"]["C_f64"] and h(S) == rec["sha256"]["S_f64"]
+    assert C[0, 0] == rec["samples"]["C[0][0]"] and C[255, 255] == rec["samples"]["C[255][255]"]
+    assert C[17, 200] == rec["samples"]["C[17][200]"]
+
+
 def test_fp32_restatements_exact_on_integers(orc):
     rng = np.random.default_rng(3)
     A = rng.integers(-4, 5, size=(33, 70)).astype(np.float16)
@@ -180,6 +197,16 @@ def test_contract_baseline_matches_einsum(orc):
     # equals the GEMM of the folded operands (the fold the library uses)
     Cg, Sg = orc.gemm_f64(A.reshape(18, 15), B.reshape(15, 11))
     assert np.allclose(C, Cg, rtol=0, atol=1e-14)
+
+
+def test_contract_baseline_golden_small(orc):
+    """The benchmark contraction's layout at a size small enough to commit: the seeded inputs
+    and the fp64 loop nest reproduce the fixture exactly."""
+    g = np.load(os.path.join(GOLDEN, "contract_baseline_small.npz"))
+    assert np.array_equal(orc.normal_f16((2, 3, 4, 5), 11, 0, 0.1).view(np.uint16), g["A"].view(np.uint16))
+    assert np.array_equal(orc.normal_f16((4, 5, 6), 11, 1, 0.1).view(np.uint16), g["B"].view(np.uint16))
+    C, S = orc.contract_baseline_f64(g["A"], g["B"])
+    assert np.array_equal(C, g["C"]) and np.array_equal(S, g["S"])
 
 
 def test_contract_reference_matches_einsum_and_pack(orc):
