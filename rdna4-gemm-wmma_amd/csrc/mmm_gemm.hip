@@ -43,6 +43,9 @@
 #ifndef MMM_XINTERLEAVE
 #define MMM_XINTERLEAVE 1  // interleave the steady-state refill loads with the last K-step's MFMAs
 #endif
+#ifndef MMM_SPREAD_BODY
+#define MMM_SPREAD_BODY 1  // spread each K-step's next-step fragment reads over its MFMAs
+#endif
 #ifndef MMM_SPREAD_READS
 #define MMM_SPREAD_READS 1  // spread the next tile's first fragment reads over the last K-step's MFMAs
 #endif
@@ -324,11 +327,21 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
     const char LDS_AS* st = lds_base + cur * T::STAGE;
 #pragma unroll
     for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
-      load_frags<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, f[(kk + 1) & 1]);
-      mfma_frags<T>(f[kk & 1], acc);
-      // keep the next step's LDS reads ahead of this step's MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);
+      if constexpr (MMM_SPREAD_BODY) {
+        // MFMA i of this step carries fragment read i of the next
+#pragma unroll
+        for (int i = 0; i < T::FM * T::FN; ++i) {
+          mfma_one<T>(f[kk & 1].b[i % T::FN], f[kk & 1].a[i / T::FN], acc[i / T::FN][i % T::FN]);
+          if (i < T::FM + T::FN) load_frag_unit<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, i, f[(kk + 1) & 1]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+        load_frags<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, f[(kk + 1) & 1]);
+        mfma_frags<T>(f[kk & 1], acc);
+        // keep the next step's LDS reads ahead of this step's MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);
+      }
     }
   };
   // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
