@@ -43,6 +43,16 @@
 #ifndef MMM_XINTERLEAVE
 #define MMM_XINTERLEAVE 1  // interleave the steady-state refill loads with the last K-step's MFMAs
 #endif
+// Count a round as 256 x (the tile's workgroups per CU) when deciding a K split (measured:
+// 3072^3 -5.5%, 1536^2 x 12288 -5%, 2304^2 x 8192 -2% against 256 per round).
+#ifndef MMM_SPLIT_OCC
+#define MMM_SPLIT_OCC 0
+#endif
+// MFMAs between two refill loads in the steady-state step (measured with 2: 8192^3 +1-2%,
+// 8192^2 x 2048 -3%, the rest within noise).
+#ifndef MMM_DMA_STRIDE
+#define MMM_DMA_STRIDE 1
+#endif
 #ifndef MMM_SPREAD_BODY
 #define MMM_SPREAD_BODY 1  // spread each K-step's next-step fragment reads over its MFMAs
 #endif
@@ -372,19 +382,22 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
     const int nslot = cur + 1 == S ? 0 : cur + 1;
     const char LDS_AS* ns = lds_base + nslot * T::STAGE;
     constexpr int NM = T::FM * T::FN, NU = MMM_SPREAD_READS ? T::FM + T::FN : 0;
-    constexpr int D0 = NM - T::LPT >= NU ? NU : (NM > T::LPT ? NM - T::LPT : 0);
+    constexpr int DS = MMM_DMA_STRIDE;  // MFMAs between two refill loads
+    constexpr int D0 = NM - DS * T::LPT >= NU ? NU : (NM > DS * T::LPT ? NM - DS * T::LPT : 0);
     if constexpr (!MMM_SPREAD_READS) load_frags<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
     const auto d = prep(t + S, cur);
+    int issued = 0;
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
       const int mb = i / T::FN, nb = i % T::FN;
       mfma_one<T>(f[1].b[nb], f[1].a[mb], acc[mb][nb]);
       if (i < NU) load_frag_unit<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, i, f[0]);
-      if (i >= D0 && i - D0 < T::LPT) dma_one(d, i - D0);
+      if (i >= D0 && (i - D0) % DS == 0 && issued < T::LPT) dma_one(d, issued++);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int j = NM - D0; j < T::LPT; ++j) dma_one(d, j);
+    for (int j = 0; j < T::LPT; ++j)
+      if (j >= issued) dma_one(d, j);
     cur = nslot;
   };
   // steady state refills by DMA only; the refill of the last tile (possibly gathered
@@ -1281,10 +1294,13 @@ TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
   const int bm = tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128;
   const int bn = tile_id == kTile256x256 || tile_id == kTile128x256 ? 256 : 128;
   const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
-  const int64_t last = tiles - (tiles - 1) / 256 * 256;  // tiles in the last round (1 .. 256)
-  if (last >= 128) return {1, 0};
+  // workgroups one round holds: one per CU, times the tile's workgroups per CU when counted
+  const int occ = MMM_SPLIT_OCC ? (tile_id == kTile256x256 ? 1 : tile_id == kTile128x128 ? 2 : MMM_T2_OCC) : 1;
+  const int64_t slots = 256 * occ;
+  const int64_t last = tiles - (tiles - 1) / slots * slots;  // tiles in the last round (1 .. slots)
+  if (last * 2 >= slots) return {1, 0};
   const int kt = (p.K + 63) / 64;  // 64-deep K tiles (the 32-deep tiles have twice as many)
-  int64_t splits = 256 / last;
+  int64_t splits = slots / last;
   if (splits > kt / 8) splits = kt / 8;
   if (splits > 16) splits = 16;
   const int64_t cap = (int64_t)(kMaxWorkspaceBytes / ((size_t)bm * bn * 4)) / last;
