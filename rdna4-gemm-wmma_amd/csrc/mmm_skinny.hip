@@ -272,20 +272,36 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
 }
 
 // C[row][strip * 128 + c] = sum over q = 0 .. splits-1 (in that order) of the strip's
-// partials; one thread per element of the ROWS x 128 strip tiles.
+// partials; one thread per 4 consecutive elements of the ROWS x 128 strip tiles.  All of a
+// thread's split loads are issued before the sum (splits <= kMaxSplits), so the kernel costs
+// one memory round trip.
+constexpr int kMaxSplits = 16;
 template <int ROWS>
 __global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int strips, int splits,
                                                             const float* partials) {
   constexpr int TILE = ROWS * 128;
   const int idx = blockIdx.x * 256 + threadIdx.x;
-  const int strip = idx / TILE, e = idx % TILE, row = e >> 7, col = strip * 128 + (e & 127);
+  const int strip = idx / (TILE / 4), e = 4 * (idx % (TILE / 4)), row = e >> 7, col = strip * 128 + (e & 127);
   if (strip >= strips) return;
-  const float* base = partials + (int64_t)strip * splits * TILE + e;
-  float sum = base[0];
-  for (int q = 1; q < splits; ++q) sum += base[q * TILE];
-  if (row < p.M && col < p.N) p.C[(int64_t)row * p.ldc + col] = sum;
+  const f32x4* base = (const f32x4*)(partials + (int64_t)strip * splits * TILE + e);
+  f32x4 v[kMaxSplits];
+#pragma unroll
+  for (int q = 0; q < kMaxSplits; ++q)
+    if (q < splits) v[q] = base[q * (TILE / 4)];
+  f32x4 sum = v[0];
+#pragma unroll
+  for (int q = 1; q < kMaxSplits; ++q)
+    if (q < splits) sum += v[q];
+  if (row >= p.M) return;
+  float* c = p.C + (int64_t)row * p.ldc + col;
+  if (p.c_vec4 && col + 3 < p.N) {
+    *(f32x4*)c = sum;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (col + i < p.N) c[i] = sum[i];
+  }
 }
-
 
 // ------------------------------------------------------------------------------------
 // Split streaming kernel (M <= 64, enough K): one workgroup per 128-column strip and K range
@@ -520,7 +536,7 @@ static StreamShape stream_shape(const GemmProblem& p) {
   const int strips = (p.N + 127) / 128;
   const int nst_all = (p.K + 63) / 64;  // 64-deep K steps
   int splits = 256 / strips;
-  splits = splits < 16 ? splits : 16;
+  splits = splits < kMaxSplits ? splits : kMaxSplits;
   splits = splits < nst_all / 4 ? splits : nst_all / 4;
   if (splits > kWsTiles / strips) splits = kWsTiles / strips;
   if (splits < 1) splits = 1;
@@ -556,7 +572,7 @@ static hipError_t launch_wide(const GemmProblem& p, int strips, int splits, floa
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   constexpr int ROWS = 16 * MR;
-  hipLaunchKernelGGL(reduce_splits_kernel<ROWS>, dim3(strips * (ROWS * 128 / 256)), dim3(256), 0, stream, p, strips,
+  hipLaunchKernelGGL(reduce_splits_kernel<ROWS>, dim3(strips * (ROWS * 128 / 4 / 256)), dim3(256), 0, stream, p, strips,
                      splits, (const float*)ws);
   return hipGetLastError();
 }
@@ -565,6 +581,7 @@ hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
   GemmProblem p = p0;
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   p.tail_regs = (a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8;
+  p.c_vec4 = (uintptr_t)p.C % 4 == 0;
   StreamShape sh = stream_shape(p);
   float* ws = sh.splits > 1 && p.ws && p.ws_bytes >= skinny_workspace_bytes(p) ? p.ws : nullptr;
   if (sh.splits > 1 && !ws && sh.mr > 1) sh.splits = 1;  // no workspace: one split
