@@ -1189,23 +1189,41 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
 
   // epilogue: lane owns row m and columns n .. n+3 of each accumulator group, scattered
   // through the C strides (MF = 32: m = l % 32, n = 32*nb + 8*q + 4*(l/32); MF = 16:
-  // m = l % 16, n = 16*nb + 4*(l/16))
+  // m = l % 16, n = 16*nb + 4*(l/16)).  A group's first column n is a multiple of 4, so when
+  // n_lo is too, its 4 columns share one n_hi block and sit cn[1] apart: one fold_off per
+  // group (computed once per lane) instead of one division per element.
   constexpr int NQ = T::MF == 32 ? 4 : 1;
   float* C = p.C;
+  const bool quad = p.n_lo % 4 == 0;  // uniform
+  const int64_t cn1 = p.cn[1];
+  int64_t coff[T::FN][NQ];
+#pragma unroll
+  for (int nb = 0; nb < T::FN; ++nb)
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int n = n0 + wn * T::TN + (T::MF == 32 ? 32 * nb + 8 * q + 4 * (lane >> 5) : 16 * nb + 4 * (lane >> 4));
+      coff[nb][q] = n < N ? fold_off(n, p.n_lo, p.cn[0], p.cn[1]) : 0;
+    }
 #pragma unroll
   for (int mb = 0; mb < T::FM; ++mb) {
     const int m = m0 + wm * T::TM + T::MF * mb + (lane % T::MF);
     if (m >= M) continue;
-    const int64_t crow = fold_off(m, p.m_lo, p.cm[0], p.cm[1]);
+    float* crow = C + fold_off(m, p.m_lo, p.cm[0], p.cm[1]);
 #pragma unroll
     for (int nb = 0; nb < T::FN; ++nb)
 #pragma unroll
-      for (int q = 0; q < NQ; ++q)
+      for (int q = 0; q < NQ; ++q) {
+        const int n = n0 + wn * T::TN + (T::MF == 32 ? 32 * nb + 8 * q + 4 * (lane >> 5) : 16 * nb + 4 * (lane >> 4));
+        if (quad && n + 3 < N) {
+          float* c = crow + coff[nb][q];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int n = n0 + wn * T::TN + (T::MF == 32 ? 32 * nb + 8 * q + 4 * (lane >> 5) : 16 * nb + 4 * (lane >> 4)) + e;
-          if (n < N) C[crow + fold_off(n, p.n_lo, p.cn[0], p.cn[1])] = acc[mb][nb][4 * q + e];
+          for (int e = 0; e < 4; ++e) c[e * cn1] = acc[mb][nb][4 * q + e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) crow[fold_off(n + e, p.n_lo, p.cn[0], p.cn[1])] = acc[mb][nb][4 * q + e];
         }
+      }
   }
 }
 
