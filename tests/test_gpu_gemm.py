@@ -650,7 +650,9 @@ def test_contraction_reference_layout_exact(mm, cuda, orc, dims):
     assert np.array_equal(got, gemm.reshape(mt, rt, bt).transpose(0, 2, 1).astype(np.float32))
 
 
-@pytest.mark.parametrize("dims", [(8, 300, 64, 3, 128), (4, 520, 32, 2, 64)], ids=lambda d: "x".join(map(str, d)))
+# bt = 301 and 258: n_lo = bt not a multiple of 4, so the epilogue takes its per-element path
+@pytest.mark.parametrize("dims", [(8, 300, 64, 3, 128), (4, 520, 32, 2, 64), (8, 301, 64, 3, 128), (4, 258, 32, 2, 64)],
+                         ids=lambda d: "x".join(map(str, d)))
 def test_contraction_reference_layout_dma_exact(mm, cuda, orc, dims):
     """Reference layout on the direct-to-LDS fold path (K tiles inside one n block): bit-exact."""
     mt, bt, rt, nt, rt_l = dims
