@@ -650,8 +650,10 @@ def test_contraction_reference_layout_exact(mm, cuda, orc, dims):
     assert np.array_equal(got, gemm.reshape(mt, rt, bt).transpose(0, 2, 1).astype(np.float32))
 
 
-# bt = 301 and 258: n_lo = bt not a multiple of 4, so the epilogue takes its per-element path
-@pytest.mark.parametrize("dims", [(8, 300, 64, 3, 128), (4, 520, 32, 2, 64), (8, 301, 64, 3, 128), (4, 258, 32, 2, 64)],
+# bt = 301 and 258: n_lo = bt not a multiple of 4, so the epilogue stores element by element;
+# rt = 6: rows of 6; 32 x 8448 x 64: 264 tiles of 256 x 256 (two rounds, the second partly filled)
+@pytest.mark.parametrize("dims", [(8, 300, 64, 3, 128), (4, 520, 32, 2, 64), (8, 301, 64, 3, 128), (4, 258, 32, 2, 64),
+                                  (8, 300, 6, 3, 128), (32, 8448, 64, 2, 64)],
                          ids=lambda d: "x".join(map(str, d)))
 def test_contraction_reference_layout_dma_exact(mm, cuda, orc, dims):
     """Reference layout on the direct-to-LDS fold path (K tiles inside one n block): bit-exact."""
@@ -664,6 +666,21 @@ def test_contraction_reference_layout_dma_exact(mm, cuda, orc, dims):
     Out = cuda.full((mt, bt, rt), float("nan"), dtype=cuda.float32, device="cuda")
     mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), to_dev(cuda, G), to_dev(cuda, In), Out)
     assert np.array_equal(Out.cpu().numpy(), truth.astype(np.float32))
+
+
+def test_contraction_reference_layout_dma_unaligned_out(mm, cuda, orc):
+    """Out 4-byte but not 16-byte aligned."""
+    mt, bt, rt, nt, rt_l = 8, 300, 64, 3, 128
+    rng = np.random.default_rng(77)
+    G = rng.integers(-4, 5, size=(rt, nt, mt, rt_l)).astype(np.float16)
+    In = rng.integers(-4, 5, size=(bt, nt, rt_l)).astype(np.float16)
+    hA = orc.pack_reference_G(G).astype(np.float64)
+    truth = (hA @ In.reshape(bt, nt * rt_l).astype(np.float64).T).reshape(mt, rt, bt).transpose(0, 2, 1)
+    buf = cuda.full((mt * bt * rt + 1,), float("nan"), dtype=cuda.float32, device="cuda")
+    Out = buf[1:].view(mt, bt, rt)
+    mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), to_dev(cuda, G), to_dev(cuda, In), Out)
+    assert np.array_equal(Out.cpu().numpy(), truth.astype(np.float32))
+    assert np.isnan(buf[0].item())
 
 
 def test_contraction_reference_layout_full_size(mm, cuda, orc):
