@@ -789,7 +789,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
 // (issued after the loads) stay outstanding, since vector-memory operations retire in issue
 // order.
 // ------------------------------------------------------------------------------------
-template <class T>
+template <class T, bool NT>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
   constexpr int S = T::STAGES;
@@ -914,8 +914,12 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
 #pragma unroll
         for (int qq = 0; qq < NQ; ++qq) {
           const int n = T::MF == 32 ? 32 * nb2 + 8 * qq + 4 * (lane >> 5) : 16 * nb2 + 4 * (lane >> 4);
-          *(f32x4*)(crow + n) = f32x4{acc[mb][nb2][4 * qq + 0], acc[mb][nb2][4 * qq + 1], acc[mb][nb2][4 * qq + 2],
-                                      acc[mb][nb2][4 * qq + 3]};
+          const f32x4 v = {acc[mb][nb2][4 * qq + 0], acc[mb][nb2][4 * qq + 1], acc[mb][nb2][4 * qq + 2],
+                           acc[mb][nb2][4 * qq + 3]};
+          if constexpr (NT)
+            __builtin_nontemporal_store(v, (f32x4*)(crow + n));
+          else
+            *(f32x4*)(crow + n) = v;
         }
     }
     if (nb >= ntiles) break;
@@ -1104,7 +1108,7 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
 //  * Output scattered through the C strides: lanes own consecutive m, so an output whose
 //    m_lo is contiguous (Out[m][b][r]) is written in 128-byte runs.
 // ------------------------------------------------------------------------------------
-template <class T>
+template <class T, bool NT>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProblem p, int tiles_m, int tiles_n,
                                                                       uint32_t a_bytes, uint32_t b_bytes) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
@@ -1217,7 +1221,12 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
         if (quad && n + 3 < N) {
           float* c = crow + coff[nb][q];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) c[e * cn1] = acc[mb][nb][4 * q + e];
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (NT)
+              __builtin_nontemporal_store(acc[mb][nb][4 * q + e], c + e * cn1);
+            else
+              c[e * cn1] = acc[mb][nb][4 * q + e];
+          }
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
@@ -1256,6 +1265,9 @@ __global__ __launch_bounds__(256) void reduce_tiles_kernel(GemmProblem p, int ti
       if (n + i < p.N) crow[n + i] = sum[i];
   }
 }
+
+// Shortest K for which the multi-round kernels store C non-temporally (see their launches).
+constexpr int kNtMinK = 4096;
 
 template <class T, bool GENERIC>
 static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
@@ -1448,8 +1460,18 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
     case kTile256x256:
       if (MMM_PERSIST && persistent_ok(p)) {
         using TP = DmaTile<256, 256>;
-        hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP>), dim3(256), dim3(TP::NT), 0, stream, p, p.M / TP::BM,
-                           p.N / TP::BN);
+        // Non-temporal C stores: the persistent grid stores a tile's C while its next tile's
+        // operand loads run, and L2-allocating stores would evict the operand panels other
+        // workgroups of the XCD are about to read.  That wins when each tile's K loop is long;
+        // with short K the slower-draining non-temporal stores weigh more (measured on MI355X:
+        // 12288^2 x 4096 +6.7%, 8192^3 +1.6-2.8%, 6144^3 -0.6%, 8192^2 x 2048 -7.1%,
+        // 16384 x 8192 x 1024 -9.3%).  16-byte-aligned C rows only.
+        if (((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 && p.K >= kNtMinK)
+          hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, p.M / TP::BM,
+                             p.N / TP::BN);
+        else
+          hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, false>), dim3(256), dim3(TP::NT), 0, stream, p,
+                             p.M / TP::BM, p.N / TP::BN);
         return hipGetLastError();
       }
       return dma_ok(p, 256) ? launch_nn<DmaTile<256, 256>, false>(p, stream)
@@ -1490,8 +1512,17 @@ hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream) {
   if (fast) {
     const int tiles_m = (p.M + TD::BM - 1) / TD::BM;
     const int tiles_n = (p.N + TD::BN - 1) / TD::BN;
-    hipLaunchKernelGGL((gemm_fold_dma_kernel<TD>), dim3((unsigned)(tiles_m * tiles_n)), dim3(TD::NT), 0, stream, p,
-                       tiles_m, tiles_n, (uint32_t)(a_ext * 2), (uint32_t)(b_ext * 2));
+    // Non-temporal C stores when the grid has more than one round and K is long: later tiles'
+    // operand loads then run while earlier tiles' C is written, and L2-allocating stores would
+    // evict operand panels (measured on MI355X at the reference's M = N = K = 8192: +13-15%).  A
+    // one-round grid writes all of C after its last K step, where L2-allocating stores drain
+    // faster (plain-GEMM tiles: 4096^3 -5.5%, 8192 x 2048 x 2048 -6.7% with non-temporal stores).
+    if ((int64_t)tiles_m * tiles_n > 256 && p.K >= kNtMinK)
+      hipLaunchKernelGGL((gemm_fold_dma_kernel<TD, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(TD::NT), 0, stream,
+                         p, tiles_m, tiles_n, (uint32_t)(a_ext * 2), (uint32_t)(b_ext * 2));
+    else
+      hipLaunchKernelGGL((gemm_fold_dma_kernel<TD, false>), dim3((unsigned)(tiles_m * tiles_n)), dim3(TD::NT), 0,
+                         stream, p, tiles_m, tiles_n, (uint32_t)(a_ext * 2), (uint32_t)(b_ext * 2));
     return hipGetLastError();
   }
   using T = RegTile<128, 128>;
