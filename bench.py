@@ -258,7 +258,10 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness):
 SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
                 (6144, 6144, 6144), (8192, 8192, 8192), (8192, 2048, 2048), (2048, 8192, 2048), (4097, 4095, 4111),
                 (16384, 1024, 4096), (1024, 16384, 4096), (8192, 8192, 1024), (1024, 1024, 8192), (3000, 5000, 1000),
-                (64, 4096, 4096), (1536, 1536, 12288)]
+                (64, 4096, 4096), (1536, 1536, 12288),
+                # partly filled last rounds (K split of the last round) and short-K few-round grids
+                (4608, 4608, 8192), (7168, 7168, 7168), (10240, 10240, 4096), (2304, 2304, 8192), (3072, 3072, 3072),
+                (6144, 6144, 2048)]
 
 
 def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool) -> None:
