@@ -497,7 +497,9 @@ struct NoHook {
 // GENERIC = false: direct-to-LDS buffer loads; needs lda, ldb, K, N multiples of 8 and
 //                  16-byte-aligned A and B (checked by the host).
 // GENERIC = true : element-wise masked loads through VGPRs; any shape and alignment.
-template <class T, bool GENERIC>
+// WT = true: C rows (16-byte aligned) are written with system-scope write-through stores
+//            (sc0 sc1), for one-round grids (see launch_nn).
+template <class T, bool GENERIC, bool WT = false>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
 
@@ -767,7 +769,10 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         const int n = n0 + wn * T::TN + col_of(nb, q);
         f32x4 v = {acc[mb][nb][4 * q + 0], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2], acc[mb][nb][4 * q + 3]};
         if (vec_ok && n + 3 < N) {
-          *(f32x4*)(crow + n) = v;
+          if constexpr (WT)
+            asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(crow + n), "v"(v) : "memory");
+          else
+            *(f32x4*)(crow + n) = v;
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
@@ -1279,8 +1284,25 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
   if (split_tiles < 0 || split_tiles > tiles) return hipErrorInvalidValue;
   const int64_t blocks = tiles - split_tiles + split_tiles * splits;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_nn_kernel<T, GENERIC>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
-                     tiles_n);
+  // A one-round grid writes all of C after its last K step, with nothing left to overlap.  When
+  // C is larger than the eight XCDs' L2 (32 MB), write-back stores end in dirty-line evictions
+  // anyway, and system-scope write-through stores drain the burst faster (measured on MI355X,
+  // 256x256 tile, no K split: 8192 x 2048 x 2048 +3.1%, 4096^3 +1.3%).  Not where C fits the L2
+  // (2048^3 -4.7%, 1024^3 -7.5%), with a K split (3072^3 on 128x256 -8.8%) or for rows of an
+  // odd ldc (-9%).
+  const bool wt = T::BM == 256 && T::BN == 256 && splits == 1 && blocks <= 256 * T::OCC &&
+                  (double)p.M * p.N * 4.0 > 32.0 * (1 << 20) && ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0;
+  if constexpr (!GENERIC) {
+    if (wt)
+      hipLaunchKernelGGL((gemm_nn_kernel<T, false, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
+                         tiles_n);
+    else
+      hipLaunchKernelGGL((gemm_nn_kernel<T, false>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
+                         tiles_n);
+  } else {
+    (void)wt;
+    hipLaunchKernelGGL((gemm_nn_kernel<T, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m, tiles_n);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   const int64_t per_tile = T::BM * T::BN / 4 / 256;  // blocks of 256 float4s per tile
