@@ -311,8 +311,12 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int s
 // sum goes to C; otherwise to the workspace, and reduce_splits_kernel, launched next on the
 // same stream, sums the splits of every strip in split order (fixed orders throughout:
 // deterministic; the kernel boundary orders the partial stores before their reads).  B slots
-// [KS][128] use the tile kernel's row swizzle (chunk c of row k at c ^ {0,6,10,12}[k & 3]) so
-// the transposing reads of four 256-byte rows hit distinct banks.  MR 16-row groups of A
+// [KS][128] have 256-byte rows -- one row of the 64 banks each -- so a chunk's banks depend only
+// on its slot position.  One pass of a 16x16x32 transposing read takes rows k .. k+3 and
+// k+8 .. k+11 at two chunks each; chunk c of row k sits at c ^ swz_b(k), swz_b(k) =
+// {0,6,10,12}[k & 3] ^ 2 * ((k >> 3) & 1): eight distinct XOR values, so the pass's 16 chunks hit
+// all 64 banks once (without the k >> 3 term rows k and k+8 collide: measured 45% of the LDS
+// cycles in bank conflicts).  MR 16-row groups of A
 // (MR = 1, 2, 4 for up to 16, 32, 64 rows) share every B fragment: MR MFMAs per B read.
 // ------------------------------------------------------------------------------------
 template <int MR>
@@ -331,7 +335,7 @@ struct Wide {
   static_assert(KS == 32 || KS == 64, "K rows per slot");
   static_assert(LDS_BYTES <= 160 * 1024, "rings and partials must fit the LDS");
   __device__ static __forceinline__ int swz_a(int row) { return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
-  __device__ static __forceinline__ int swz_b(int k) { return (0xCA60 >> (4 * (k & 3))) & 15; }
+  __device__ static __forceinline__ int swz_b(int k) { return ((0xCA60 >> (4 * (k & 3))) & 15) ^ (((k >> 3) & 1) << 1); }
 };
 
 template <int MR>
@@ -371,9 +375,12 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     a_kc[i] = 8 * ((lane % CA) ^ W::swz_a(row));
     a_goff[i] = (uint32_t)((row * lda + a_kc[i]) * 2);
   }
+  // B rows of load i are 4i + b_row (RPI = 4): swz_b(4i + b_row) = swz_b(b_row) ^ 2 when
+  // (i >> 1) is odd, i.e. chunk slot c holds logical chunk c ^ swz_b(b_row) or its ^ 2 partner
   const int b_row = lane / CPR;
-  const int b_nc = 8 * ((lane % CPR) ^ W::swz_b(b_row));  // swz_b depends on row % 4 = b_row (RPI = 4)
-  const uint32_t b_goff = (uint32_t)((b_row * ldb + b_nc) * 2);
+  static_assert(RPI == 4, "the B swizzle's row phases assume four rows per load");
+  const int b_nc0 = 8 * ((lane % CPR) ^ W::swz_b(b_row)), b_nc1 = b_nc0 ^ 16;
+  const uint32_t b_goff0 = (uint32_t)((b_row * ldb + b_nc0) * 2), b_goff1 = (uint32_t)((b_row * ldb + b_nc1) * 2);
   const uint32_t b_rstep = (uint32_t)(RPI * ldb * 2);
   const i32x4 rb_full = make_rsrc(p.B + n0, clip_records(((int64_t)(K - 1) * ldb + N - n0) * 2));
 
@@ -388,7 +395,7 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     }
     const uint32_t bk = (uint32_t)((int64_t)k0 * ldb * 2);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) dma_b128(dst + ABYTES + i * 1024, rb_full, bk + b_goff + i * b_rstep);
+    for (int i = 0; i < NB; ++i) dma_b128(dst + ABYTES + i * 1024, rb_full, bk + ((i >> 1) & 1 ? b_goff1 : b_goff0) + i * b_rstep);
   };
   // globally last K slot of an unaligned problem: gathered element by element (same layout)
   const _Float16* Ah = (const _Float16*)p.A;
@@ -409,7 +416,7 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const int k = k0 + i * RPI + b_row, n = n0 + b_nc;
+      const int k = k0 + i * RPI + b_row, n = n0 + ((i >> 1) & 1 ? b_nc1 : b_nc0);
       half8 v = {};
       if (k < K) {
 #pragma unroll
