@@ -330,7 +330,10 @@ struct Wide {
   static constexpr int NT = NS / 16, CPR = NS / 8, RPI = 64 / CPR;  // 8 tiles, 16 chunks per row, 4 rows
   static constexpr int CA = KS / 8, RPI_A = 64 / CA;
   static constexpr int RING_BYTES = kWaves * SLOTS * SLOT;
-  static constexpr int PART_BYTES = kWaves * ROWS * NS * 4;  // [wave][ROWS][128] fp32
+  // [wave][ROWS][PS] fp32 partial sums; rows padded by 4 floats so the four 4-row lane groups of
+  // an accumulator store (rows 4 apart) land 16 banks apart instead of on the same banks
+  static constexpr int PS = NS + 4;
+  static constexpr int PART_BYTES = kWaves * ROWS * PS * 4;
   static constexpr int LDS_BYTES = RING_BYTES > PART_BYTES ? RING_BYTES : PART_BYTES;
   static_assert(KS == 32 || KS == 64, "K rows per slot");
   static_assert(LDS_BYTES <= 160 * 1024, "rings and partials must fit the LDS");
@@ -498,21 +501,22 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
 
   // four K partials -> LDS, summed in wave order, to C (one split) or the workspace
   __syncthreads();
-  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][ROWS][128]
+  constexpr int PS = W::PS;
+  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][ROWS][PS]
 #pragma unroll
   for (int g = 0; g < MR; ++g)
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) part[(w * ROWS + 16 * g + 4 * fg + v) * NS + 16 * j + fr] = acc[g][j][v];
+      for (int v = 0; v < 4; ++v) part[(w * ROWS + 16 * g + 4 * fg + v) * PS + 16 * j + fr] = acc[g][j][v];
   __syncthreads();
   float* mine = splits > 1 ? partials + (int64_t)(strip * splits + q) * (ROWS * NS) : nullptr;
 #pragma unroll
   for (int e = 0; e < ROWS * NS / 256; ++e) {
     const int idx = tid + 256 * e, row = idx / NS, col = idx % NS;
-    const float sum = ((part[(0 * ROWS + row) * NS + col] + part[(1 * ROWS + row) * NS + col]) +
-                       part[(2 * ROWS + row) * NS + col]) +
-                      part[(3 * ROWS + row) * NS + col];
+    const float sum = ((part[(0 * ROWS + row) * PS + col] + part[(1 * ROWS + row) * PS + col]) +
+                       part[(2 * ROWS + row) * PS + col]) +
+                      part[(3 * ROWS + row) * PS + col];
     if (mine)
       mine[idx] = sum;
     else if (row < M && n0 + col < N)
