@@ -145,7 +145,7 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
   if (sp.splits > 1) {
     const double whole_rounds = std::ceil((tiles - sp.tiles) / 256.0);
     t = whole_rounds * round(k_full) + round(std::ceil((double)p.K / sp.splits / 64.0) * 64.0) +
-        (double)sp.tiles * bm * bn * 4.0 * (2.0 * sp.splits + 1) / 4e12 + 3e-6;
+        (double)sp.tiles * bm * bn * 4.0 * (2.0 * sp.splits + 1) / kSplitTrafficBps + 3e-6;
   } else {
     t = std::ceil(tiles / 256.0) * round(k_full);
   }

@@ -1290,9 +1290,9 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
   // 256x256 tile, no K split: 8192 x 2048 x 2048 +3.1%, 4096^3 +1.3%).  Not where C fits the L2
   // (2048^3 -4.7%, 1024^3 -7.5%), with a K split (3072^3 on 128x256 -8.8%) or for rows of an
   // odd ldc (-9%).
-  const bool wt = T::BM == 256 && T::BN == 256 && splits == 1 && blocks <= 256 * T::OCC &&
-                  (double)p.M * p.N * 4.0 > 32.0 * (1 << 20) && ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0;
-  if constexpr (!GENERIC) {
+  const bool wt = splits == 1 && blocks <= 256 * T::OCC && (double)p.M * p.N * 4.0 > 32.0 * (1 << 20) &&
+                  ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0;
+  if constexpr (!GENERIC && T::BM == 256 && T::BN == 256) {
     if (wt)
       hipLaunchKernelGGL((gemm_nn_kernel<T, false, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
                          tiles_n);
@@ -1301,7 +1301,8 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
                          tiles_n);
   } else {
     (void)wt;
-    hipLaunchKernelGGL((gemm_nn_kernel<T, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m, tiles_n);
+    hipLaunchKernelGGL((gemm_nn_kernel<T, GENERIC>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
+                       tiles_n);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
@@ -1425,11 +1426,13 @@ TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
   if (splits > cap) splits = cap;
   if (splits < 2) return {1, 0};
   // one tile's round at 4.8 TFLOP/s per CU (the 256x256 tile at 8192^3; smaller tiles run
-  // slower, so this underestimates the saving); reduction at 4 TB/s plus 3 us
+  // slower, so this underestimates the saving); reduction traffic at kSplitTrafficBps plus 3 us
   const double round = 2.0 * bm * bn * (kt * 64.0) / 4.8e12;
   const double saved = round * (1.0 - 1.0 / (double)splits);
-  const double cost = (double)last * bm * bn * 4.0 * (2.0 * splits + 1.0) / 4e12 + 3e-6;
-  if (saved <= cost) return {1, 0};
+  const double cost = (double)last * bm * bn * 4.0 * (2.0 * splits + 1.0) / kSplitTrafficBps + 3e-6;
+  // split only with a clear margin: near break-even the estimate's error decides (measured on
+  // MI355X: 6144^2 x 1024 split in two -2%, 6150 x 6144 x 2048 +2.4%)
+  if (saved <= 1.5 * cost) return {1, 0};
   return {(int)splits, (int)last};
 }
 

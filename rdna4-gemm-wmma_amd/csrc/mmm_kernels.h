@@ -38,6 +38,15 @@ struct FoldProblem {
 
 enum TileId { kTile256x256 = 0, kTile128x256 = 1, kTile256x128 = 2, kTile128x128 = 3 };
 
+// Effective rate of a K split's partial-tile traffic (written by the split workgroups, read back
+// with C written by the reduction), as the tile planner prices it.  The partials of an
+// under-filled round (tens of MB) are read back from the 256 MB Infinity Cache: fitted to the
+// measured times of split launches on MI355X (2304^2 x 8192 on 256x256 tiles: 90 us measured).
+#ifndef MMM_SPLIT_TRAFFIC_BPS
+#define MMM_SPLIT_TRAFFIC_BPS 10e12
+#endif
+constexpr double kSplitTrafficBps = MMM_SPLIT_TRAFFIC_BPS;
+
 hipError_t launch_gemm_nn(const GemmProblem& p, int tile_id, hipStream_t stream);
 bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id);  // else the register-staged path
 // K split of a tile launch: the last `tiles` tiles in dispatch order (the last, partly filled
