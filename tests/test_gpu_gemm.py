@@ -420,7 +420,7 @@ def test_exact_persistent(mm, cuda, case):
 # the reduction would cost more than the round it saves)
 TAIL_SPLITS = [((6144, 6144, 2048), ("256x256", 4, 64)), ((3072, 3072, 3072), ("128x256", 6, 32)),
                ((4608, 4608, 8192), ("256x256", 3, 68)), ((7168, 7168, 7168), ("256x256", 14, 16)),
-               ((4357, 4095, 4111), ("256x256", 8, 32)), ((2304, 2304, 8192), ("128x128", 3, 68)),
+               ((4357, 4095, 4111), ("256x256", 8, 32)), ((2304, 2304, 8192), ("256x256", 3, 81)),
                ((6150, 6144, 1030), ("256x256", 1, 0))]
 
 
@@ -444,7 +444,7 @@ def test_exact_tail_split(mm, cuda, case):
 
 # (M, N, K, tile or None) -> K splits of the tile kernel
 TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((65, 4096, 4096, None), 8), ((300, 264, 2048, None), 4),
-               ((100, 200, 1001, None), 2), ((256, 512, 4096, "256x256"), 8), ((256, 512, 2048, "256x128"), 4),
+               ((100, 200, 1001, None), 1), ((256, 512, 4096, "256x256"), 8), ((256, 512, 2048, "256x128"), 4),
                ((200, 300, 3000, "128x256"), 5), ((2000, 2000, 512, None), 1)]
 
 
