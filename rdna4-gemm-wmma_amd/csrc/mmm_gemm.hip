@@ -933,6 +933,183 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
 }
 
 // ------------------------------------------------------------------------------------
+// Persistent grid over whole tiles and the last round's K-split pieces (same conditions as
+// gemm_nn_persistent_kernel, plus a K split of an under-filled last round): the split pieces
+// are the grid's final work items, so each workgroup's whole tiles keep the next-tile overlap
+// and the split pieces follow without a kernel boundary; their partial tiles go to the
+// workspace for reduce_tiles_kernel.  A separate kernel: folding the item bookkeeping into
+// gemm_nn_persistent_kernel changed its register allocation (it spilled).
+// ------------------------------------------------------------------------------------
+template <class T, bool NT>
+__global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_split_kernel(GemmProblem p, int tiles_m, int tiles_n) {
+  __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
+  constexpr int S = T::STAGES;
+  constexpr int NQ = T::MF == 32 ? 4 : 1;       // float4 groups per accumulator
+  constexpr int NST = T::FM * T::FN * NQ;       // C stores per thread per tile
+  const int ntiles = tiles_m * tiles_n;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / T::WGN, wn = w % T::WGN;
+  const int K = p.K;
+  const int64_t lda = p.lda, ldb = p.ldb;
+
+  // staging map and fragment offsets: as gemm_nn_kernel
+  constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
+  static_assert(RPA % T::SWZ_A_ROWS == 0 && RPB % T::SWZ_B_ROWS == 0, "round strides must preserve the swizzle");
+  const int a_row0 = w * (64 / T::CA) + lane / T::CA;
+  const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
+  const int b_row0 = w * (64 / T::CB) + lane / T::CB;
+  const int b_nc = 8 * ((lane % T::CB) ^ T::swz_bk(b_row0));
+  uint32_t a_off[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int kk = 0; kk < T::KSTEPS; ++kk)
+#pragma unroll
+    for (int ph = 0; ph < T::APAR; ++ph) {
+      const int m = wm * T::TM + ph * T::MF + (lane % T::MF);
+      const int chunk = (T::KK / 8) * kk + lane / T::MF;
+      a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
+    }
+  uint32_t b_off[4] = {0, 0, 0, 0};
+  {
+    const int k = 8 * (lane / T::MF) + ((lane >> 2) & 3);
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb) {
+      const int n = T::MF == 32 ? wn * T::TN + 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)
+                                : wn * T::TN + 16 * nb + 4 * (lane & 3);
+      b_off[nb] = k * T::BN * 2 + (((n >> 3) ^ T::swz_bk(k)) * 16) + (n & 7) * 2;
+    }
+  }
+
+  const int KT_all = (K + T::BK - 1) / T::BK;
+  // Work items: whole tiles 0 .. whole-1 of the XCD-aware order over all of K, then (K split)
+  // item whole + q * split_tiles + j = K range q of tile whole + j, as gemm_nn_kernel numbers
+  // its blocks.  Workgroup b takes items b, b + grid, ...: whole tiles first, split pieces last.
+  const int ksplit = p.k_splits > 1 ? p.k_splits : 1;
+  const int whole = ksplit > 1 ? ntiles - p.split_tiles : ntiles;
+  const int nitems = whole + (ksplit > 1 ? p.split_tiles * ksplit : 0);
+  struct Item {
+    int m0, n0, kt0, kt, q, j;  // tile origin, first K tile and K tiles, split index, split tile
+  };
+  auto item_of = [&](int it) {
+    Item r;
+    int bt = it, nsplit = 1;
+    r.q = 0, r.j = 0;
+    if (it >= whole) {
+      const int i2 = it - whole;
+      r.q = i2 / p.split_tiles, r.j = i2 - r.q * p.split_tiles;
+      bt = whole + r.j, nsplit = ksplit;
+    }
+    int tmi, tni;
+    tile_of_block(bt, tiles_m, tiles_n, 4, &tmi, &tni);
+    r.m0 = __builtin_amdgcn_readfirstlane(tmi * T::BM), r.n0 = __builtin_amdgcn_readfirstlane(tni * T::BN);
+    r.kt0 = __builtin_amdgcn_readfirstlane((r.q * KT_all) / nsplit);
+    r.kt = __builtin_amdgcn_readfirstlane(((r.q + 1) * KT_all) / nsplit) - r.kt0;
+    r.q = __builtin_amdgcn_readfirstlane(r.q), r.j = __builtin_amdgcn_readfirstlane(r.j);
+    return r;
+  };
+  char LDS_AS* lds_base = (char LDS_AS*)lds;
+  int a_kc_t = a_kc;  // a_kc for the K-tail test, made opaque per tile like the offset bases
+  uint32_t a_goff = (uint32_t)((a_row0 * lda + a_kc) * 2);
+  uint32_t b_goff = (uint32_t)((b_row0 * ldb + b_nc) * 2);
+  const uint32_t a_rstep = (uint32_t)(RPA * lda * 2), b_rstep = (uint32_t)(RPB * ldb * 2);
+  const int64_t b_step = (int64_t)T::BK * ldb * 2;
+  // per-item running load state (an item's K tiles are prepared in order from its first)
+  const char* a_ptr;
+  const char* b_ptr;
+  int64_t a_left, b_left;
+  int kt0 = 0;  // the item's first K tile
+  auto start_tile = [&](const Item& it) {
+    // The per-lane offset bases pass through an empty asm each tile, so the offsets of a tile's
+    // first loads are recomputed from them rather than kept live across the K loop (which
+    // runs at the register limit).
+    asm volatile("" : "+v"(a_goff), "+v"(b_goff), "+v"(a_kc_t));
+    kt0 = it.kt0;
+    const int64_t k0 = (int64_t)kt0 * T::BK;
+    a_ptr = (const char*)(p.A + (int64_t)it.m0 * lda + k0);
+    b_ptr = (const char*)(p.B + k0 * ldb + it.n0);
+    a_left = ((int64_t)(p.M - 1 - it.m0) * lda + K - k0) * 2;
+    b_left = ((K - 1 - k0) * ldb + p.N - it.n0) * 2;
+  };
+  struct TileDma {
+    i32x4 ra, rb;
+    uint32_t a_dst, b_dst, a_base;
+  };
+  auto prep = [&](int t, int stage) {
+    const int k0 = (kt0 + t) * T::BK;
+    TileDma d;
+    d.ra = make_rsrc(a_ptr, clip_records(a_left));
+    d.rb = make_rsrc(b_ptr, clip_records(b_left));
+    a_ptr += T::BK * 2, a_left -= T::BK * 2;
+    b_ptr += b_step, b_left -= b_step;
+    d.a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
+    d.b_dst = d.a_dst + T::A_BYTES;
+    const uint32_t a_dead = (uint32_t)(K - 1 - (k0 + a_kc_t)) >> 31;
+    d.a_base = a_goff + a_dead * kOobOffset;
+    return d;
+  };
+  auto dma_one = [&](const TileDma& d, int j) {
+    if (j < T::RA)
+      dma_b128(d.a_dst + j * T::NT * 16, d.ra, d.a_base + j * a_rstep);
+    else
+      dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, d.rb, b_goff + (j - T::RA) * b_rstep);
+  };
+  auto issue = [&](int t, int stage) {
+    const TileDma d = prep(t, stage);
+#pragma unroll
+    for (int j = 0; j < T::LPT; ++j) dma_one(d, j);
+  };
+
+  int b = blockIdx.x;
+  Item cur = item_of(b);
+  start_tile(cur);
+#pragma unroll
+  for (int s = 0; s < S; ++s) issue(s, s);
+  int pre = 1;
+  AccT<T> acc[T::FM][T::FN];
+  while (true) {
+#pragma unroll
+    for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < T::FN; ++jj) acc[i][jj] = AccT<T>{};
+    cross_stage<T, false, NST>(lds_base, cur.kt, false, a_off, b_off, acc, prep, dma_one, issue, pre);
+    const int nb = b + (int)gridDim.x;
+    Item nxt = cur;
+    if (nb < nitems) {
+      block_sync();  // every wave has read its last fragments of the ring
+      nxt = item_of(nb);
+      start_tile(nxt);
+#pragma unroll
+      for (int s = 0; s < S; ++s) issue(s, s);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before the stores below
+    }
+    // epilogue: NST 16-byte stores per thread -- an interior tile of C, or a split piece's whole
+    // partial tile, [split tile][split][BM][BN], for reduce_tiles_kernel
+    const bool split_item = b >= whole;  // uniform
+    float* base = split_item ? p.partials + ((int64_t)cur.j * ksplit + cur.q) * (T::BM * T::BN)
+                             : p.C + (int64_t)cur.m0 * p.ldc + cur.n0;
+    const int64_t ld = split_item ? T::BN : p.ldc;
+#pragma unroll
+    for (int mb = 0; mb < T::FM; ++mb) {
+      float* crow = base + (int64_t)(wm * T::TM + T::MF * mb + (lane % T::MF)) * ld + wn * T::TN;
+#pragma unroll
+      for (int nb2 = 0; nb2 < T::FN; ++nb2)
+#pragma unroll
+        for (int qq = 0; qq < NQ; ++qq) {
+          const int n = T::MF == 32 ? 32 * nb2 + 8 * qq + 4 * (lane >> 5) : 16 * nb2 + 4 * (lane >> 4);
+          const f32x4 v = {acc[mb][nb2][4 * qq + 0], acc[mb][nb2][4 * qq + 1], acc[mb][nb2][4 * qq + 2],
+                           acc[mb][nb2][4 * qq + 3]};
+          if constexpr (NT)
+            __builtin_nontemporal_store(v, (f32x4*)(crow + n));
+          else
+            *(f32x4*)(crow + n) = v;
+        }
+    }
+    if (nb >= nitems) break;
+    b = nb, cur = nxt, pre = 2;
+  }
+}
+
+// ------------------------------------------------------------------------------------
 // Folded (5-D contraction) kernel: each GEMM axis is a (hi, lo) pair of sub-indices with
 // its own strides per operand (mmm.h, mmm_contract_desc).  Operands are gathered element by
 // element into the same swizzled LDS stages and multiplied by the same MFMA core; the
@@ -1455,7 +1632,7 @@ size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id) {
 #endif
 static bool persistent_ok(const GemmProblem& p) {
   using TP = DmaTile<256, 256>;
-  if (!dma_ok(p, 256) || p.tail_regs || !p.c_vec4 || p.k_splits > 1) return false;
+  if (!dma_ok(p, 256) || p.tail_regs || !p.c_vec4) return false;
   if (p.M % TP::BM || p.N % TP::BN) return false;
   if ((int64_t)(p.M / TP::BM) * (p.N / TP::BN) <= 256) return false;
   return (p.K + TP::BK - 1) / TP::BK >= TP::STAGES + 1;
@@ -1491,12 +1668,30 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
         // with short K the slower-draining non-temporal stores weigh more (measured on MI355X:
         // 12288^2 x 4096 +6.7%, 8192^3 +1.6-2.8%, 6144^3 -0.6%, 8192^2 x 2048 -7.1%,
         // 16384 x 8192 x 1024 -9.3%).  16-byte-aligned C rows only.
-        if (((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 && p.K >= kNtMinK)
-          hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, p.M / TP::BM,
-                             p.N / TP::BN);
+        const int tiles_m = p.M / TP::BM, tiles_n = p.N / TP::BN;
+        const bool nt = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 && p.K >= kNtMinK;
+        if (p.k_splits <= 1) {
+          if (nt)
+            hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
+                               tiles_n);
+          else
+            hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, false>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
+                               tiles_n);
+          return hipGetLastError();
+        }
+        if (nt)
+          hipLaunchKernelGGL((gemm_nn_persistent_split_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
+                             tiles_n);
         else
-          hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, false>), dim3(256), dim3(TP::NT), 0, stream, p,
-                             p.M / TP::BM, p.N / TP::BN);
+          hipLaunchKernelGGL((gemm_nn_persistent_split_kernel<TP, false>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
+                             tiles_n);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        // the last round's K-split pieces ran as the grid's final items: sum their partials
+        const int64_t tiles = (int64_t)tiles_m * tiles_n;
+        constexpr int64_t per_tile = TP::BM * TP::BN / 4 / 256;  // blocks of 256 float4s per tile
+        hipLaunchKernelGGL((reduce_tiles_kernel<TP::BM, TP::BN>), dim3((unsigned)(p.split_tiles * per_tile)), dim3(256),
+                           0, stream, p, tiles_m, tiles_n, (int)(tiles - p.split_tiles), p.k_splits);
         return hipGetLastError();
       }
       return dma_ok(p, 256) ? launch_nn<DmaTile<256, 256>, false>(p, stream)
