@@ -65,24 +65,6 @@
 #ifndef MMM_PIN_BODY
 #define MMM_PIN_BODY 1  // keep a tile's body MFMAs ahead of the next tile's load wait and barrier
 #endif
-// Read each K-step's fragments in the order the MFMAs consume them (A0, B0 .. B(FN-1), A1 ..)
-// rather than all A fragments first: LDS reads retire in order, so the first MFMAs of a step
-// then wait for 1 + FN reads instead of FM + 1.
-#ifndef MMM_READ_ORDER
-#define MMM_READ_ORDER 0
-#endif
-// Build the steady-state refill's buffer descriptors under the last body K-step's MFMAs
-// instead of between the body's last MFMA and the tile barrier, where they would run while
-// the matrix pipe drains.
-#ifndef MMM_PREP_EARLY
-#define MMM_PREP_EARLY 0
-#endif
-// Steady-state refill loads deferred from the last K-step to the next tile's first body
-// K-step (spread evenly over its MFMAs), so the refill's address traffic is spread over a
-// whole tile instead of one K-step.
-#ifndef MMM_DMA_DEFER
-#define MMM_DMA_DEFER 0
-#endif
 
 namespace mmm {
 
@@ -266,20 +248,12 @@ __device__ __forceinline__ void load_frag_unit(const char LDS_AS* a_st, const ch
   }
 }
 
-// Fragment unit read i-th in a K-step: all A fragments then all B fragments, or (READ_ORDER)
-// in MFMA consumption order A0, B0 .. B(FN-1), A1 .. A(FM-1) (MFMA i uses A i / FN, B i % FN).
-template <class T>
-__device__ __forceinline__ constexpr int read_unit(int i) {
-  if constexpr (!MMM_READ_ORDER) return i;
-  return i == 0 ? 0 : i <= T::FN ? T::FM + i - 1 : i - T::FN;
-}
-
 // All fragment reads of K-step kk from an LDS stage.
 template <class T, bool BKM>
 __device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char LDS_AS* b_st, const uint32_t (&a_off)[4],
                                            const uint32_t (&b_off)[4], int kk, Frags<T>& f) {
 #pragma unroll
-  for (int u = 0; u < T::FM + T::FN; ++u) load_frag_unit<T, BKM>(a_st, b_st, a_off, b_off, kk, read_unit<T>(u), f);
+  for (int u = 0; u < T::FM + T::FN; ++u) load_frag_unit<T, BKM>(a_st, b_st, a_off, b_off, kk, u, f);
 }
 
 // One MFMA of the tile's shape, operands swapped (B fragment as src A): acc holds C^T.
@@ -362,13 +336,7 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
   int cur = 0;
   // K-steps 0 .. KSTEPS-2 of the tile in slot `cur` (each step's MFMAs run while the next
   // step's fragments are read).
-  // `hook` runs once, under the last body step's MFMAs after its fragment reads (MFMA PREP_AT).
-  constexpr int PREP_AT = T::FM + T::FN < T::FM * T::FN ? T::FM + T::FN : T::FM * T::FN - 1;
-  // `defer(q)` issues deferred refill load q (q < NDEF) of the previous tile's refill; it goes on
-  // MFMA q * (FM * FN / NDEF) of the first body step.
-  constexpr int NDEF = (MMM_XINTERLEAVE && MMM_SPREAD_BODY && T::KSTEPS >= 2 && MMM_DMA_DEFER < T::LPT) ? MMM_DMA_DEFER : 0;
-  auto no_defer = [](int) {};
-  auto tile_body = [&](auto&& hook, auto&& defer) {
+  auto tile_body = [&] {
     const char LDS_AS* st = lds_base + cur * T::STAGE;
 #pragma unroll
     for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
@@ -377,12 +345,7 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
 #pragma unroll
         for (int i = 0; i < T::FM * T::FN; ++i) {
           mfma_one<T>(f[kk & 1].b[i % T::FN], f[kk & 1].a[i / T::FN], acc[i / T::FN][i % T::FN]);
-          if (i < T::FM + T::FN)
-            load_frag_unit<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, read_unit<T>(i), f[(kk + 1) & 1]);
-          if (kk + 2 == T::KSTEPS && i == PREP_AT) hook();
-          if constexpr (NDEF > 0)
-            if (kk == 0 && i % (T::FM * T::FN / NDEF) == 0 && i / (T::FM * T::FN / NDEF) < NDEF)
-              defer(i / (T::FM * T::FN / NDEF));
+          if (i < T::FM + T::FN) load_frag_unit<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, i, f[(kk + 1) & 1]);
           __builtin_amdgcn_sched_barrier(0);
         }
       } else {
@@ -391,11 +354,9 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
         // keep the next step's LDS reads ahead of this step's MFMAs
         __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);
-        if (kk + 2 == T::KSTEPS) hook();
       }
     }
   };
-  auto no_hook = [] {};
   // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
   // retired slot (`refill` loads tile t+S into slot `cur`), then the MFMAs.
   auto tile_next = [&](int t, auto&& refill) {
@@ -417,75 +378,52 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
   // neither a burst of LDS reads nor a burst of load issue leaves the matrix pipe idle.
   // MFMA i carries fragment read i (i < FM + FN) when MMM_SPREAD_READS is set, and the DMA
   // loads go on the MFMAs after the reads when there are enough of them.
-  using Dma = decltype(prep(0, 0));
-  auto tile_next_interleaved = [&](int t, const Dma* early, Dma& out) {
+  auto tile_next_interleaved = [&](int t) {
     if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
     wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(S - 2);  // steady state: S-2 tiles after t+1 in flight
     block_sync();
     const int nslot = cur + 1 == S ? 0 : cur + 1;
     const char LDS_AS* ns = lds_base + nslot * T::STAGE;
     constexpr int NM = T::FM * T::FN, NU = MMM_SPREAD_READS ? T::FM + T::FN : 0;
-    constexpr int NL = T::LPT - NDEF;  // loads issued here; the rest go in the next body step
+    constexpr int NL = T::LPT;
     constexpr int DS = MMM_DMA_STRIDE > 0 ? MMM_DMA_STRIDE : (NM / NL > 1 ? NM / NL : 1);  // MFMAs between loads
     constexpr int D0 = NM - DS * NL >= NU ? NU : (NM > DS * NL ? NM - DS * NL : 0);
     if constexpr (!MMM_SPREAD_READS) load_frags<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
-    const Dma d = early ? *early : prep(t + S, cur);
+    const auto d = prep(t + S, cur);
     int issued = 0;
 #pragma unroll
     for (int i = 0; i < NM; ++i) {
       const int mb = i / T::FN, nb = i % T::FN;
       mfma_one<T>(f[1].b[nb], f[1].a[mb], acc[mb][nb]);
-      if (i < NU) load_frag_unit<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, read_unit<T>(i), f[0]);
+      if (i < NU) load_frag_unit<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, i, f[0]);
       if (i >= D0 && (i - D0) % DS == 0 && issued < NL) dma_one(d, issued++);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int j = 0; j < NL; ++j)
       if (j >= issued) dma_one(d, j);
-    out = d;
     cur = nslot;
   };
   // steady state refills by DMA only; the refill of the last tile (possibly gathered
   // through VGPRs) is peeled so the loop carries no gather registers
   int t = 0;
-  Dma pend;                // the last steady-state refill, whose loads NL .. LPT-1 are deferred
-  bool have_pend = false;  // (uniform) the next body step issues them
-  auto deferred = [&](int q) { dma_one(pend, T::LPT - NDEF + q); };
-  // a body step outside the steady state: issues the deferred loads it inherits
-  auto body_tail = [&] {
-    if (NDEF > 0 && have_pend)
-      tile_body(no_hook, deferred);
-    else
-      tile_body(no_hook, no_defer);
-    have_pend = false;
-  };
   for (; t + S < KT - 1; ++t) {
-    if constexpr (MMM_XINTERLEAVE) {
-      Dma d;
-      auto early = [&] { d = prep(t + S, cur); };
-      constexpr bool E = MMM_PREP_EARLY && T::KSTEPS >= 2;
-      if (NDEF > 0 && have_pend) {
-        if constexpr (E) tile_body(early, deferred); else tile_body(no_hook, deferred);
-      } else {
-        if constexpr (E) tile_body(early, no_defer); else tile_body(no_hook, no_defer);
-      }
-      tile_next_interleaved(t, E ? &d : nullptr, pend);
-      have_pend = NDEF > 0;
-    } else {
-      tile_body(no_hook, no_defer);
+    tile_body();
+    if constexpr (MMM_XINTERLEAVE)
+      tile_next_interleaved(t);
+    else
       tile_next(t, [&] { issue(t + S, cur); });
-    }
   }
   if (t + S == KT - 1) {
-    body_tail();
+    tile_body();
     tile_next(t, [&] { issue_tile(t + S, cur); });
     ++t;
   }
   for (; t + 1 < KT; ++t) {
-    body_tail();
+    tile_body();
     tile_next(t, [] {});
   }
-  body_tail();
+  tile_body();
   mfma_frags<T>(f[1], acc);
 }
 
