@@ -19,7 +19,8 @@ Extra objects on the line:
   hipblaslt    -- hipBLASLt on the same inputs and problem (FP16 in, FP32 out).
 
 Other workloads (parity configs, reported with --workload or --report, never the default):
-gemm256, ragged, contraction, skinny.  One GPU only: --gpus above 1 exits with a message.
+gemm256, ragged, contraction, skinny (and skinny_nows, the same problem without a workspace),
+contraction_ref.  One GPU only: --gpus above 1 exits with a message.
 """
 from __future__ import annotations
 
@@ -48,6 +49,8 @@ WORKLOADS = {
     "ragged": (4097, 4095, 4111, "gemm", 2, "uniform"),
     "contraction": (8192, 2048, 2048, "contraction", 3, "normal"),
     "skinny": (16, 8192, 8192, "gemm", 4, "uniform"),
+    # the same problem through the entry point without a workspace (K reduced inside each workgroup)
+    "skinny_nows": (16, 8192, 8192, "gemm", 4, "uniform"),
     # the reference's own contraction (mmmTensor.cpp:20-28): G[r][n][m][l] x Input[b][n][l]
     "contraction_ref": (8192, 8192, 8192, "contraction_ref", 5, "uniform"),
     # known-size reference for the HBM byte counters: a 256 MiB fp32 device-to-device copy
@@ -59,6 +62,7 @@ DESCRIPTIONS = {
     "ragged": "gemm_nn 4097x4095x4111 fp16 row-major, U[-1,1) seed 2",
     "contraction": "contract5d C[b,i,j]=sum_kl A[b,i,k,l] B[k,l,j], b=8 i=1024 k=32 l=64 j=2048, N(0,1)*0.1 seed 3",
     "skinny": "gemm_nn 16x8192x8192 fp16 row-major, U[-1,1) seed 4, 3 rotating B buffers",
+    "skinny_nows": "gemm_nn 16x8192x8192 fp16 row-major without a workspace, U[-1,1) seed 4, 3 rotating B buffers",
     "contraction_ref": "contract5d Out[m][b][r]=sum_nl G[r][n][m][l] In[b][n][l], mt=128 bt=8192 rt=64 nt=64 rt_l=128, "
                        "U[-1,1) seed 5",
     "copy": "copy 256 MiB fp32 device-to-device (counter scaling reference), zeros",
@@ -106,7 +110,8 @@ def make_workload(name, torch, mmm):
         }
     A = torch.empty((M, K), dtype=torch.float16, device=dev)
     fill(A, seed, 0)
-    nb = 3 if name == "skinny" else 1  # rotate B past the 256 MB Infinity Cache
+    nb = 3 if name.startswith("skinny") else 1  # rotate B past the 256 MB Infinity Cache
+    ws = False if name == "skinny_nows" else None
     Bs = []
     for r in range(nb):
         Bt = torch.empty((K, N), dtype=torch.float16, device=dev)
@@ -116,7 +121,7 @@ def make_workload(name, torch, mmm):
     state = {"i": 0}
 
     def launch():
-        mmm.gemm(A, Bs[state["i"] % nb], Cd)
+        mmm.gemm(A, Bs[state["i"] % nb], Cd, workspace=ws)
         state["i"] += 1
 
     def witness():
@@ -223,7 +228,7 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness):
     algo_bytes = W.get("bytes", 2.0 * M * K + 2.0 * K * N + 4.0 * M * N)
     ms, per, wall = time_launches(torch, W["launch"], steps, warmup)
     avg_launch = statistics.fmean(per)
-    hbm = name in ("skinny", "copy")
+    hbm = name in ("skinny", "skinny_nows", "copy")
     with_witness = with_witness and W["witness"] is not None
     with_cpu = with_cpu and W["host_inputs"] is not None
     res = {
@@ -339,7 +344,7 @@ def main() -> int:
 
     if args.report:
         report = []
-        for name in ["gemm8192", "contraction", "ragged", "skinny", "gemm256", "contraction_ref"]:
+        for name in ["gemm8192", "contraction", "ragged", "skinny", "skinny_nows", "gemm256", "contraction_ref"]:
             _log(f"[bench] {name}")
             r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=False,
                              with_witness=not args.no_witness)
@@ -354,7 +359,7 @@ def main() -> int:
     r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=not args.no_cpu,
                      with_witness=not args.no_witness)
     M, N, K = WORKLOADS[name][:3]
-    skinny = name in ("skinny", "copy")
+    skinny = name in ("skinny", "skinny_nows", "copy")
     line = {
         "metric": METRIC if name == "gemm8192" else f"{name} {'GB/s' if skinny else 'TFLOP/s'}",
         "value": round(r["gbs"] if skinny else r["tflops"], 2),

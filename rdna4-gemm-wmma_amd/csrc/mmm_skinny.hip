@@ -110,7 +110,9 @@ __device__ __forceinline__ void stream_columns(const GemmProblem& p, int n0, int
   // DMA map.  A [16][KS]: CA = KS/8 chunks per row; one wave-wide instruction covers
   // 64/CA rows, lane -> row lane/CA (+ 64/CA per instruction), slot chunk lane%CA holding
   // logical chunk (lane%CA) ^ swz(row).  B [KS][NS]: lane -> row lane/CPR (+ 64/CPR per
-  // instruction), chunk lane%CPR (natural layout).
+  // instruction), slot chunk lane%CPR holding logical chunk (lane%CPR) ^ 2*((row >> 3) & 1):
+  // a pass of a 16x16x32 transposing read takes rows k .. k+3 and k+8 .. k+11, and with
+  // 64-byte rows, rows 8 apart sit on the same banks unless their chunk pairs are swapped.
   constexpr int CA = kKS / 8, RPI_A = 64 / CA, NA = kABytes / 1024;
   const int a_row = lane / CA;
   uint32_t a_goff[NA];
@@ -121,7 +123,9 @@ __device__ __forceinline__ void stream_columns(const GemmProblem& p, int n0, int
     a_kc[i] = 8 * ((lane % CA) ^ swz_a(row));
     a_goff[i] = (uint32_t)((row * lda + a_kc[i]) * 2);
   }
-  const uint32_t b_goff = (uint32_t)(((lane / kCPR) * ldb + 8 * (lane % kCPR)) * 2);
+  static_assert(kCPR == 4 && (64 / kCPR) % 16 == 0, "the B swizzle's row bit 3 is fixed per lane across loads");
+  const int b_sw = 2 * (((lane / kCPR) >> 3) & 1);  // rows of load i: lane/CPR + 16i, same bit 3
+  const uint32_t b_goff = (uint32_t)(((lane / kCPR) * ldb + 8 * ((lane % kCPR) ^ b_sw)) * 2);
   const uint32_t b_rstep = (uint32_t)((64 / kCPR) * ldb * 2);
   const i32x4 rb_full = make_rsrc(p.B + n0, clip_records(((int64_t)(K - 1) * ldb + N - n0) * 2));
 
@@ -163,7 +167,7 @@ __device__ __forceinline__ void stream_columns(const GemmProblem& p, int n0, int
     }
 #pragma unroll
     for (int i = 0; i < kBBytes / 1024; ++i) {
-      const int k = k0 + i * (64 / kCPR) + lane / kCPR, n = n0 + 8 * (lane % kCPR);
+      const int k = k0 + i * (64 / kCPR) + lane / kCPR, n = n0 + 8 * ((lane % kCPR) ^ b_sw);
       half8 v = {};
       if (k < K) {
 #pragma unroll
@@ -187,7 +191,10 @@ __device__ __forceinline__ void stream_columns(const GemmProblem& p, int n0, int
   uint32_t a_off[KQ];
 #pragma unroll
   for (int q = 0; q < KQ; ++q) a_off[q] = fr * (kKS * 2) + (((4 * q + fg) ^ swz_a(fr)) * 16);
+  // B rows 8fg + (fr >> 2) (+4, +32q): row bit 3 = fg & 1, which swaps the two 16-column tiles'
+  // chunk pairs
   const uint32_t b_off = kABytes + (8 * fg + (fr >> 2)) * (kNS * 2) + 4 * (fr & 3) * 2;
+  const int b_js = fg & 1;
 
   auto compute = [&](int slot) {
     const char LDS_AS* sl = ring + slot * kSlot;
@@ -196,7 +203,7 @@ __device__ __forceinline__ void stream_columns(const GemmProblem& p, int n0, int
       const half8 af = *(const half8 LDS_AS*)(sl + a_off[q]);
 #pragma unroll
       for (int j = 0; j < kNT; ++j) {
-        const char LDS_AS* bp = sl + b_off + (32 * q) * (kNS * 2) + 16 * j * 2;
+        const char LDS_AS* bp = sl + b_off + (32 * q) * (kNS * 2) + 16 * (j ^ b_js) * 2;
         fp16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)bp);
         fp16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((fp16x4 LDS_AS*)(bp + 4 * kNS * 2));
         const half8 bf = __builtin_shufflevector(__builtin_bit_cast(half4, lo), __builtin_bit_cast(half4, hi), 0, 1,

@@ -242,6 +242,20 @@ def test_exact_skinny_unaligned(mm, cuda, shape):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
+@pytest.mark.parametrize("shape", [(16, 8192, 8192), (3, 1001, 777), (16, 4095, 4111), (9, 130, 2050),
+                                   (1, 4095, 4111), (16, 96, 64), (5, 33, 8)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_exact_skinny_no_workspace(mm, cuda, shape):
+    """M <= 16 without a workspace: one workgroup streams its column strip over all of K and
+    reduces its waves' K ranges in LDS (aligned, odd N and K, gathered last slot)."""
+    M, N, K = shape
+    A, B, truth = _exact_case(np.random.default_rng(M * 7 + N + 3 * K), M, N, K)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd, workspace=False)
+    C = Cd.cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
 @pytest.mark.parametrize("shape", [(16 * 256 + 1, 4096, 264), (16 * 256 + 40, 4096, 264), (16 * 256 + 64, 4096, 1000),
                                    (16 * 256 + 17, 4095, 523)],
                          ids=lambda s: "x".join(map(str, s)))
