@@ -222,10 +222,8 @@ def gemm(A, B, C_out=None, tile=None, stream=None, workspace=None):
     st = _stream(stream)
     L = lib()
     if tile is None:
-        need = C.c_size_t(0)
-        _check("mmm_gemm_workspace_f16f32",
-               L.mmm_gemm_workspace_f16f32(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, C.byref(need)))
-        wp, wb = _ws_args(workspace, A.device, st, need.value)
+        # one library call: the per-stream workspace holds the largest split the library plans
+        wp, wb = _ws_args(workspace, A.device, st, MAX_WORKSPACE_BYTES)
         _check("mmm_gemm_f16f32_ws",
                L.mmm_gemm_f16f32_ws(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, wp, wb, st))
     else:
@@ -334,10 +332,7 @@ def contract(desc: ContractDesc, A, B, C_out, stream=None, workspace=None):
         raise TypeError("C must be a CUDA float32 tensor")
     st = _stream(stream)
     L = lib()
-    need = C.c_size_t(0)
-    _check("mmm_contract5d_workspace_f16f32",
-           L.mmm_contract5d_workspace_f16f32(C.byref(desc), _ptr(A), _ptr(B), _ptr(C_out), C.byref(need)))
-    wp, wb = _ws_args(workspace, A.device, st, need.value)
+    wp, wb = _ws_args(workspace, A.device, st, MAX_WORKSPACE_BYTES)
     _check("mmm_contract5d_f16f32_ws",
            L.mmm_contract5d_f16f32_ws(C.byref(desc), _ptr(A), _ptr(B), _ptr(C_out), wp, wb, st))
     return C_out
