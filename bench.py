@@ -314,7 +314,8 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=100,
+                    help="untimed launches first (the clock ramps up over the first ~50 ms of load)")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="gemm8192")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-witness", action="store_true", help="skip the hipBLASLt comparison")
