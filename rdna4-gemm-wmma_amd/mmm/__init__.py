@@ -234,6 +234,60 @@ def gemm(A, B, C_out=None, tile=None, stream=None, workspace=None):
     return C_out
 
 
+def _ws_tensor(workspace, device, st):
+    """The workspace tensor a bound launcher keeps alive: the caller's, the per-stream one, or None."""
+    if workspace is False:
+        return None
+    return workspace if workspace is not None else _workspace(device, st, MAX_WORKSPACE_BYTES)
+
+
+def _bound(fn, name: str, args: tuple, keep: tuple):
+    def launch():
+        rc = fn(*args)
+        if rc != HIP_SUCCESS:
+            raise MMMError(name, rc)
+
+    launch.tensors = keep  # the launcher holds its operands (and workspace) alive
+    return launch
+
+
+def bind_gemm(A, B, C_out, stream=None, workspace=None):
+    """A zero-argument launcher of C = A @ B on fixed tensors and a fixed stream.
+
+    gemm()'s checks run once, here; each call of the result is one mmm_gemm_f16f32_ws call with
+    prebuilt arguments, for loops that launch one problem many times (a benchmark, a serving
+    step).  ``workspace`` as for gemm.  The tensors must keep their storage while it is used."""
+    import torch
+
+    if C_out is None or C_out.dtype != torch.float32:
+        raise ValueError("C must be a row-major float32 [M,N] tensor")
+    M, N, K, lda, ldb, ldc = _gemm_shapes(A, B, C_out)
+    st = _stream(stream)
+    ws = _ws_tensor(workspace, A.device, st)
+    wp = C.c_void_p(ws.data_ptr()) if ws is not None else None
+    wb = ws.numel() * ws.element_size() if ws is not None else 0
+    args = (_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, wp, wb, st)
+    return _bound(lib().mmm_gemm_f16f32_ws, "mmm_gemm_f16f32_ws", args, (A, B, C_out, ws))
+
+
+def bind_contract(desc: "ContractDesc", A, B, C_out, stream=None, workspace=None):
+    """A zero-argument launcher of contract(desc, A, B, C_out) on fixed tensors and stream: one
+    mmm_contract5d_f16f32_ws call per launch (the library validates the descriptor each call)."""
+    import torch
+
+    _check_f16("A", A)
+    _check_f16("B", B)
+    if C_out.dtype != torch.float32 or not C_out.is_cuda:
+        raise TypeError("C must be a CUDA float32 tensor")
+    st = _stream(stream)
+    d = ContractDesc.from_buffer_copy(desc)
+    ws = _ws_tensor(workspace, A.device, st)
+    wp = C.c_void_p(ws.data_ptr()) if ws is not None else None
+    wb = ws.numel() * ws.element_size() if ws is not None else 0
+    args = (C.pointer(d), _ptr(A), _ptr(B), _ptr(C_out), wp, wb, st)
+    return _bound(lib().mmm_contract5d_f16f32_ws, "mmm_contract5d_f16f32_ws", args, (A, B, C_out, ws, d))
+
+
 KERNELS = {0: "none", 1: "zero", 2: "tile", 3: "stream", 4: "tile+stream"}
 
 

@@ -753,3 +753,52 @@ def test_fill_normal_matches_oracle(mm, cuda, orc):
     if diff.any():
         ulps = np.abs(got[diff].view(np.uint16).astype(np.int32) - ref[diff].view(np.uint16).astype(np.int32))
         assert ulps.max() <= 1
+
+
+# ------------------------------------------------------------------------------ bound launchers
+@pytest.mark.parametrize("shape,ws", [((16, 8192, 2048), None), ((16, 4095, 4111), False), ((300, 264, 2048), None),
+                                      ((1024, 1024, 1024), None)],
+                         ids=["skinny-split", "skinny-no-workspace", "tile-split", "tile"])
+def test_bind_gemm(mm, cuda, shape, ws):
+    """mmm.bind_gemm: the launcher bound once gives gemm()'s exact result on every call, and sees
+    new contents of its operands (it binds storage, not values)."""
+    M, N, K = shape
+    rng = np.random.default_rng(M + N + K + 5)
+    A, B, truth = _exact_case(rng, M, N, K)
+    Ad, Bd = to_dev(cuda, A), to_dev(cuda, B)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    launch = mm.bind_gemm(Ad, Bd, Cd, workspace=ws)
+    for _ in range(2):
+        Cd.fill_(float("nan"))
+        launch()
+        assert np.array_equal(Cd.cpu().numpy(), truth)
+    Ad.neg_()
+    launch()
+    assert np.array_equal(Cd.cpu().numpy(), -truth)
+
+
+def test_bind_contract(mm, cuda, orc):
+    """mmm.bind_contract on the baseline fold and the reference layout: exact, repeatable."""
+    b, i, k, l, j = 2, 33, 3, 40, 70
+    rng = np.random.default_rng(22)
+    A = rng.integers(-4, 5, size=(b, i, k, l)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(k, l, j)).astype(np.float16)
+    truth = np.einsum("bikl,klj->bij", A.astype(np.int64), B.astype(np.int64)).astype(np.float32)
+    C = cuda.full((b, i, j), float("nan"), dtype=cuda.float32, device="cuda")
+    launch = mm.bind_contract(mm.contract_desc_baseline(b, i, k, l, j), to_dev(cuda, A), to_dev(cuda, B), C)
+    for _ in range(2):
+        C.fill_(float("nan"))
+        launch()
+        assert np.array_equal(C.cpu().numpy(), truth)
+    mt, bt, rt, nt, rt_l = 8, 300, 64, 3, 128
+    G = rng.integers(-4, 5, size=(rt, nt, mt, rt_l)).astype(np.float16)
+    In = rng.integers(-4, 5, size=(bt, nt, rt_l)).astype(np.float16)
+    truth = np.einsum("rnml,bnl->mbr", G.astype(np.int64), In.astype(np.int64)).astype(np.float32)
+    Out = cuda.full((mt, bt, rt), float("nan"), dtype=cuda.float32, device="cuda")
+    desc = mm.contract_desc_reference(mt, bt, rt, nt, rt_l)
+    launch = mm.bind_contract(desc, to_dev(cuda, G), to_dev(cuda, In), Out)
+    del desc  # the launcher holds its own copy of the descriptor
+    for _ in range(2):
+        Out.fill_(float("nan"))
+        launch()
+        assert np.array_equal(Out.cpu().numpy(), truth)
