@@ -552,6 +552,15 @@ static int stream_mr(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 static StreamShape stream_shape(const GemmProblem& p) {
   const int mr = stream_mr(p.M);
   const int strips = (p.N + 127) / 128;
+  // M <= 16 on B rows that are not 16-byte aligned: the split kernel's 256-byte row pieces load
+  // misaligned and its reduction is a second dependent launch.  The wave-split kernel ran
+  // 1 x 4095 x 4111 in 14.6 us against 19.8 (split kernel + reduction), 2 x 4095 x 4111 in 15.0
+  // against 19.8; on aligned rows the two tie at that size and the split kernel leads on larger
+  // B (16 x 8192^2: 32.7 against 39.8 us).  Taken when its 32-column strips fill at least half
+  // the chip and B is at most 64 MiB.
+  const bool b_unaligned = ((uintptr_t)p.B & 15) || p.ldb % 8;
+  if (mr == 1 && b_unaligned && (p.N + kNS - 1) / kNS >= 128 && (int64_t)p.K * p.ldb * 2 <= ((int64_t)64 << 20))
+    return {mr, strips, 0};
   const int nst_all = (p.K + 63) / 64;  // 64-deep K steps
   int splits = 256 / strips;
   splits = splits < kMaxSplits ? splits : kMaxSplits;

@@ -282,7 +282,7 @@ def _exact_case(rng, M, N, K):
 
 # (M, N, K) -> K ranges the streaming kernel reduces across workgroups (0: within one workgroup)
 STREAM_SPLITS = [((16, 8192, 8192), 4), ((7, 16384, 4096), 2), ((16, 4096, 8192), 8), ((5, 1024, 8192), 16),
-                 ((16, 32768, 512), 1), ((3, 2000, 4000), 15), ((16, 4095, 4111), 8), ((1, 130, 9000), 16),
+                 ((16, 32768, 512), 1), ((3, 2000, 4000), 15), ((16, 4095, 4111), 0), ((16, 6001, 4111), 0), ((16, 8191, 4111), 4), ((16, 2047, 4111), 16), ((1, 130, 9000), 16),
                  ((16, 8192, 256), 0), ((2, 264, 200), 0)]
 
 

@@ -194,7 +194,9 @@ def test_gemm_plan(mm):
     assert p["direct_to_lds"] == 1 and p["tile_workgroups"] == 32 * 32 and p["stream_rows"] == 0
     p = mm.gemm_plan(4097, 4095, 4111)  # one row past 16 tile rows: that row streams
     assert p["kernel"] == "tile+stream" and p["tile_rows"] == 4096 and p["stream_rows"] == 1
-    # 32 strips of 128 columns, K split 8 ways across workgroups
+    # B rows 2-byte aligned: 128 strips of 32 columns, K reduced inside each workgroup
+    assert p["stream_workgroups"] == 128 and p["stream_splits"] == 0
+    p = mm.gemm_plan(4097, 4096, 4112)  # aligned rows: 32 strips of 128 columns, K split 8 ways
     assert p["stream_workgroups"] == 32 * 8 and p["stream_splits"] == 8
     p = mm.gemm_plan(16, 8192, 8192)
     assert p["kernel"] == "stream" and p["stream_rows"] == 16 and p["tile_workgroups"] == 0
