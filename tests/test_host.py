@@ -198,6 +198,12 @@ def test_gemm_plan(mm):
     assert p["stream_workgroups"] == 128 and p["stream_splits"] == 0
     p = mm.gemm_plan(4097, 4096, 4112)  # aligned rows: 32 strips of 128 columns, K split 8 ways
     assert p["stream_workgroups"] == 32 * 8 and p["stream_splits"] == 8
+    # the in-workgroup kernel's bounds for M <= 16: B rows not 16-byte aligned, at least 128
+    # strips of 32 columns (N >= 4065), B at most 64 MiB; otherwise the split kernel
+    for (M, N, K, ldb), splits in [((16, 4065, 4111, None), 0), ((16, 4063, 4111, None), 8),
+                                   ((16, 4095, 8193, None), 0), ((16, 4095, 8200, None), 8),
+                                   ((16, 4095, 4111, 4096), 8), ((17, 4095, 4111, None), 8)]:
+        assert mm.gemm_plan(M, N, K, ldb=ldb)["stream_splits"] == splits, (M, N, K, ldb)
     p = mm.gemm_plan(16, 8192, 8192)
     assert p["kernel"] == "stream" and p["stream_rows"] == 16 and p["tile_workgroups"] == 0
     assert p["stream_splits"] == 4 and p["stream_workgroups"] == 64 * 4
