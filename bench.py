@@ -55,6 +55,11 @@ WORKLOADS = {
     "contraction_ref": (8192, 8192, 8192, "contraction_ref", 5, "uniform"),
     # known-size reference for the HBM byte counters: a 256 MiB fp32 device-to-device copy
     "copy": (8192, 8192, 1, "copy", 0, "uniform"),
+    # measured ceilings (library probes): the 8192^3 tile kernel's MFMA stream with register-
+    # resident operands, and streaming reads of 1 GiB (plain loads / direct to LDS)
+    "mfma_ceiling": (8192, 8192, 8192, "mfma_ceiling", 1, "uniform"),
+    "read_ceiling": (1 << 30, 1, 1, "read", 0, "uniform"),
+    "read_ceiling_lds": (1 << 30, 1, 1, "read_lds", 0, "uniform"),
 }
 DESCRIPTIONS = {
     "gemm256": "gemm_nn 256x256x256 fp16 row-major, U[-1,1) seed 0",
@@ -66,6 +71,10 @@ DESCRIPTIONS = {
     "contraction_ref": "contract5d Out[m][b][r]=sum_nl G[r][n][m][l] In[b][n][l], mt=128 bt=8192 rt=64 nt=64 rt_l=128, "
                        "U[-1,1) seed 5",
     "copy": "copy 256 MiB fp32 device-to-device (counter scaling reference), zeros",
+    "mfma_ceiling": "MFMA ceiling probe: the 8192x8192x8192 persistent tile kernel's MFMA stream and C stores with "
+                    "register-resident operands (no loads, LDS or barriers), U[-1,1) seed 1",
+    "read_ceiling": "HBM read ceiling probe: one pass over 1 GiB with 16-byte loads into registers, zeros",
+    "read_ceiling_lds": "HBM read ceiling probe: one pass over 1 GiB with direct-to-LDS 16-byte loads, zeros",
 }
 
 
@@ -83,6 +92,20 @@ def make_workload(name, torch, mmm):
         dst = torch.empty_like(src)
         return {"launch": lambda: dst.copy_(src), "witness": None, "host_inputs": None, "M": M, "N": N, "K": K,
                 "bytes": 2.0 * src.numel() * 4}
+    if kind in ("read", "read_lds"):
+        src = torch.zeros(M, dtype=torch.uint8, device=dev)
+        out = torch.empty(2048 * 256, dtype=torch.int32, device=dev)
+        lds = kind == "read_lds"
+        return {"launch": lambda: mmm.probe_read(src, out, direct_to_lds=lds), "witness": None, "host_inputs": None,
+                "M": M, "N": N, "K": K, "bytes": float(M)}
+    if kind == "mfma_ceiling":
+        A = torch.empty((M, K), dtype=torch.float16, device=dev)
+        B = torch.empty((K, N), dtype=torch.float16, device=dev)
+        fill(A, seed, 0)
+        fill(B, seed, 1)
+        Cd = torch.empty((M, N), dtype=torch.float32, device=dev)
+        return {"launch": lambda: mmm.probe_mfma_ceiling(A, B, Cd), "witness": None, "host_inputs": None,
+                "M": M, "N": N, "K": K}
     if kind == "contraction_ref":
         mt, bt, rt, nt, rt_l = 128, 8192, 64, 64, 128
         G = torch.empty((rt, nt, mt, rt_l), dtype=torch.float16, device=dev)
@@ -104,7 +127,7 @@ def make_workload(name, torch, mmm):
         A2, B2, C2 = A.view(M, K), B.view(K, N), Cd.view(M, N)
         return {
             "launch": mmm.bind_contract(desc, A, B, Cd),
-            "witness": lambda: mmm.witness_hipblaslt(A2, B2, C2),
+            "witness": lambda: mmm.bind_witness_hipblaslt(A2, B2, C2),
             "host_inputs": lambda: (A2.cpu().numpy(), B2.cpu().numpy()),
             "M": M, "N": N, "K": K,
         }
@@ -127,18 +150,27 @@ def make_workload(name, torch, mmm):
         state["i"] += 1
 
     def witness():
-        mmm.witness_hipblaslt(A, Bs[state["i"] % nb], Cd)
-        state["i"] += 1
+        # hipBLASLt planned once per B buffer (descriptors, layouts, heuristic), one matmul per launch
+        wb = [mmm.bind_witness_hipblaslt(A, Bt, Cd) for Bt in Bs]
+        wstate = {"i": 0}
+
+        def run():
+            wb[wstate["i"] % nb]()
+            wstate["i"] += 1
+
+        return run
 
     return {"launch": launch, "witness": witness, "host_inputs": lambda: (A.cpu().numpy(), Bs[0].cpu().numpy()),
             "M": M, "N": N, "K": K}
 
 
-def time_launches(torch, fn, steps: int, warmup: int):
+def time_launches(torch, fn, steps: int, warmup: int, clock=None):
     """W untimed launches, then exactly `steps` launches between synchronizations.
 
     Returns (ms per step over the whole timed region, list of per-launch ms from HIP events
-    recorded on the launch stream, wall seconds)."""
+    recorded on the launch stream, wall seconds).  With `clock` (the mmm module), the library's
+    shader-clock probe runs on the same stream right before the first and right after the last
+    timed launch, outside the timed events; its readings (MHz) are in time_launches.clocks."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -147,19 +179,54 @@ def time_launches(torch, fn, steps: int, warmup: int):
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t_begin = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
+    probes = None
+    if clock is not None:
+        probes = torch.zeros(4, dtype=torch.int64, device="cuda")
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
+    if probes is not None:
+        clock.probe_clock(probes[0:2], CLOCK_PROBE_TICKS)
     t_begin.record(stream)
     for s in range(steps):
         starts[s].record(stream)
         fn()
         ends[s].record(stream)
     t_end.record(stream)
+    if probes is not None:
+        clock.probe_clock(probes[2:4], CLOCK_PROBE_TICKS)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_begin.elapsed_time(t_end)
     per = [starts[s].elapsed_time(ends[s]) for s in range(steps)]
+    time_launches.clocks = None
+    if probes is not None:
+        h = probes.cpu()
+        time_launches.clocks = (clock.clock_mhz(h[0:2]), clock.clock_mhz(h[2:4]))
     return total_ms / steps, per, wall
+
+
+# Shader-clock probe length: 20 us of the 100 MHz real-time counter (short against the power
+# controller's reaction time, so it reads the clock the preceding kernels ran at).
+CLOCK_PROBE_TICKS = 2000
+
+
+def smi_snapshot():
+    """The SMU's own readings (amdsmi gpu_metrics: current gfx clock per XCD, socket power);
+    refreshed about once a second, so they describe the last second, not one launch."""
+    try:
+        import amdsmi
+
+        amdsmi.amdsmi_init()
+        try:
+            h = amdsmi.amdsmi_get_processor_handles()[0]
+            m = amdsmi.amdsmi_get_gpu_metrics_info(h)
+            return {"gfxclk_mhz": m.get("current_gfxclk"), "gfxclk_mhz_per_xcd": m.get("current_gfxclks"),
+                    "socket_power_w": m.get("current_socket_power"),
+                    "power_limit_w": amdsmi.amdsmi_get_power_info(h).get("power_limit", 0) / 1e6}
+        finally:
+            amdsmi.amdsmi_shut_down()
+    except Exception as e:  # informational only
+        return {"error": repr(e)[:200]}
 
 
 def read_traffic(workload: str):
@@ -223,14 +290,15 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness):
+def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_ceiling=False):
     W = make_workload(name, torch, mmm)
     M, N, K = W["M"], W["N"], W["K"]
     flops = 2.0 * M * N * K
     algo_bytes = W.get("bytes", 2.0 * M * K + 2.0 * K * N + 4.0 * M * N)
-    ms, per, wall = time_launches(torch, W["launch"], steps, warmup)
+    ms, per, wall = time_launches(torch, W["launch"], steps, warmup, clock=mmm)
+    clocks = time_launches.clocks
     avg_launch = statistics.fmean(per)
-    hbm = name in ("skinny", "skinny_nows", "copy")
+    hbm = name in ("skinny", "skinny_nows", "copy", "read_ceiling", "read_ceiling_lds")
     with_witness = with_witness and W["witness"] is not None
     with_cpu = with_cpu and W["host_inputs"] is not None
     res = {
@@ -238,9 +306,14 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness):
         "ms_per_step": ms,
         "tflops": flops / (ms * 1e-3) / 1e12,
         "gbs": algo_bytes / (ms * 1e-3) / 1e9,
-        "launch_ms": {"avg": avg_launch, "min": min(per), "median": statistics.median(per)},
+        "launch_ms": {"avg": avg_launch, "min": min(per), "median": statistics.median(per),
+                      "first": per[0], "last": per[-1]},
         "wall_s": wall,
     }
+    sclk = statistics.fmean(clocks)
+    res["clock"] = {"sclk_mhz": round(sclk, 1), "before": round(clocks[0], 1), "after": round(clocks[1], 1),
+                    "method": "s_memtime / s_memrealtime probe kernel (20 us) on the launch stream right before "
+                              "the first and right after the last timed launch; sclk_mhz is their mean"}
     if hbm:
         achieved = algo_bytes / (avg_launch * 1e-3) / 1e9
         res["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
@@ -249,13 +322,30 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness):
         achieved = flops / (avg_launch * 1e-3) / 1e12
         res["roofline"] = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                            "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(name)}
+        # dense FP16 peak at the measured clock: 256 CU x 4096 flop per clock
+        peak_clk = 256 * 4096 * sclk * 1e6 / 1e12
+        res["pct_peak_at_clock"] = round(100.0 * res["tflops"] / peak_clk, 2)
+    res["smi"] = smi_snapshot()
     if with_witness:
         try:
-            wms, wper, _ = time_launches(torch, W["witness"], steps, warmup)
+            wms, wper, _ = time_launches(torch, W["witness"](), steps, warmup, clock=mmm)
             res["hipblaslt"] = {"ms_per_step": wms, "tflops": flops / (wms * 1e-3) / 1e12,
-                                "gbs": algo_bytes / (wms * 1e-3) / 1e9}
+                                "gbs": algo_bytes / (wms * 1e-3) / 1e9,
+                                "launch_ms_median": statistics.median(wper),
+                                "sclk_mhz": round(statistics.fmean(time_launches.clocks), 1)}
         except Exception as e:  # the comparison point must not hide the measurement
             res["hipblaslt"] = {"error": str(e)}
+    if with_ceiling:
+        # the same step count on the library's MFMA-ceiling probe (this workload's MFMA stream
+        # with register-resident operands), measured live in this process
+        C = make_workload("mfma_ceiling", torch, mmm)
+        cms, cper, _ = time_launches(torch, C["launch"], steps, warmup, clock=mmm)
+        ctf = flops / (cms * 1e-3) / 1e12
+        res["ceiling"] = {"mfma_tflops": round(ctf, 1), "sclk_mhz": round(statistics.fmean(time_launches.clocks), 1),
+                          "frac": round(res["tflops"] / ctf, 4),
+                          "what": "mmm_probe_mfma_ceiling: the same grid's MFMA stream and C stores without "
+                                  "operand loads, LDS or barriers; frac = value / mfma_tflops"}
+        del C
     if with_cpu:
         res["cpu_baseline"] = cpu_baseline(W)
     return res
@@ -293,13 +383,14 @@ def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool
         pick = plan["kernel"] if plan["kernel"] != "tile" else f"{plan['block_m']}x{plan['block_n']}"
         if plan["kernel"] == "tile+stream":
             pick = f"{plan['block_m']}x{plan['block_n']} + stream {plan['stream_rows']}"
-        auto = tf(lambda: mmm.gemm(A, B, Cm))
-        per_tile = {t: tf(lambda t=t: mmm.gemm(A, B, Cm, tile=t)) for t in tiles}
+        # every launcher bound once (checks, marshalling and hipBLASLt's planning outside the timing)
+        auto = tf(mmm.bind_gemm(A, B, Cm))
+        per_tile = {t: tf(mmm.bind_gemm(A, B, Cm, tile=t)) for t in tiles}
         best = max(per_tile, key=per_tile.get)
         wit = float("nan")
         if with_witness:
             try:
-                wit = tf(lambda: mmm.witness_hipblaslt(A, B, Cm))
+                wit = tf(mmm.bind_witness_hipblaslt(A, B, Cm))
             except Exception as e:  # witness library absent or hipBLASLt refused the shape
                 _log(f"[sweep] hipBLASLt unavailable for {M}x{N}x{K}: {e}")
         row = (f"| {M} x {N} x {K} | {pick} | {auto:.1f} | " + " | ".join(f"{per_tile[t]:.1f}" for t in tiles) +
@@ -321,6 +412,7 @@ def main() -> int:
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="gemm8192")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-witness", action="store_true", help="skip the hipBLASLt comparison")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the live MFMA-ceiling probe (gemm8192 only)")
     ap.add_argument("--report", metavar="PATH", help="measure every workload and write a JSON report to PATH")
     ap.add_argument("--sweep", metavar="PATH", help="time every tile against the library's pick over a shape "
                                                      "grid and write a markdown table to PATH")
@@ -360,9 +452,9 @@ def main() -> int:
 
     name = args.workload
     r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=not args.no_cpu,
-                     with_witness=not args.no_witness)
+                     with_witness=not args.no_witness, with_ceiling=name == "gemm8192" and not args.no_ceiling)
     M, N, K = WORKLOADS[name][:3]
-    skinny = name in ("skinny", "skinny_nows", "copy")
+    skinny = name in ("skinny", "skinny_nows", "copy", "read_ceiling", "read_ceiling_lds")
     line = {
         "metric": METRIC if name == "gemm8192" else f"{name} {'GB/s' if skinny else 'TFLOP/s'}",
         "value": round(r["gbs"] if skinny else r["tflops"], 2),
@@ -380,7 +472,13 @@ def main() -> int:
         "pct_peak": round(100.0 * r["tflops"] / PEAK_TFLOPS, 2),
         "launch_ms": {k: round(v, 5) for k, v in r["launch_ms"].items()},
         "roofline": r["roofline"],
+        "clock": r["clock"],
     }
+    if "pct_peak_at_clock" in r:
+        line["pct_peak_at_clock"] = r["pct_peak_at_clock"]
+    if "ceiling" in r:
+        line["ceiling"] = r["ceiling"]
+    line["smi"] = r["smi"]
     if "cpu_baseline" in r:
         line["cpu_baseline"] = r["cpu_baseline"]
     if "hipblaslt" in r:

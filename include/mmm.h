@@ -219,6 +219,33 @@ hipError_t mmm_fill_normal_f16(mmm_half* out, int64_t n, uint64_t seed, uint32_t
  */
 hipError_t mmm_tile_of_block(int block, int tiles_m, int tiles_n, int* tm, int* tn);
 
+/*
+ * Measurement probes.  No reference counterpart: the reference reports only milliseconds and
+ * GFLOPS (mmm.cpp:1503-1504; mmmTensor.cpp:434-436).  They give the kernels' roofline
+ * fractions a measured denominator beside the published peaks, since the MI355X clock falls
+ * under sustained matrix-core load (power limit).
+ *
+ * mmm_probe_clock: one wave spins for `ticks` ticks (1 .. 10^7) of the constant 100 MHz
+ *   real-time counter and writes out[0] = shader-clock cycles elapsed, out[1] = real-time
+ *   ticks elapsed (shader clock = out[0] / out[1] * 100 MHz).
+ * mmm_probe_mfma_ceiling: the persistent 256x256 tile kernel's MFMA stream (256 workgroups x
+ *   8 waves, 8 x 4 v_mfma_f32_16x16x32_f16 per wave per 32-deep K-step, over every tile and all
+ *   of K: 2*M*N*K flops) with the operands held in registers -- no operand loads, LDS or
+ *   barriers.  A [M][K] and B [K][N] are contiguous row-major inputs whose first K-steps supply
+ *   the fragments; store_tiles != 0 writes each tile's accumulators to C [M][N] as the tile
+ *   kernel does, store_tiles == 0 writes one float per thread into C's first 256 * 512 floats.
+ *   The values written are not A*B.  M, N multiples of 256, K of 64.
+ * mmm_probe_read: streams `bytes` (a multiple of 1024, 16-byte-aligned src) once: with plain
+ *   16-byte loads into registers (direct_to_lds == 0; out receives 2048 * 256 words), or with
+ *   the tile kernels' direct-to-LDS loads (direct_to_lds != 0, bytes < 2^31; out receives 2048
+ *   words).
+ */
+hipError_t mmm_probe_clock(uint64_t* out, int64_t ticks, hipStream_t stream);
+hipError_t mmm_probe_mfma_ceiling(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
+                                  int store_tiles, hipStream_t stream);
+hipError_t mmm_probe_read(const void* src, int64_t bytes, int direct_to_lds, uint32_t* out, int64_t out_words,
+                          hipStream_t stream);
+
 /* Library version string. */
 const char* mmm_version(void);
 

@@ -241,8 +241,12 @@ static bool collapse(int64_t ext_hi, int64_t ext_lo, int64_t s_hi, int64_t s_lo,
 static hipError_t fold_from_desc(const mmm_contract_desc* d, const mmm_half* A, const mmm_half* B, float* C,
                                  FoldProblem* out) {
   if (!d) return hipErrorInvalidValue;
+  // every extent fits int32 before any product is formed (a product of two caller extents could
+  // otherwise overflow int64 and wrap to a small or zero size)
   for (int q = 0; q < 2; ++q)
-    if (d->m_ext[q] < 0 || d->n_ext[q] < 0 || d->k_ext[q] < 0) return hipErrorInvalidValue;
+    if (d->m_ext[q] < 0 || d->n_ext[q] < 0 || d->k_ext[q] < 0 || d->m_ext[q] > 0x7fffffff ||
+        d->n_ext[q] > 0x7fffffff || d->k_ext[q] > 0x7fffffff)
+      return hipErrorInvalidValue;
   const int64_t M = d->m_ext[0] * d->m_ext[1], N = d->n_ext[0] * d->n_ext[1], K = d->k_ext[0] * d->k_ext[1];
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return hipErrorInvalidValue;
   FoldProblem& p = *out;

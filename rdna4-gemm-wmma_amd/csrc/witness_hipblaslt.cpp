@@ -4,73 +4,116 @@
 //
 // Row-major C[M][N] = A[M][K] * B[K][N] is computed as the column-major product
 // C^T[N][M] = B^T[N][K] * A^T[K][M] (the operand swap of mmm.cpp:1519-1521).
+//
+// A bound plan (mmm_witness_hipblaslt_create) builds the matmul descriptor, the three layouts
+// and the preference and runs the algorithm heuristic once per shape; each
+// mmm_witness_hipblaslt_run is then one hipblasLtMatmul call, so a timed loop measures the
+// vendor kernel and its launch, as the library's bound launchers are measured.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 #include <stdint.h>
 
+#include <new>
+
 namespace {
 
-struct Plan {
+hipblasLtHandle_t& shared_handle() {
+  static thread_local hipblasLtHandle_t h = nullptr;
+  return h;
+}
+
+struct WitnessPlan {
   hipblasLtHandle_t handle = nullptr;
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  hipblasLtMatmulHeuristicResult_t heur{};
 };
 
-Plan& plan() {
-  static thread_local Plan p;
-  return p;
+void release(WitnessPlan* w) {
+  if (w->pref) hipblasLtMatmulPreferenceDestroy(w->pref);
+  if (w->lc) hipblasLtMatrixLayoutDestroy(w->lc);
+  if (w->lb) hipblasLtMatrixLayoutDestroy(w->lb);
+  if (w->la) hipblasLtMatrixLayoutDestroy(w->la);
+  if (w->desc) hipblasLtMatmulDescDestroy(w->desc);
+  delete w;
 }
 
 }  // namespace
 
 extern "C" {
 
-// Returns 0 on success, a hipblasStatus_t (+1000) or hipError_t otherwise.
-int mmm_witness_hipblaslt_gemm(const void* A, const void* B, float* C, int M, int N, int K, int64_t lda,
-                               int64_t ldb, int64_t ldc, void* workspace, size_t ws_bytes, hipStream_t stream) {
-  Plan& p = plan();
-  if (!p.handle && hipblasLtCreate(&p.handle) != HIPBLAS_STATUS_SUCCESS) return 1001;
-  hipblasLtMatmulDesc_t desc = nullptr;
-  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
-  hipblasLtMatmulPreference_t pref = nullptr;
+// Plans the row-major problem once.  Returns 0 and *out on success, a hipblasStatus_t (+1000)
+// or 2000 (no algorithm) otherwise.
+int mmm_witness_hipblaslt_create(int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc, size_t ws_bytes,
+                                 void** out) {
+  if (!out) return 2001;
+  *out = nullptr;
+  hipblasLtHandle_t& h = shared_handle();
+  if (!h && hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return 1001;
+  WitnessPlan* w = new (std::nothrow) WitnessPlan;
+  if (!w) return 2002;
+  w->handle = h;
   int rc = 0;
-  hipblasOperation_t op = HIPBLAS_OP_N;
-  hipblasLtMatmulHeuristicResult_t heur[1];
   int found = 0;
-  const float alpha = 1.0f, beta = 0.0f;
-#define WCHK(x)                                     \
-  do {                                              \
-    hipblasStatus_t s_ = (x);                       \
-    if (s_ != HIPBLAS_STATUS_SUCCESS) {             \
-      rc = 1000 + (int)s_;                          \
-      goto done;                                    \
-    }                                               \
+  hipblasOperation_t op = HIPBLAS_OP_N;
+#define WCHK(x)                         \
+  do {                                  \
+    hipblasStatus_t s_ = (x);           \
+    if (s_ != HIPBLAS_STATUS_SUCCESS) { \
+      rc = 1000 + (int)s_;              \
+      goto fail;                        \
+    }                                   \
   } while (0)
-  WCHK(hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
-  WCHK(hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op, sizeof(op)));
-  WCHK(hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op, sizeof(op)));
+  WCHK(hipblasLtMatmulDescCreate(&w->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+  WCHK(hipblasLtMatmulDescSetAttribute(w->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op, sizeof(op)));
+  WCHK(hipblasLtMatmulDescSetAttribute(w->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op, sizeof(op)));
   // column-major: "A" = B^T (N x K, ld ldb), "B" = A^T (K x M, ld lda), "C" = C^T (N x M, ld ldc)
-  WCHK(hipblasLtMatrixLayoutCreate(&la, HIP_R_16F, N, K, ldb));
-  WCHK(hipblasLtMatrixLayoutCreate(&lb, HIP_R_16F, K, M, lda));
-  WCHK(hipblasLtMatrixLayoutCreate(&lc, HIP_R_32F, N, M, ldc));
-  WCHK(hipblasLtMatmulPreferenceCreate(&pref));
+  WCHK(hipblasLtMatrixLayoutCreate(&w->la, HIP_R_16F, N, K, ldb));
+  WCHK(hipblasLtMatrixLayoutCreate(&w->lb, HIP_R_16F, K, M, lda));
+  WCHK(hipblasLtMatrixLayoutCreate(&w->lc, HIP_R_32F, N, M, ldc));
+  WCHK(hipblasLtMatmulPreferenceCreate(&w->pref));
   {
     uint64_t ws = ws_bytes;
-    WCHK(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)));
+    WCHK(hipblasLtMatmulPreferenceSetAttribute(w->pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)));
   }
-  WCHK(hipblasLtMatmulAlgoGetHeuristic(p.handle, desc, la, lb, lc, lc, pref, 1, heur, &found));
+  WCHK(hipblasLtMatmulAlgoGetHeuristic(h, w->desc, w->la, w->lb, w->lc, w->lc, w->pref, 1, &w->heur, &found));
+#undef WCHK
   if (found < 1) {
     rc = 2000;
-    goto done;
+    goto fail;
   }
-  WCHK(hipblasLtMatmul(p.handle, desc, &alpha, B, la, A, lb, &beta, C, lc, C, lc, &heur[0].algo, workspace, ws_bytes,
-                       stream));
-done:
-  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-  if (lc) hipblasLtMatrixLayoutDestroy(lc);
-  if (lb) hipblasLtMatrixLayoutDestroy(lb);
-  if (la) hipblasLtMatrixLayoutDestroy(la);
-  if (desc) hipblasLtMatmulDescDestroy(desc);
+  *out = w;
+  return 0;
+fail:
+  release(w);
   return rc;
-#undef WCHK
+}
+
+// One hipblasLtMatmul of a bound plan (C = A * B, alpha 1, beta 0).
+int mmm_witness_hipblaslt_run(void* plan, const void* A, const void* B, float* C, void* workspace, size_t ws_bytes,
+                              hipStream_t stream) {
+  if (!plan) return 2001;
+  WitnessPlan* w = (WitnessPlan*)plan;
+  const float alpha = 1.0f, beta = 0.0f;
+  const hipblasStatus_t s = hipblasLtMatmul(w->handle, w->desc, &alpha, B, w->la, A, w->lb, &beta, C, w->lc, C, w->lc,
+                                            &w->heur.algo, workspace, ws_bytes, stream);
+  return s == HIPBLAS_STATUS_SUCCESS ? 0 : 1000 + (int)s;
+}
+
+void mmm_witness_hipblaslt_destroy(void* plan) {
+  if (plan) release((WitnessPlan*)plan);
+}
+
+// One-shot form (plan, run, release): for checks, not for timing.
+int mmm_witness_hipblaslt_gemm(const void* A, const void* B, float* C, int M, int N, int K, int64_t lda,
+                               int64_t ldb, int64_t ldc, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  void* plan = nullptr;
+  int rc = mmm_witness_hipblaslt_create(M, N, K, lda, ldb, ldc, ws_bytes, &plan);
+  if (rc != 0) return rc;
+  rc = mmm_witness_hipblaslt_run(plan, A, B, C, workspace, ws_bytes, stream);
+  mmm_witness_hipblaslt_destroy(plan);
+  return rc;
 }
 
 }  // extern "C"

@@ -125,11 +125,15 @@ def lib() -> C.CDLL:
     L.mmm_gemm_truth_f64.argtypes = [p, p, p, p, i, i, i, i64, i64, i64, s]
     L.mmm_contract5d_truth_f64.argtypes = [C.POINTER(ContractDesc), p, p, p, p, s]
     L.mmm_gemm_plan_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, C.POINTER(GemmPlan)]
+    L.mmm_probe_clock.argtypes = [p, i64, s]
+    L.mmm_probe_mfma_ceiling.argtypes = [p, p, p, i, i, i, i, s]
+    L.mmm_probe_read.argtypes = [p, i64, i, p, i64, s]
     for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_ws", "mmm_gemm_workspace_f16f32", "mmm_gemm_f16f32_tiled",
                  "mmm_contract_desc_baseline", "mmm_contract_desc_reference", "mmm_contract5d_f16f32",
                  "mmm_contract5d_f16f32_ws", "mmm_contract5d_workspace_f16f32", "mmm_fill_uniform_f16",
                  "mmm_fill_normal_f16", "mmm_tile_of_block", "mmm_gemm_naive_f16f32", "mmm_gemm_truth_f64",
-                 "mmm_contract5d_truth_f64", "mmm_gemm_plan_f16f32"):
+                 "mmm_contract5d_truth_f64", "mmm_gemm_plan_f16f32", "mmm_probe_clock", "mmm_probe_mfma_ceiling",
+                 "mmm_probe_read"):
         getattr(L, name).restype = C.c_int
     L.mmm_version.restype = C.c_char_p
     L.mmm_version.argtypes = []
@@ -251,12 +255,13 @@ def _bound(fn, name: str, args: tuple, keep: tuple):
     return launch
 
 
-def bind_gemm(A, B, C_out, stream=None, workspace=None):
+def bind_gemm(A, B, C_out, stream=None, workspace=None, tile=None):
     """A zero-argument launcher of C = A @ B on fixed tensors and a fixed stream.
 
-    gemm()'s checks run once, here; each call of the result is one mmm_gemm_f16f32_ws call with
-    prebuilt arguments, for loops that launch one problem many times (a benchmark, a serving
-    step).  ``workspace`` as for gemm.  The tensors must keep their storage while it is used."""
+    gemm()'s checks run once, here; each call of the result is one mmm_gemm_f16f32_ws call (or
+    mmm_gemm_f16f32_tiled with ``tile``) with prebuilt arguments, for loops that launch one
+    problem many times (a benchmark, a serving step).  ``workspace`` and ``tile`` as for gemm.
+    The tensors must keep their storage while it is used."""
     import torch
 
     if C_out is None or C_out.dtype != torch.float32:
@@ -266,6 +271,10 @@ def bind_gemm(A, B, C_out, stream=None, workspace=None):
     ws = _ws_tensor(workspace, A.device, st)
     wp = C.c_void_p(ws.data_ptr()) if ws is not None else None
     wb = ws.numel() * ws.element_size() if ws is not None else 0
+    if tile is not None:
+        params = TILES[tile] if isinstance(tile, str) else tuple(tile)
+        args = (_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, *params, wp, wb, st)
+        return _bound(lib().mmm_gemm_f16f32_tiled, "mmm_gemm_f16f32_tiled", args, (A, B, C_out, ws))
     args = (_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, wp, wb, st)
     return _bound(lib().mmm_gemm_f16f32_ws, "mmm_gemm_f16f32_ws", args, (A, B, C_out, ws))
 
@@ -417,32 +426,121 @@ def version() -> str:
     return lib().mmm_version().decode()
 
 
+# ------------------------------------------------------------------------------ measurement probes
+def probe_clock(out, ticks: int = 2000, stream=None):
+    """Enqueue the shader-clock probe (one wave spinning `ticks` ticks of the 100 MHz real-time
+    counter); out is a CUDA int64 tensor of at least 2 elements receiving (shader cycles,
+    real-time ticks).  clock_mhz(out) converts after a synchronisation."""
+    import torch
+
+    if out.dtype != torch.int64 or not out.is_cuda or out.numel() < 2:
+        raise TypeError("out must be a CUDA int64 tensor of at least 2 elements")
+    _check("mmm_probe_clock", lib().mmm_probe_clock(_ptr(out), ticks, _stream(stream)))
+    return out
+
+
+def clock_mhz(out) -> float:
+    """Shader clock in MHz from a probe_clock result (host copy of the two counters)."""
+    cyc, ticks = (int(v) for v in out[:2].tolist())
+    return cyc / ticks * 100.0 if ticks > 0 else float("nan")
+
+
+def probe_mfma_ceiling(A, B, C_out, store_tiles: bool = True, stream=None):
+    """The persistent 256x256 tile kernel's MFMA stream with register-resident operands (see
+    include/mmm.h); 2*M*N*K flops per call, no operand traffic."""
+    _check_f16("A", A)
+    _check_f16("B", B)
+    M, K = A.shape
+    N = B.shape[1]
+    _check("mmm_probe_mfma_ceiling", lib().mmm_probe_mfma_ceiling(_ptr(A), _ptr(B), _ptr(C_out), M, N, K,
+                                                                  1 if store_tiles else 0, _stream(stream)))
+    return C_out
+
+
+def probe_read(src, out, direct_to_lds: bool = False, stream=None):
+    """Stream every byte of the CUDA tensor src once (plain 16-byte loads, or direct to LDS)."""
+    nbytes = src.numel() * src.element_size()
+    _check("mmm_probe_read", lib().mmm_probe_read(_ptr(src), nbytes, 1 if direct_to_lds else 0, _ptr(out),
+                                                  out.numel() * out.element_size() // 4, _stream(stream)))
+    return out
+
+
 # ------------------------------------------------------------------------------ vendor witness
 WITNESS_PATH = os.path.join(PKG_ROOT, "lib", "libmmm_witness.so")
 _witness = None
 _witness_ws = None
 
 
-def witness_hipblaslt(A, B, C_out=None, stream=None):
-    """hipBLASLt on the same FP16->FP32 row-major problem (comparison point only)."""
-    import torch
-
-    global _witness, _witness_ws
+def _witness_lib():
+    global _witness
     if _witness is None:
         lib()  # torch first, then this library, so both bind to torch's HIP runtime
         W = C.CDLL(WITNESS_PATH)
-        W.mmm_witness_hipblaslt_gemm.restype = C.c_int
-        W.mmm_witness_hipblaslt_gemm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int,
-                                                 C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_size_t, C.c_void_p]
+        p, i, i64, sz = C.c_void_p, C.c_int, C.c_int64, C.c_size_t
+        W.mmm_witness_hipblaslt_gemm.restype = i
+        W.mmm_witness_hipblaslt_gemm.argtypes = [p, p, p, i, i, i, i64, i64, i64, p, sz, p]
+        W.mmm_witness_hipblaslt_create.restype = i
+        W.mmm_witness_hipblaslt_create.argtypes = [i, i, i, i64, i64, i64, sz, C.POINTER(p)]
+        W.mmm_witness_hipblaslt_run.restype = i
+        W.mmm_witness_hipblaslt_run.argtypes = [p, p, p, p, p, sz, p]
+        W.mmm_witness_hipblaslt_destroy.restype = None
+        W.mmm_witness_hipblaslt_destroy.argtypes = [p]
         _witness = W
+    return _witness
+
+
+def _witness_workspace(device):
+    import torch
+
+    global _witness_ws
     if _witness_ws is None:
-        _witness_ws = torch.empty(64 << 20, dtype=torch.uint8, device=A.device)
+        _witness_ws = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+    return _witness_ws
+
+
+def witness_hipblaslt(A, B, C_out=None, stream=None):
+    """hipBLASLt on the same FP16->FP32 row-major problem (comparison point only; plans the
+    problem on every call -- use bind_witness_hipblaslt for timing)."""
+    import torch
+
+    W = _witness_lib()
+    ws = _witness_workspace(A.device)
     M, K = A.shape
     N = B.shape[1]
     if C_out is None:
         C_out = torch.empty((M, N), dtype=torch.float32, device=A.device)
-    rc = _witness.mmm_witness_hipblaslt_gemm(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, A.stride(0), B.stride(0),
-                                             C_out.stride(0), _ptr(_witness_ws), _witness_ws.numel(), _stream(stream))
+    rc = W.mmm_witness_hipblaslt_gemm(_ptr(A), _ptr(B), _ptr(C_out), M, N, K, A.stride(0), B.stride(0),
+                                      C_out.stride(0), _ptr(ws), ws.numel(), _stream(stream))
     if rc != 0:
         raise MMMError("mmm_witness_hipblaslt_gemm", rc)
     return C_out
+
+
+class _WitnessPlan:
+    """A hipBLASLt plan (descriptors, layouts, heuristic result) built once for one shape."""
+
+    def __init__(self, W, M, N, K, lda, ldb, ldc, ws_bytes):
+        self._W = W
+        self.ptr = C.c_void_p()
+        rc = W.mmm_witness_hipblaslt_create(M, N, K, lda, ldb, ldc, ws_bytes, C.byref(self.ptr))
+        if rc != 0:
+            raise MMMError("mmm_witness_hipblaslt_create", rc)
+
+    def __del__(self):
+        if getattr(self, "ptr", None) and self.ptr.value:
+            self._W.mmm_witness_hipblaslt_destroy(self.ptr)
+
+
+def bind_witness_hipblaslt(A, B, C_out, stream=None):
+    """A zero-argument launcher of hipBLASLt's C = A @ B on fixed tensors and stream: the
+    descriptors, layouts and algorithm heuristic are built once here, and each call is one
+    hipblasLtMatmul -- the same footing as bind_gemm's launchers."""
+    W = _witness_lib()
+    ws = _witness_workspace(A.device)
+    M, K = A.shape
+    N = B.shape[1]
+    plan = _WitnessPlan(W, M, N, K, A.stride(0), B.stride(0), C_out.stride(0), ws.numel())
+    args = (plan.ptr, _ptr(A), _ptr(B), _ptr(C_out), _ptr(ws), ws.numel(), _stream(stream))
+    launch = _bound(W.mmm_witness_hipblaslt_run, "mmm_witness_hipblaslt_run", args, (A, B, C_out, ws))
+    launch.plan = plan  # keeps the plan alive as long as the launcher
+    return launch

@@ -36,6 +36,20 @@ def _check_sampled(orc, A, B, C, rows, cols, label):
     return max(worst, worst2)
 
 
+def _check_refkernel(orc, A, B, C, rows, cols, label):
+    """Sampled rows and columns against the CPU restatement of the reference kernel's fp32
+    arithmetic (K blocked 32 -> 16-deep steps, zero fill past K; mmm.cpp:1309-1356,
+    mmmTensor.cpp:135-178), within the same BASELINE tolerance."""
+    R = orc.gemm_refkernel_f32(A, B, rows=rows)
+    _, S = orc.gemm_f64(A, B, rows=rows)
+    d = np.abs(np.ascontiguousarray(C[rows]).astype(np.float64) - R)
+    assert np.all(d <= TOL * S), f"{label}: rows vs reference-kernel math off by {np.max(d / S):.3g} of S"
+    R = orc.gemm_refkernel_f32(A, B, cols=cols)
+    _, S = orc.gemm_f64(A, B, cols=cols)
+    d = np.abs(np.ascontiguousarray(C[:, cols]).astype(np.float64) - R)
+    assert np.all(d <= TOL * S), f"{label}: columns vs reference-kernel math off by {np.max(d / S):.3g} of S"
+
+
 def _check_checksums(A, B, C, label):
     A64 = A.astype(np.float64)
     B64 = B.astype(np.float64)
@@ -104,9 +118,7 @@ def test_config2_8192_sampled(orc, mm, cuda):
     rows = _sample(n, 24, rng, must=(0, 255, 256, n - 1))
     cols = _sample(n, 8, rng, must=(0, n - 1))
     _check_sampled(orc, A, B, C, rows, cols, "8192^3")
-    R = orc.gemm_refkernel_f32(A, B, rows=rows[:4])
-    T, S = orc.gemm_f64(A, B, rows=rows[:4])
-    assert np.all(np.abs(C[rows[:4]].astype(np.float64) - R) <= TOL * S)
+    _check_refkernel(orc, A, B, C, rows, cols, "8192^3")
     _check_checksums(A, B, C, "8192^3")
 
 
@@ -123,6 +135,7 @@ def test_config3_ragged(orc, mm, cuda):
     rows = _sample(M, 20, rng, must=(0, 127, 128, 255, 256, M - 2, M - 1))
     cols = _sample(N, 12, rng, must=(0, 127, 128, N - 2, N - 1))
     _check_sampled(orc, A, B, C, rows, cols, "ragged")
+    _check_refkernel(orc, A, B, C, rows, cols, "ragged")
     _check_checksums(A, B, C, "ragged")
 
 
@@ -141,7 +154,11 @@ def test_config4_contraction_baseline(orc, mm, cuda):
     Cs = np.ascontiguousarray(C.reshape(b * i, j)[bi])
     bad, worst = orc.check_tol(Cs, T, S, TOL)
     assert bad == 0, f"{bad} violations vs the 5-D loop nest (worst {worst:.3g})"
-    _check_checksums(A.reshape(b * i, k * l), B.reshape(k * l, j), C.reshape(b * i, j), "contraction")
+    # the second reference: the reference kernel's fp32 math on the folded GEMM (M = b*i, K = k*l)
+    A2, B2, C2 = A.reshape(b * i, k * l), B.reshape(k * l, j), C.reshape(b * i, j)
+    cols = _sample(j, 12, rng, must=(0, j - 1))
+    _check_refkernel(orc, A2, B2, C2, bi, cols, "contraction")
+    _check_checksums(A2, B2, C2, "contraction")
 
 
 def test_config5_skinny_full(orc, mm, cuda):

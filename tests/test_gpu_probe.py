@@ -1,0 +1,83 @@
+"""GPU tests of the measurement probes and the bound hipBLASLt comparison launcher.
+
+The probes (include/mmm.h, mmm_probe_*) give the bench line a measured clock and measured
+ceilings; these tests check that they run and report values in the ranges the hardware allows,
+and that the bound hipBLASLt launcher computes the same GEMM as the library (tolerance).
+"""
+import numpy as np
+import pytest
+
+from conftest import to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def test_probe_clock_range(mm, cuda):
+    """Shader clock from s_memtime / s_memrealtime: between the MI355X's lowest DPM level and
+    its 2.4 GHz maximum (with margin), and the spin lasted the requested real-time ticks."""
+    out = cuda.zeros(2, dtype=cuda.int64, device="cuda")
+    for ticks in (2000, 20000):
+        mm.probe_clock(out, ticks)
+        cuda.cuda.synchronize()
+        h = out.cpu()
+        assert int(h[1]) >= ticks
+        mhz = mm.clock_mhz(h)
+        assert 300.0 <= mhz <= 2600.0, mhz
+
+
+def test_probe_mfma_ceiling_runs(mm, cuda):
+    """The ceiling probe writes every tile of C (store_tiles) with finite values, and one float
+    per thread without it; it rejects shapes its grid does not cover."""
+    M, N, K = 512, 768, 128
+    A = cuda.empty((M, K), dtype=cuda.float16, device="cuda")
+    B = cuda.empty((K, N), dtype=cuda.float16, device="cuda")
+    mm.fill_uniform(A, 9, 0)
+    mm.fill_uniform(B, 9, 1)
+    C = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.probe_mfma_ceiling(A, B, C, store_tiles=True)
+    cuda.cuda.synchronize()
+    assert cuda.isfinite(C).all()
+    C.fill_(float("nan"))
+    mm.probe_mfma_ceiling(A, B, C, store_tiles=False)
+    cuda.cuda.synchronize()
+    grid = (M // 256) * (N // 256)
+    assert cuda.isfinite(C.view(-1)[: grid * 512]).all()
+    assert cuda.isnan(C.view(-1)[grid * 512:]).all()
+    with pytest.raises(mm.MMMError):
+        mm.probe_mfma_ceiling(A[:, :96], B[:96], C)  # K % 64 != 0
+
+
+@pytest.mark.parametrize("lds", [False, True])
+def test_probe_read_runs(mm, cuda, lds):
+    """The streaming-read probe reads every byte: an all-zero buffer XOR-folds to zeros, and a
+    single planted word shows up in the plain-load fold."""
+    src = cuda.zeros(1 << 24, dtype=cuda.uint8, device="cuda")
+    out = cuda.full((2048 * 256,), -1, dtype=cuda.int32, device="cuda")
+    mm.probe_read(src, out, direct_to_lds=lds)
+    cuda.cuda.synchronize()
+    if not lds:
+        assert (out == 0).all()
+        src.view(cuda.int32)[12345] = 0x5A5A5A5A
+        mm.probe_read(src, out)
+        cuda.cuda.synchronize()
+        folded = int(np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32)))
+        assert folded == 0x5A5A5A5A
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 256), (1000, 777, 320), (16, 4096, 4096)])
+def test_bound_hipblaslt_matches_library(orc, mm, cuda, shape):
+    """The bound hipBLASLt launcher (descriptors and heuristic planned once) computes the same
+    FP16 -> FP32 GEMM as the library, within the BASELINE tolerance, on repeated calls."""
+    M, N, K = shape
+    A = orc.uniform_f16((M, K), 5, 0)
+    B = orc.uniform_f16((K, N), 5, 1)
+    Ad, Bd = to_dev(cuda, A), to_dev(cuda, B)
+    ours = mm.gemm(Ad, Bd).cpu().numpy().astype(np.float64)
+    Cw = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    launch = mm.bind_witness_hipblaslt(Ad, Bd, Cw)
+    for _ in range(3):
+        launch()
+    cuda.cuda.synchronize()
+    W = Cw.cpu().numpy().astype(np.float64)
+    _, S = orc.gemm_f64(A, B)
+    assert np.all(np.abs(W - ours) <= 2e-3 * S)

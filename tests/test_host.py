@@ -116,6 +116,32 @@ def test_argument_validation_without_gpu(mm):
     tm, tn = C.c_int(), C.c_int()
     assert L.mmm_tile_of_block(4, 2, 2, C.byref(tm), C.byref(tn)) == HIP_INVALID
     assert L.mmm_tile_of_block(0, 0, 2, C.byref(tm), C.byref(tn)) == HIP_INVALID
+    # measurement probes validate before launching
+    assert L.mmm_probe_clock(null, 2000, null) == HIP_INVALID
+    assert L.mmm_probe_clock(dummy, 0, null) == HIP_INVALID
+    assert L.mmm_probe_clock(dummy, 10 ** 8, null) == HIP_INVALID  # more than 100 ms of spinning
+    assert L.mmm_probe_mfma_ceiling(dummy, dummy, dummy, 300, 256, 64, 1, null) == HIP_INVALID  # M % 256
+    assert L.mmm_probe_mfma_ceiling(dummy, dummy, dummy, 256, 256, 96, 1, null) == HIP_INVALID  # K % 64
+    assert L.mmm_probe_mfma_ceiling(null, dummy, dummy, 256, 256, 64, 1, null) == HIP_INVALID
+    assert L.mmm_probe_read(dummy, 1000, 0, dummy, 1 << 20, null) == HIP_INVALID  # not a multiple of 1024
+    assert L.mmm_probe_read(dummy, 1 << 20, 0, dummy, 100, null) == HIP_INVALID  # out too small
+    assert L.mmm_probe_read(dummy, 1 << 31, 1, dummy, 1 << 20, null) == HIP_INVALID  # LDS path: < 2^31 bytes
+
+
+def test_contract_descriptor_overflow_rejected(mm):
+    """Extents whose product would overflow int64 (2^33 * 2^31) are rejected before they are
+    multiplied, by every entry point that reads a descriptor (no GPU needed)."""
+    L = mm.lib()
+    HIP_INVALID = mm.HIP_ERROR_INVALID_VALUE
+    dummy = C.c_void_p(0x1000)
+    for field, ext in (("m_ext", (1 << 33, 1 << 31)), ("n_ext", (1 << 31, 1 << 33)), ("k_ext", (1 << 32, 1 << 32)),
+                       ("m_ext", (1 << 31, 1))):
+        d = mm.contract_desc_baseline(2, 3, 4, 5, 6)
+        getattr(d, field)[0], getattr(d, field)[1] = ext
+        need = C.c_size_t(7)
+        assert L.mmm_contract5d_workspace_f16f32(C.byref(d), None, None, None, C.byref(need)) == HIP_INVALID, field
+        assert L.mmm_contract5d_f16f32(C.byref(d), dummy, dummy, dummy, None) == HIP_INVALID, field
+        assert L.mmm_contract5d_truth_f64(C.byref(d), dummy, dummy, dummy, None, None) == HIP_INVALID, field
 
 
 def test_bench_refuses_multi_gpu():
