@@ -104,8 +104,17 @@ def make_workload(name, torch, mmm):
         fill(A, seed, 0)
         fill(B, seed, 1)
         Cd = torch.empty((M, N), dtype=torch.float32, device=dev)
+        def clocked(clock):
+            st = {"i": 0}
+
+            def run():
+                mmm.probe_mfma_ceiling(A, B, Cd, clock=clock[st["i"] % clock.shape[0]])
+                st["i"] += 1
+
+            return run
+
         return {"launch": lambda: mmm.probe_mfma_ceiling(A, B, Cd), "witness": None, "host_inputs": None,
-                "M": M, "N": N, "K": K}
+                "clocked": clocked, "M": M, "N": N, "K": K}
     if kind == "contraction_ref":
         mt, bt, rt, nt, rt_l = 128, 8192, 64, 64, 128
         G = torch.empty((rt, nt, mt, rt_l), dtype=torch.float16, device=dev)
@@ -128,6 +137,7 @@ def make_workload(name, torch, mmm):
         return {
             "launch": mmm.bind_contract(desc, A, B, Cd),
             "witness": lambda: mmm.bind_witness_hipblaslt(A2, B2, C2),
+            "clocked": lambda clock: mmm.bind_gemm_clocked(A2, B2, C2, clock),
             "host_inputs": lambda: (A2.cpu().numpy(), B2.cpu().numpy()),
             "M": M, "N": N, "K": K,
         }
@@ -160,17 +170,18 @@ def make_workload(name, torch, mmm):
 
         return run
 
-    return {"launch": launch, "witness": witness, "host_inputs": lambda: (A.cpu().numpy(), Bs[0].cpu().numpy()),
+    # the tile kernels record their clock (the M <= 64 streaming kernels do not)
+    clocked = (lambda clock: mmm.bind_gemm_clocked(A, Bs[0], Cd, clock, workspace=ws)) if M > 64 else None
+    return {"launch": launch, "witness": witness, "clocked": clocked,
+            "host_inputs": lambda: (A.cpu().numpy(), Bs[0].cpu().numpy()),
             "M": M, "N": N, "K": K}
 
 
-def time_launches(torch, fn, steps: int, warmup: int, clock=None):
+def time_launches(torch, fn, steps: int, warmup: int):
     """W untimed launches, then exactly `steps` launches between synchronizations.
 
     Returns (ms per step over the whole timed region, list of per-launch ms from HIP events
-    recorded on the launch stream, wall seconds).  With `clock` (the mmm module), the library's
-    shader-clock probe runs on the same stream right before the first and right after the last
-    timed launch, outside the timed events; its readings (MHz) are in time_launches.clocks."""
+    recorded on the launch stream, wall seconds)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -179,35 +190,32 @@ def time_launches(torch, fn, steps: int, warmup: int, clock=None):
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t_begin = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
-    probes = None
-    if clock is not None:
-        probes = torch.zeros(4, dtype=torch.int64, device="cuda")
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
-    if probes is not None:
-        clock.probe_clock(probes[0:2], CLOCK_PROBE_TICKS)
     t_begin.record(stream)
     for s in range(steps):
         starts[s].record(stream)
         fn()
         ends[s].record(stream)
     t_end.record(stream)
-    if probes is not None:
-        clock.probe_clock(probes[2:4], CLOCK_PROBE_TICKS)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_begin.elapsed_time(t_end)
     per = [starts[s].elapsed_time(ends[s]) for s in range(steps)]
-    time_launches.clocks = None
-    if probes is not None:
-        h = probes.cpu()
-        time_launches.clocks = (clock.clock_mhz(h[0:2]), clock.clock_mhz(h[2:4]))
     return total_ms / steps, per, wall
 
 
-# Shader-clock probe length: 20 us of the 100 MHz real-time counter (short against the power
-# controller's reaction time, so it reads the clock the preceding kernels ran at).
-CLOCK_PROBE_TICKS = 2000
+def clocked_pass(torch, mmm, W, steps: int):
+    """`steps` more launches right after the timed region, through the entry point that records
+    the shader clock inside the kernel (workgroup 0's s_memtime / s_memrealtime at its start and
+    end): the clock those launches ran at, and their own throughput."""
+    clock = torch.zeros((steps, 4), dtype=torch.int64, device="cuda")
+    ms, per, _ = time_launches(torch, W["clocked"](clock), steps, 0)
+    mhz = [c for c in mmm.clocks_mhz(clock) if c == c]
+    if not mhz:
+        return None
+    return {"sclk_mhz": round(statistics.fmean(mhz), 1), "min": round(min(mhz), 1), "max": round(max(mhz), 1),
+            "launches": steps, "ms_per_launch": round(statistics.fmean(per), 5)}
 
 
 def smi_snapshot():
@@ -295,8 +303,8 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_c
     M, N, K = W["M"], W["N"], W["K"]
     flops = 2.0 * M * N * K
     algo_bytes = W.get("bytes", 2.0 * M * K + 2.0 * K * N + 4.0 * M * N)
-    ms, per, wall = time_launches(torch, W["launch"], steps, warmup, clock=mmm)
-    clocks = time_launches.clocks
+    ms, per, wall = time_launches(torch, W["launch"], steps, warmup)
+    clk = clocked_pass(torch, mmm, W, steps) if W.get("clocked") else None
     avg_launch = statistics.fmean(per)
     hbm = name in ("skinny", "skinny_nows", "copy", "read_ceiling", "read_ceiling_lds")
     with_witness = with_witness and W["witness"] is not None
@@ -310,10 +318,6 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_c
                       "first": per[0], "last": per[-1]},
         "wall_s": wall,
     }
-    sclk = statistics.fmean(clocks)
-    res["clock"] = {"sclk_mhz": round(sclk, 1), "before": round(clocks[0], 1), "after": round(clocks[1], 1),
-                    "method": "s_memtime / s_memrealtime probe kernel (20 us) on the launch stream right before "
-                              "the first and right after the last timed launch; sclk_mhz is their mean"}
     if hbm:
         achieved = algo_bytes / (avg_launch * 1e-3) / 1e9
         res["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
@@ -322,30 +326,36 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_c
         achieved = flops / (avg_launch * 1e-3) / 1e12
         res["roofline"] = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                            "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(name)}
+    if clk is not None:
         # dense FP16 peak at the measured clock: 256 CU x 4096 flop per clock
-        peak_clk = 256 * 4096 * sclk * 1e6 / 1e12
-        res["pct_peak_at_clock"] = round(100.0 * res["tflops"] / peak_clk, 2)
+        tf = flops / (clk["ms_per_launch"] * 1e-3) / 1e12
+        clk["tflops"] = round(tf, 1)
+        clk["pct_peak_at_clock"] = round(100.0 * tf / (256 * 4096 * clk["sclk_mhz"] * 1e6 / 1e12), 2)
+        clk["method"] = ("in-kernel: workgroup 0's s_memtime / s_memrealtime at its start and end "
+                         "(mmm_gemm_f16f32_clocked), over `launches` launches right after the timed region; "
+                         "tflops and pct_peak_at_clock are those launches' own")
+        res["clock"] = clk
     res["smi"] = smi_snapshot()
     if with_witness:
         try:
-            wms, wper, _ = time_launches(torch, W["witness"](), steps, warmup, clock=mmm)
+            wms, wper, _ = time_launches(torch, W["witness"](), steps, warmup)
             res["hipblaslt"] = {"ms_per_step": wms, "tflops": flops / (wms * 1e-3) / 1e12,
                                 "gbs": algo_bytes / (wms * 1e-3) / 1e9,
-                                "launch_ms_median": statistics.median(wper),
-                                "sclk_mhz": round(statistics.fmean(time_launches.clocks), 1)}
+                                "launch_ms_median": statistics.median(wper)}
         except Exception as e:  # the comparison point must not hide the measurement
             res["hipblaslt"] = {"error": str(e)}
     if with_ceiling:
         # the same step count on the library's MFMA-ceiling probe (this workload's MFMA stream
         # with register-resident operands), measured live in this process
-        C = make_workload("mfma_ceiling", torch, mmm)
-        cms, cper, _ = time_launches(torch, C["launch"], steps, warmup, clock=mmm)
+        Cw = make_workload("mfma_ceiling", torch, mmm)
+        cms, cper, _ = time_launches(torch, Cw["launch"], steps, warmup)
+        cclk = clocked_pass(torch, mmm, Cw, steps)
         ctf = flops / (cms * 1e-3) / 1e12
-        res["ceiling"] = {"mfma_tflops": round(ctf, 1), "sclk_mhz": round(statistics.fmean(time_launches.clocks), 1),
-                          "frac": round(res["tflops"] / ctf, 4),
+        res["ceiling"] = {"mfma_tflops": round(ctf, 1), "frac": round(res["tflops"] / ctf, 4),
+                          "sclk_mhz": cclk["sclk_mhz"] if cclk else None,
                           "what": "mmm_probe_mfma_ceiling: the same grid's MFMA stream and C stores without "
-                                  "operand loads, LDS or barriers; frac = value / mfma_tflops"}
-        del C
+                                  "operand loads, LDS or barriers, same warm-up and steps; frac = value / mfma_tflops"}
+        del Cw
     if with_cpu:
         res["cpu_baseline"] = cpu_baseline(W)
     return res
@@ -472,10 +482,9 @@ def main() -> int:
         "pct_peak": round(100.0 * r["tflops"] / PEAK_TFLOPS, 2),
         "launch_ms": {k: round(v, 5) for k, v in r["launch_ms"].items()},
         "roofline": r["roofline"],
-        "clock": r["clock"],
     }
-    if "pct_peak_at_clock" in r:
-        line["pct_peak_at_clock"] = r["pct_peak_at_clock"]
+    if "clock" in r:
+        line["clock"] = r["clock"]
     if "ceiling" in r:
         line["ceiling"] = r["ceiling"]
     line["smi"] = r["smi"]

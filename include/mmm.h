@@ -67,6 +67,20 @@ hipError_t mmm_gemm_f16f32_ws(const mmm_half* A, const mmm_half* B, float* C, in
                               int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Measurement form of mmm_gemm_f16f32_ws: the same launch, and when it runs a matrix-core tile
+ * kernel, thread 0 of its workgroup 0 writes clock[0] = shader-clock counter (s_memtime) and
+ * clock[1] = 100 MHz real-time counter (s_memrealtime) at its start and clock[2], clock[3] at its
+ * end (device memory, 8-byte aligned; NULL: nothing is written, exactly mmm_gemm_f16f32_ws).
+ * The shader clock during the launch is (clock[2] - clock[0]) / (clock[3] - clock[1]) * 100 MHz.
+ * Other kernels (M <= 64 streaming, K == 0) leave clock unwritten.  No reference counterpart:
+ * it gives a benchmark the clock its own launches ran at, the MI355X clock falling under
+ * sustained matrix-core load (power limit).
+ */
+hipError_t mmm_gemm_f16f32_clocked(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
+                                   int64_t lda, int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes,
+                                   uint64_t* clock, hipStream_t stream);
+
+/*
  * Workspace bytes mmm_gemm_f16f32_ws needs for these arguments (0: it would not split).
  * Host only, no GPU call; A, B, C only for their alignment and may be NULL (taken as
  * 256-byte aligned).  No reference counterpart (see mmm_gemm_f16f32_ws).
@@ -234,7 +248,8 @@ hipError_t mmm_tile_of_block(int block, int tiles_m, int tiles_n, int* tm, int* 
  *   barriers.  A [M][K] and B [K][N] are contiguous row-major inputs whose first K-steps supply
  *   the fragments; store_tiles != 0 writes each tile's accumulators to C [M][N] as the tile
  *   kernel does, store_tiles == 0 writes one float per thread into C's first 256 * 512 floats.
- *   The values written are not A*B.  M, N multiples of 256, K of 64.
+ *   The values written are not A*B.  M, N multiples of 256, K of 64.  clock (NULL allowed)
+ *   receives workgroup 0's start and end counters as mmm_gemm_f16f32_clocked writes them.
  * mmm_probe_read: streams `bytes` (a multiple of 1024, 16-byte-aligned src) once: with plain
  *   16-byte loads into registers (direct_to_lds == 0; out receives 2048 * 256 words), or with
  *   the tile kernels' direct-to-LDS loads (direct_to_lds != 0, bytes < 2^31; out receives 2048
@@ -242,7 +257,7 @@ hipError_t mmm_tile_of_block(int block, int tiles_m, int tiles_n, int* tm, int* 
  */
 hipError_t mmm_probe_clock(uint64_t* out, int64_t ticks, hipStream_t stream);
 hipError_t mmm_probe_mfma_ceiling(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
-                                  int store_tiles, hipStream_t stream);
+                                  int store_tiles, uint64_t* clock, hipStream_t stream);
 hipError_t mmm_probe_read(const void* src, int64_t bytes, int direct_to_lds, uint32_t* out, int64_t out_words,
                           hipStream_t stream);
 

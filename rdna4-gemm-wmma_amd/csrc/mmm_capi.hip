@@ -329,12 +329,20 @@ hipError_t mmm_gemm_f16f32(const mmm_half* A, const mmm_half* B, float* C, int M
 
 hipError_t mmm_gemm_f16f32_ws(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
                               int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return mmm_gemm_f16f32_clocked(A, B, C, M, N, K, lda, ldb, ldc, workspace, workspace_bytes, nullptr, stream);
+}
+
+hipError_t mmm_gemm_f16f32_clocked(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
+                                   int64_t lda, int64_t ldb, int64_t ldc, void* workspace, size_t workspace_bytes,
+                                   uint64_t* clock, hipStream_t stream) {
   hipError_t e = check_gemm(A, B, C, M, N, K, lda, ldb, ldc);
   if (e != hipSuccess) return e;
   if ((e = check_workspace(workspace)) != hipSuccess) return e;
+  if ((uintptr_t)clock & 7) return hipErrorInvalidValue;
   GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
   p.ws = (float*)workspace;
   p.ws_bytes = workspace ? workspace_bytes : 0;
+  p.clk = clock;
   const GemmPlan pl = plan_gemm(p);
   switch (pl.kind) {
     case MMM_KERNEL_NONE:
@@ -347,6 +355,7 @@ hipError_t mmm_gemm_f16f32_ws(const mmm_half* A, const mmm_half* B, float* C, in
       GemmProblem pm = p, pr = p;
       pm.M = pl.tile_rows;
       pr.M = M - pl.tile_rows;
+      pr.clk = nullptr;
       pr.A = A + (int64_t)pl.tile_rows * lda;
       pr.C = C + (int64_t)pl.tile_rows * ldc;
       e = launch_gemm_nn(pm, pl.tile, stream);

@@ -316,6 +316,15 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
 
 __device__ __forceinline__ void block_sync() { __syncthreads(); }
 
+// Measurement: thread 0 of workgroup 0 writes the shader-clock counter (s_memtime) and the 100 MHz
+// real-time counter (s_memrealtime) to clk[at], clk[at + 1] when the caller asked for them.
+__device__ __forceinline__ void record_clock(uint64_t* clk, int at) {
+  if (clk != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    clk[at] = __builtin_amdgcn_s_memtime();
+    clk[at + 1] = __builtin_amdgcn_s_memrealtime();
+  }
+}
+
 // Cross-stage K loop over KT K tiles (the direct-to-LDS kernels).  The caller supplies the
 // loads: prep(t, slot) builds the per-tile load state of K tile t for ring slot `slot` (and
 // advances any running state: tiles are prepared in order), dma_one(d, j) issues load j of
@@ -465,6 +474,7 @@ struct NoHook {
 template <class T, bool GENERIC, bool WT = false>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
+  record_clock(p.clk, 0);
 
   // K split (direct-to-LDS path only).  Blocks [0, whole) compute tiles 0 .. whole-1 of the
   // XCD-aware order over their full K range; the last split_tiles tiles of that order are split:
@@ -715,6 +725,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
           *(f32x4*)(prow + col_of(nb, qq)) = f32x4{acc[mb][nb][4 * qq + 0], acc[mb][nb][4 * qq + 1],
                                                    acc[mb][nb][4 * qq + 2], acc[mb][nb][4 * qq + 3]};
     }
+    record_clock(p.clk, 2);
     return;
   }
   float* C = p.C;
@@ -744,6 +755,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       }
     }
   }
+  record_clock(p.clk, 2);
 }
 
 // ------------------------------------------------------------------------------------
@@ -760,6 +772,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
 template <class T, bool NT>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
+  record_clock(p.clk, 0);
   constexpr int S = T::STAGES;
   constexpr int NQ = T::MF == 32 ? 4 : 1;       // float4 groups per accumulator
   constexpr int NST = T::FM * T::FN * NQ;       // C stores per thread per tile
@@ -893,6 +906,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
     if (nb >= ntiles) break;
     b = nb, m0 = nm0, n0 = nn0, pre = 2;
   }
+  record_clock(p.clk, 2);
 }
 
 // ------------------------------------------------------------------------------------
@@ -906,6 +920,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
 template <class T, bool NT>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_split_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
+  record_clock(p.clk, 0);
   constexpr int S = T::STAGES;
   constexpr int NQ = T::MF == 32 ? 4 : 1;       // float4 groups per accumulator
   constexpr int NST = T::FM * T::FN * NQ;       // C stores per thread per tile
@@ -1070,6 +1085,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_split_kernel
     if (nb >= nitems) break;
     b = nb, cur = nxt, pre = 2;
   }
+  record_clock(p.clk, 2);
 }
 
 // ------------------------------------------------------------------------------------

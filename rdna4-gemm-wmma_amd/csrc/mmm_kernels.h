@@ -22,6 +22,8 @@ struct GemmProblem {
   float* partials; // k_splits > 1: [split tile][split][BM][BN] fp32 partial tiles
   float* ws;       // caller's workspace for K splits (16-byte aligned), or null: no split
   size_t ws_bytes; // its size
+  uint64_t* clk;   // null, or 4 counters workgroup 0 of a tile kernel writes: shader clock and
+                   // real-time counter at its start, then at its end (measurement only)
 };
 
 // Folded problem (the 5-D contraction descriptor, see mmm.h), with int32 extents.

@@ -43,7 +43,11 @@ __global__ __launch_bounds__(64) void clock_probe_kernel(uint64_t* out, uint64_t
 constexpr int kCeilFM = 8, kCeilFN = 4;
 
 __global__ __launch_bounds__(512, 1) void mfma_ceiling_kernel(const mmm_half* A, const mmm_half* B, float* C, int M,
-                                                              int N, int K, int store_tiles) {
+                                                              int N, int K, int store_tiles, uint64_t* clk) {
+  if (clk != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    clk[0] = __builtin_amdgcn_s_memtime();
+    clk[1] = __builtin_amdgcn_s_memrealtime();
+  }
   const int tiles_m = M / 256, tiles_n = N / 256, ntiles = tiles_m * tiles_n;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -101,6 +105,10 @@ __global__ __launch_bounds__(512, 1) void mfma_ceiling_kernel(const mmm_half* A,
     }
   }
   if (!store_tiles) C[(int64_t)blockIdx.x * 512 + threadIdx.x] = keep;
+  if (clk != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    clk[2] = __builtin_amdgcn_s_memtime();
+    clk[3] = __builtin_amdgcn_s_memrealtime();
+  }
 }
 
 // HBM read ceiling, plain loads: lanes stream 16-byte chunks (global_load_dwordx4) over
@@ -166,15 +174,16 @@ hipError_t mmm_probe_clock(uint64_t* out, int64_t ticks, hipStream_t stream) {
 }
 
 hipError_t mmm_probe_mfma_ceiling(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
-                                  int store_tiles, hipStream_t stream) {
-  if (!A || !B || !C || M <= 0 || N <= 0 || K <= 0) return hipErrorInvalidValue;
+                                  int store_tiles, uint64_t* clock, hipStream_t stream) {
+  if (!A || !B || !C || M <= 0 || N <= 0 || K <= 0 || ((uintptr_t)clock & 7)) return hipErrorInvalidValue;
   if (M % 256 || N % 256 || K % 64) return hipErrorInvalidValue;
   if ((int64_t)(M / 256) * (N / 256) > 0x7fffffff || ((uintptr_t)A & 15) || ((uintptr_t)C & 15))
     return hipErrorInvalidValue;
   const int64_t tiles = (int64_t)(M / 256) * (N / 256);
   // store_tiles == 0 writes one float per thread: grid * 512 <= tiles * 512 < M * N floats of C
   const int grid = (int)(tiles < 256 ? tiles : 256);
-  hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(grid), dim3(512), 0, stream, A, B, C, M, N, K, store_tiles ? 1 : 0);
+  hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(grid), dim3(512), 0, stream, A, B, C, M, N, K, store_tiles ? 1 : 0,
+                     clock);
   return hipGetLastError();
 }
 

@@ -111,6 +111,7 @@ def lib() -> C.CDLL:
     p, i, i64, s, sz = C.c_void_p, C.c_int, C.c_int64, C.c_void_p, C.c_size_t
     L.mmm_gemm_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, s]
     L.mmm_gemm_f16f32_ws.argtypes = [p, p, p, i, i, i, i64, i64, i64, p, sz, s]
+    L.mmm_gemm_f16f32_clocked.argtypes = [p, p, p, i, i, i, i64, i64, i64, p, sz, p, s]
     L.mmm_gemm_workspace_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, C.POINTER(sz)]
     L.mmm_gemm_f16f32_tiled.argtypes = [p, p, p, i, i, i, i64, i64, i64, i, i, i, i, p, sz, s]
     L.mmm_contract_desc_baseline.argtypes = [C.POINTER(ContractDesc), i, i, i, i, i]
@@ -126,9 +127,9 @@ def lib() -> C.CDLL:
     L.mmm_contract5d_truth_f64.argtypes = [C.POINTER(ContractDesc), p, p, p, p, s]
     L.mmm_gemm_plan_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, C.POINTER(GemmPlan)]
     L.mmm_probe_clock.argtypes = [p, i64, s]
-    L.mmm_probe_mfma_ceiling.argtypes = [p, p, p, i, i, i, i, s]
+    L.mmm_probe_mfma_ceiling.argtypes = [p, p, p, i, i, i, i, p, s]
     L.mmm_probe_read.argtypes = [p, i64, i, p, i64, s]
-    for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_ws", "mmm_gemm_workspace_f16f32", "mmm_gemm_f16f32_tiled",
+    for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_ws", "mmm_gemm_f16f32_clocked", "mmm_gemm_workspace_f16f32", "mmm_gemm_f16f32_tiled",
                  "mmm_contract_desc_baseline", "mmm_contract_desc_reference", "mmm_contract5d_f16f32",
                  "mmm_contract5d_f16f32_ws", "mmm_contract5d_workspace_f16f32", "mmm_fill_uniform_f16",
                  "mmm_fill_normal_f16", "mmm_tile_of_block", "mmm_gemm_naive_f16f32", "mmm_gemm_truth_f64",
@@ -277,6 +278,41 @@ def bind_gemm(A, B, C_out, stream=None, workspace=None, tile=None):
         return _bound(lib().mmm_gemm_f16f32_tiled, "mmm_gemm_f16f32_tiled", args, (A, B, C_out, ws))
     args = (_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, wp, wb, st)
     return _bound(lib().mmm_gemm_f16f32_ws, "mmm_gemm_f16f32_ws", args, (A, B, C_out, ws))
+
+
+def bind_gemm_clocked(A, B, C_out, clock, stream=None, workspace=None):
+    """As bind_gemm, through mmm_gemm_f16f32_clocked: launch i (i = 0, 1, ...) writes workgroup 0's
+    start and end counters to clock[i] (a CUDA int64 tensor [n, 4]; launches past n wrap)."""
+    import torch
+
+    if C_out is None or C_out.dtype != torch.float32:
+        raise ValueError("C must be a row-major float32 [M,N] tensor")
+    if clock.dtype != torch.int64 or clock.dim() != 2 or clock.shape[1] != 4 or not clock.is_contiguous():
+        raise ValueError("clock must be a contiguous CUDA int64 tensor [n, 4]")
+    M, N, K, lda, ldb, ldc = _gemm_shapes(A, B, C_out)
+    st = _stream(stream)
+    ws = _ws_tensor(workspace, A.device, st)
+    wp = C.c_void_p(ws.data_ptr()) if ws is not None else None
+    wb = ws.numel() * ws.element_size() if ws is not None else 0
+    fn = lib().mmm_gemm_f16f32_clocked
+    state = {"i": 0}
+    base = (_ptr(A), _ptr(B), _ptr(C_out), M, N, K, lda, ldb, ldc, wp, wb)
+
+    def launch():
+        slot = C.c_void_p(clock.data_ptr() + 32 * (state["i"] % clock.shape[0]))
+        state["i"] += 1
+        rc = fn(*base, slot, st)
+        if rc != HIP_SUCCESS:
+            raise MMMError("mmm_gemm_f16f32_clocked", rc)
+
+    launch.tensors = (A, B, C_out, ws, clock)
+    return launch
+
+
+def clocks_mhz(clock):
+    """Shader clock (MHz) of each launch recorded by bind_gemm_clocked (rows of [n, 4] counters)."""
+    h = clock.cpu().tolist()
+    return [(c1 - c0) / (r1 - r0) * 100.0 if r1 > r0 else float("nan") for c0, r0, c1, r1 in h]
 
 
 def bind_contract(desc: "ContractDesc", A, B, C_out, stream=None, workspace=None):
@@ -445,15 +481,17 @@ def clock_mhz(out) -> float:
     return cyc / ticks * 100.0 if ticks > 0 else float("nan")
 
 
-def probe_mfma_ceiling(A, B, C_out, store_tiles: bool = True, stream=None):
+def probe_mfma_ceiling(A, B, C_out, store_tiles: bool = True, stream=None, clock=None):
     """The persistent 256x256 tile kernel's MFMA stream with register-resident operands (see
-    include/mmm.h); 2*M*N*K flops per call, no operand traffic."""
+    include/mmm.h); 2*M*N*K flops per call, no operand traffic.  ``clock``: None, or a CUDA int64
+    tensor of 4 elements receiving workgroup 0's start and end counters."""
     _check_f16("A", A)
     _check_f16("B", B)
     M, K = A.shape
     N = B.shape[1]
+    ck = C.c_void_p(clock.data_ptr()) if clock is not None else None
     _check("mmm_probe_mfma_ceiling", lib().mmm_probe_mfma_ceiling(_ptr(A), _ptr(B), _ptr(C_out), M, N, K,
-                                                                  1 if store_tiles else 0, _stream(stream)))
+                                                                  1 if store_tiles else 0, ck, _stream(stream)))
     return C_out
 
 

@@ -81,3 +81,41 @@ def test_bound_hipblaslt_matches_library(orc, mm, cuda, shape):
     W = Cw.cpu().numpy().astype(np.float64)
     _, S = orc.gemm_f64(A, B)
     assert np.all(np.abs(W - ours) <= 2e-3 * S)
+
+
+@pytest.mark.parametrize("shape", [(512, 768, 320), (8192, 8192, 512), (4097, 4095, 1000)])
+def test_clocked_entry_point(mm, cuda, shape):
+    """mmm_gemm_f16f32_clocked computes exactly what mmm_gemm_f16f32_ws computes (same launch)
+    and, for the tile kernels, writes workgroup 0's counters: a positive duration at a clock in
+    the hardware's range."""
+    M, N, K = shape
+    A = cuda.empty((M, K), dtype=cuda.float16, device="cuda")
+    B = cuda.empty((K, N), dtype=cuda.float16, device="cuda")
+    mm.fill_uniform(A, 3, 0)
+    mm.fill_uniform(B, 3, 1)
+    ref = mm.gemm(A, B)
+    Cc = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    clock = cuda.zeros((2, 4), dtype=cuda.int64, device="cuda")
+    launch = mm.bind_gemm_clocked(A, B, Cc, clock)
+    launch()
+    launch()
+    cuda.cuda.synchronize()
+    assert cuda.equal(Cc, ref)
+    h = clock.cpu()
+    assert (h[:, 2] > h[:, 0]).all() and (h[:, 3] > h[:, 1]).all()
+    for mhz in mm.clocks_mhz(clock):
+        assert 300.0 <= mhz <= 2600.0, mhz
+
+
+def test_clocked_streaming_kernel_leaves_clock(mm, cuda):
+    """The M <= 64 streaming kernels record nothing: the counters stay as the caller left them."""
+    A = cuda.empty((16, 2048), dtype=cuda.float16, device="cuda")
+    B = cuda.empty((2048, 4096), dtype=cuda.float16, device="cuda")
+    mm.fill_uniform(A, 4, 0)
+    mm.fill_uniform(B, 4, 1)
+    Cc = cuda.empty((16, 4096), dtype=cuda.float32, device="cuda")
+    clock = cuda.full((1, 4), 7, dtype=cuda.int64, device="cuda")
+    mm.bind_gemm_clocked(A, B, Cc, clock)()
+    cuda.cuda.synchronize()
+    assert (clock.cpu() == 7).all()
+    assert cuda.equal(Cc, mm.gemm(A, B))

@@ -120,9 +120,13 @@ def test_argument_validation_without_gpu(mm):
     assert L.mmm_probe_clock(null, 2000, null) == HIP_INVALID
     assert L.mmm_probe_clock(dummy, 0, null) == HIP_INVALID
     assert L.mmm_probe_clock(dummy, 10 ** 8, null) == HIP_INVALID  # more than 100 ms of spinning
-    assert L.mmm_probe_mfma_ceiling(dummy, dummy, dummy, 300, 256, 64, 1, null) == HIP_INVALID  # M % 256
-    assert L.mmm_probe_mfma_ceiling(dummy, dummy, dummy, 256, 256, 96, 1, null) == HIP_INVALID  # K % 64
-    assert L.mmm_probe_mfma_ceiling(null, dummy, dummy, 256, 256, 64, 1, null) == HIP_INVALID
+    assert L.mmm_probe_mfma_ceiling(dummy, dummy, dummy, 300, 256, 64, 1, null, null) == HIP_INVALID  # M % 256
+    assert L.mmm_probe_mfma_ceiling(dummy, dummy, dummy, 256, 256, 96, 1, null, null) == HIP_INVALID  # K % 64
+    assert L.mmm_probe_mfma_ceiling(null, dummy, dummy, 256, 256, 64, 1, null, null) == HIP_INVALID
+    assert L.mmm_probe_mfma_ceiling(dummy, dummy, dummy, 256, 256, 64, 1, C.c_void_p(0x1004), null) == HIP_INVALID
+    assert L.mmm_gemm_f16f32_clocked(dummy, dummy, dummy, 8, 8, 8, 8, 8, 8, null, 0, C.c_void_p(0x1004),
+                                     null) == HIP_INVALID  # clock not 8-byte aligned
+    assert L.mmm_gemm_f16f32_clocked(dummy, dummy, dummy, 8, 8, 8, 7, 8, 8, null, 0, null, null) == HIP_INVALID
     assert L.mmm_probe_read(dummy, 1000, 0, dummy, 1 << 20, null) == HIP_INVALID  # not a multiple of 1024
     assert L.mmm_probe_read(dummy, 1 << 20, 0, dummy, 100, null) == HIP_INVALID  # out too small
     assert L.mmm_probe_read(dummy, 1 << 31, 1, dummy, 1 << 20, null) == HIP_INVALID  # LDS path: < 2^31 bytes
