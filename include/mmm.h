@@ -81,6 +81,20 @@ hipError_t mmm_gemm_f16f32_clocked(const mmm_half* A, const mmm_half* B, float* 
                                    uint64_t* clock, hipStream_t stream);
 
 /*
+ * As mmm_gemm_f16f32_ws, with the K-split partials in a 64 MiB array inside the library (one per
+ * GPU, held until the process ends) instead of a caller's workspace: the entry point calls no
+ * allocating routine.  No reference counterpart: it is for callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The array serves the
+ * current device; the first call on a device looks its address up (do that before a capture).
+ * Results equal mmm_gemm_f16f32_ws's with a workspace of at least mmm_gemm_workspace_f16f32
+ * bytes.  Returns hipErrorInvalidValue where mmm_gemm_f16f32_ws would, and when a planned split
+ * needs more than the array holds (not reached by the planner's 64 MiB limit).  Every call on one
+ * GPU shares its array: calls that overlap on one GPU (different streams) race on it.
+ */
+hipError_t mmm_gemm_f16f32_noalloc(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
+                                   int64_t lda, int64_t ldb, int64_t ldc, hipStream_t stream);
+
+/*
  * Workspace bytes mmm_gemm_f16f32_ws needs for these arguments (0: it would not split).
  * Host only, no GPU call; A, B, C only for their alignment and may be NULL (taken as
  * 256-byte aligned).  No reference counterpart (see mmm_gemm_f16f32_ws).

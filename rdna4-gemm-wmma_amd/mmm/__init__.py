@@ -112,6 +112,7 @@ def lib() -> C.CDLL:
     L.mmm_gemm_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, s]
     L.mmm_gemm_f16f32_ws.argtypes = [p, p, p, i, i, i, i64, i64, i64, p, sz, s]
     L.mmm_gemm_f16f32_clocked.argtypes = [p, p, p, i, i, i, i64, i64, i64, p, sz, p, s]
+    L.mmm_gemm_f16f32_noalloc.argtypes = [p, p, p, i, i, i, i64, i64, i64, s]
     L.mmm_gemm_workspace_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, C.POINTER(sz)]
     L.mmm_gemm_f16f32_tiled.argtypes = [p, p, p, i, i, i, i64, i64, i64, i, i, i, i, p, sz, s]
     L.mmm_contract_desc_baseline.argtypes = [C.POINTER(ContractDesc), i, i, i, i, i]
@@ -129,7 +130,7 @@ def lib() -> C.CDLL:
     L.mmm_probe_clock.argtypes = [p, i64, s]
     L.mmm_probe_mfma_ceiling.argtypes = [p, p, p, i, i, i, i, p, s]
     L.mmm_probe_read.argtypes = [p, i64, i, p, i64, s]
-    for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_ws", "mmm_gemm_f16f32_clocked", "mmm_gemm_workspace_f16f32", "mmm_gemm_f16f32_tiled",
+    for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_ws", "mmm_gemm_f16f32_clocked", "mmm_gemm_f16f32_noalloc", "mmm_gemm_workspace_f16f32", "mmm_gemm_f16f32_tiled",
                  "mmm_contract_desc_baseline", "mmm_contract_desc_reference", "mmm_contract5d_f16f32",
                  "mmm_contract5d_f16f32_ws", "mmm_contract5d_workspace_f16f32", "mmm_fill_uniform_f16",
                  "mmm_fill_normal_f16", "mmm_tile_of_block", "mmm_gemm_naive_f16f32", "mmm_gemm_truth_f64",
