@@ -103,15 +103,16 @@ hipError_t mmm_gemm_workspace_f16f32(const mmm_half* A, const mmm_half* B, const
                                      int64_t lda, int64_t ldb, int64_t ldc, size_t* bytes);
 
 /*
- * As mmm_gemm_f16f32, with the tile shape chosen by the caller through the reference's
- * template parameters (mmm.cpp:694-695, 1462-1465), reinterpreted for wave64 MFMA:
- *   WAVE_M, WAVE_N   -- 32x32 MFMA tiles per wave along M and N (the reference counts
- *                       16x16 WMMA tiles);
- *   WAVES_I, WAVES_J -- waves per workgroup along M and N.
- * Block tile = (WAVES_I*WAVE_M*32) x (WAVES_J*WAVE_N*32), K step 64.
- * Instantiated shapes (WAVE_M,WAVE_N,WAVES_I,WAVES_J): (4,4,2,2) 256x256, (2,4,2,2) 128x256,
- * (4,2,2,2) 256x128, (2,2,2,2) 128x128.  Others return hipErrorInvalidValue.  The workspace
- * (NULL allowed) serves the tile's K split as in mmm_gemm_f16f32_ws.
+ * As mmm_gemm_f16f32, with the block tile chosen by the caller through the reference's
+ * template parameters (mmm.cpp:694-695, 1462-1465): block tile = (WAVES_I*WAVE_M*32) x
+ * (WAVES_J*WAVE_N*32), i.e. the parameters count 32x32 output blocks per wave and waves per
+ * workgroup along M and N (the reference counts 16x16 WMMA tiles).  They select the block tile
+ * only; each block tile's waves, MFMA shape and K step are the library's own:
+ *   (4,4,2,2) 256x256 -- 8 waves (2 x 4) of 128x64, v_mfma_f32_16x16x32_f16, 64-deep K steps;
+ *   (2,4,2,2) 128x256, (4,2,2,2) 256x128 -- 4 waves, v_mfma_f32_32x32x16_f16, 32-deep K steps;
+ *   (2,2,2,2) 128x128 -- 4 waves, v_mfma_f32_32x32x16_f16, 64-deep K steps.
+ * Other parameter sets return hipErrorInvalidValue.  The workspace (NULL allowed) serves the
+ * tile's K split as in mmm_gemm_f16f32_ws.
  */
 hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
                                  int64_t lda, int64_t ldb, int64_t ldc, int wave_m, int wave_n, int waves_i,

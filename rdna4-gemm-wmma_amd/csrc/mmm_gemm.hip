@@ -466,8 +466,10 @@ struct NoHook {
 };
 
 
-// GENERIC = false: direct-to-LDS buffer loads; needs lda, ldb, K, N multiples of 8 and
-//                  16-byte-aligned A and B (checked by the host).
+// GENERIC = false: direct-to-LDS buffer loads; needs 2-byte-aligned A and B and per-tile byte
+//                  offsets within 32 bits (dma_ok).  Rows that are not 16-byte aligned are read
+//                  by unaligned buffer loads; the last K tile of an unaligned problem is gathered
+//                  through VGPRs (tail_regs).
 // GENERIC = true : element-wise masked loads through VGPRs; any shape and alignment.
 // WT = true: C rows (16-byte aligned) are written with system-scope write-through stores
 //            (sc0 sc1), for one-round grids (see launch_nn).
@@ -760,7 +762,8 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
 
 // ------------------------------------------------------------------------------------
 // Persistent direct-to-LDS tile kernel, for grids of whole interior tiles (M and N multiples
-// of the tile, aligned operands and C, no K split) over more than one round: grid =
+// of the tile, aligned operands and C; a K split of the last round runs as
+// gemm_nn_persistent_split_kernel instead) over more than one round: grid =
 // min(tiles, 256) workgroups; workgroup b computes tiles b, b + grid, b + 2*grid, ... of the
 // XCD-aware order (grid % 8 == 0 keeps it on one XCD, walking that XCD's tile patches in
 // order).  Between two tiles it waits for every wave to finish reading the ring, issues the
@@ -1535,10 +1538,13 @@ using FoldDmaTile = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA
 template <int BM, int BN>
 using RegTile = Tile<BM, BN, 2, 2, 64, 2>;
 
-// True when the direct-to-LDS path can serve the problem: fp16 operands (2-byte aligned;
-// rows that are not 16-byte aligned are read by unaligned buffer loads, which gfx9-family
-// hardware serves under ROCm's unaligned memory mode), and per-tile byte offsets that fit
-// the 32-bit buffer offsets.
+// True when the direct-to-LDS path can serve the problem: fp16 operands (2-byte aligned), and
+// per-tile byte offsets that fit the 32-bit buffer offsets.  Rows that are not 16-byte aligned
+// (odd lda or ldb, e.g. the 4097 x 4095 x 4111 configuration) are read by 16-byte buffer loads
+// at 2-byte-aligned addresses: this relies on the unaligned buffer access the gfx9 family
+// serves in ROCm's default (unaligned) memory mode, which MI355X boxes run -- the exact
+// full-size ragged tests cover it.  A platform without unaligned buffer access must send
+// 2-byte-aligned rows to the register-staged path (return false for them here).
 static bool dma_ok(const GemmProblem& p, int bm) {
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   if ((a & 1) || (b & 1)) return false;
@@ -1603,7 +1609,7 @@ size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id) {
 }
 
 // The persistent kernel's conditions: whole interior 256x256 tiles over more than one round of
-// 256 workgroups, aligned operands (no gathered K tile), 4-byte-aligned C, no K split, and at
+// 256 workgroups, aligned operands (no gathered K tile), 4-byte-aligned C, and at
 // least S + 1 K tiles.  Measured against one workgroup per tile (same box): 8192^3 +1%,
 // 8192^2 x 2048 +3.7%, 16384 x 8192 x 1024 +3.8%.
 #ifndef MMM_PERSIST

@@ -337,8 +337,8 @@ def test_exact_stream_rows(mm, cuda, case):
 
 
 def test_stream_split_repeat_and_resize(mm, cuda):
-    """Arrival counters return to zero after every call: shapes with different strip and
-    split counts alternate on one stream, each checked."""
+    """Shapes with different strip and split counts alternate on one stream and reuse one
+    per-stream workspace (no clearing between calls); every call stays exact."""
     rng = np.random.default_rng(5)
     cases = [_exact_case(rng, *shp) for shp in [(16, 8192, 2048), (4, 1024, 4096), (16, 4096, 1024)]]
     dev = [(to_dev(cuda, A), to_dev(cuda, B), truth) for A, B, truth in cases]

@@ -132,6 +132,18 @@ def test_argument_validation_without_gpu(mm):
     assert L.mmm_probe_read(dummy, 1 << 31, 1, dummy, 1 << 20, null) == HIP_INVALID  # LDS path: < 2^31 bytes
 
 
+def test_unaligned_rows_use_direct_to_lds(mm):
+    """Rows that are only 2-byte aligned (odd lda / ldb) stay on the direct-to-LDS path: its
+    16-byte buffer loads then run at 2-byte-aligned addresses, which MI355X serves in ROCm's
+    unaligned memory mode (exact results: the full-size ragged GPU tests).  Odd byte addresses
+    take the register-staged path."""
+    for (M, N, K) in [(4097, 4095, 4111), (4096, 4096, 4111), (1000, 777, 333)]:
+        p = mm.gemm_plan(M, N, K)
+        assert p["direct_to_lds"] == 1, (M, N, K)
+    assert mm.gemm_plan(4096, 4096, 4112, lda=4113)["direct_to_lds"] == 1
+    assert mm.gemm_plan(300, 264, 200, A=3)["direct_to_lds"] == 0
+
+
 def test_contract_descriptor_overflow_rejected(mm):
     """Extents whose product would overflow int64 (2^33 * 2^31) are rejected before they are
     multiplied, by every entry point that reads a descriptor (no GPU needed)."""
