@@ -361,6 +361,42 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_c
     return res
 
 
+def steady_state(name, torch, mmm, seconds: float):
+    """The workload launched back to back for `seconds` (the first 60% untimed, so the power
+    controller settles), then: throughput over the rest (HIP events around it), the SMU's
+    gfx clock and socket power read right after (amdsmi, refreshed about once a second), and
+    the in-kernel clock of 20 clock-recording launches that follow."""
+    W = make_workload(name, torch, mmm)
+    M, N, K = W["M"], W["N"], W["K"]
+    work = W.get("bytes", 2.0 * M * N * K)
+    fn = W["launch"]
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.6 * seconds:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = 0
+    e0.record()
+    t1 = time.perf_counter()
+    while time.perf_counter() - t1 < 0.4 * seconds:
+        for _ in range(20):
+            fn()
+        n += 20
+        torch.cuda.synchronize()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    out = {"seconds": seconds, "launches_timed": n, "ms_per_launch": round(ms, 5), "smi": smi_snapshot()}
+    if "bytes" in W:
+        out["gbs"] = round(work / (ms * 1e-3) / 1e9, 1)
+    else:
+        out["tflops"] = round(work / (ms * 1e-3) / 1e12, 1)
+    if W.get("clocked"):
+        out["clock"] = clocked_pass(torch, mmm, W, 20)
+    return out
+
+
 # shapes of the tile sweep (--sweep): squares, the configs, and tall / wide / deep / shallow cases
 SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
                 (6144, 6144, 6144), (8192, 8192, 8192), (8192, 2048, 2048), (2048, 8192, 2048), (4097, 4095, 4111),
@@ -423,6 +459,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-witness", action="store_true", help="skip the hipBLASLt comparison")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the live MFMA-ceiling probe (gemm8192 only)")
+    ap.add_argument("--steady", type=float, metavar="SECONDS", default=0.0,
+                    help="also run the workload back to back for SECONDS and add its steady-state throughput, "
+                         "SMU clock/power and in-kernel clock to the line (object `steady`)")
     ap.add_argument("--report", metavar="PATH", help="measure every workload and write a JSON report to PATH")
     ap.add_argument("--sweep", metavar="PATH", help="time every tile against the library's pick over a shape "
                                                      "grid and write a markdown table to PATH")
@@ -488,6 +527,8 @@ def main() -> int:
     if "ceiling" in r:
         line["ceiling"] = r["ceiling"]
     line["smi"] = r["smi"]
+    if args.steady > 0:
+        line["steady"] = steady_state(name, torch, mmm, args.steady)
     if "cpu_baseline" in r:
         line["cpu_baseline"] = r["cpu_baseline"]
     if "hipblaslt" in r:

@@ -125,6 +125,11 @@ hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------- tile selection
+#ifndef MMM_PARTIAL_ROUND_BOOST
+#define MMM_PARTIAL_ROUND_BOOST 0.6
+#endif
+constexpr double kPartialRoundBoost = MMM_PARTIAL_ROUND_BOOST;
+
 // Estimated time of a tile launch, in seconds: rounds of 256 concurrent workgroups (one per
 // CU) times the MFMA time of one tile's K range at the tile's relative efficiency (measured
 // at 8192^3, each tile forced: 256x256 1.0, 128x256 0.84, 256x128 0.80, 128x128 0.78) plus a
@@ -139,15 +144,26 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
   const TileSplit sp = gemm_nn_split(p, tile);
   const double tiles = (double)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
   const double per_cu_flops = 4.8e12;  // sustained MFMA rate of one CU under load (256x256 at 8192^3)
-  auto round = [&](double k) { return 2.0 * bm * bn * k / (per_cu_flops * shape[tile].eff) + 3e-6; };
+  // A round with `active` of its 256 slots busy runs each CU faster: the chip is then below its
+  // power cap and keeps a higher clock.  Fitted to the forced-tile times of the 23-shape sweep
+  // (any factor from 0.5 to 0.8 picks the fastest measured tile on every shape; 3072^3 ran 878
+  // TFLOP/s on 144 256x256 tiles against 811 on the 128x256 tile the full-load rate preferred).
+  auto round = [&](double k, double active) {
+    const double boost = 1.0 + kPartialRoundBoost * (1.0 - std::min(active, 256.0) / 256.0);
+    return 2.0 * bm * bn * k / (per_cu_flops * shape[tile].eff * boost) + 3e-6;
+  };
+  auto rounds = [&](double n, double k) {  // n workgroups of K depth k, in rounds of 256
+    const double full = std::floor(n / 256.0), rest = n - full * 256.0;
+    return full * round(k, 256.0) + (rest > 0.0 ? round(k, rest) : 0.0);
+  };
   const double k_full = std::ceil((double)p.K / 64.0) * 64.0;
   double t;
   if (sp.splits > 1) {
-    const double whole_rounds = std::ceil((tiles - sp.tiles) / 256.0);
-    t = whole_rounds * round(k_full) + round(std::ceil((double)p.K / sp.splits / 64.0) * 64.0) +
+    t = rounds(tiles - sp.tiles, k_full) +
+        round(std::ceil((double)p.K / sp.splits / 64.0) * 64.0, (double)sp.tiles * sp.splits) +
         (double)sp.tiles * bm * bn * 4.0 * (2.0 * sp.splits + 1) / kSplitTrafficBps + 3e-6;
   } else {
-    t = std::ceil(tiles / 256.0) * round(k_full);
+    t = rounds(tiles, k_full);
   }
   *splits_out = sp.splits;
   return t;

@@ -19,7 +19,7 @@ import yaml
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 REPO_ROOT = os.path.dirname(PKG_ROOT)
-SOURCES = ["csrc/mmm_gemm.hip", "csrc/mmm_skinny.hip", "csrc/mmm_check.hip", "csrc/mmm_capi.hip"]
+SOURCES = ["csrc/mmm_gemm.hip", "csrc/mmm_skinny.hip", "csrc/mmm_check.hip", "csrc/mmm_capi.hip", "csrc/mmm_probe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I../include", "-Icsrc", "-S", "--offload-device-only"]
