@@ -78,6 +78,12 @@ DESCRIPTIONS = {
 }
 
 
+def data_description(name: str) -> str:
+    """The distribution and seed part of a workload's description ("U[-1,1) seed 1", "zeros")."""
+    m = re.search(r"(U\[-1,1\) seed \d+|N\(0,1\)\*0\.1 seed \d+|zeros)", DESCRIPTIONS[name])
+    return DESCRIPTIONS[name][m.start():] if m else DESCRIPTIONS[name]
+
+
 def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
@@ -331,8 +337,9 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_c
         tf = flops / (clk["ms_per_launch"] * 1e-3) / 1e12
         clk["tflops"] = round(tf, 1)
         clk["pct_peak_at_clock"] = round(100.0 * tf / (256 * 4096 * clk["sclk_mhz"] * 1e6 / 1e12), 2)
-        clk["method"] = ("in-kernel: workgroup 0's s_memtime / s_memrealtime at its start and end "
-                         "(mmm_gemm_f16f32_clocked), over `launches` launches right after the timed region; "
+        entry = {"mfma_ceiling": "mmm_probe_mfma_ceiling"}.get(name, "mmm_gemm_f16f32_clocked")
+        clk["method"] = (f"in-kernel: workgroup 0's s_memtime / s_memrealtime at its start and end ({entry}), "
+                         "over `launches` launches right after the timed region; "
                          "tflops and pct_peak_at_clock are those launches' own")
         res["clock"] = clk
     res["smi"] = smi_snapshot()
@@ -516,7 +523,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16 (f32 accumulate)",
-        "data": f"synthetic: seeded on-device generator, {DESCRIPTIONS[name].split(', ', 1)[1]}",
+        "data": f"synthetic: seeded on-device generator, {data_description(name)}",
         "config": {"workload": DESCRIPTIONS[name], "M": M, "N": N, "K": K},
         "pct_peak": round(100.0 * r["tflops"] / PEAK_TFLOPS, 2),
         "launch_ms": {k: round(v, 5) for k, v in r["launch_ms"].items()},
