@@ -1529,6 +1529,15 @@ struct DmaCfg<128, 256> {
 };
 template <int BM, int BN>
 using DmaTile = typename DmaCfg<BM, BN>::T;
+// The 128x128 tile in a launch of at most one round (one workgroup per CU): no second
+// workgroup on the CU covers the load latency, so the ring is one stage deeper.  Measured on
+// MI355X (interleaved runs, same box): 2048^3 567 -> 624 TFLOP/s, 2048^2 x 4096 720 -> 791,
+// 1024^2 x 8192 (K split) 508 -> 540; 4 stages no better than 3.  Grids of more rounds keep two
+// workgroups per CU on the 2-stage ring (3072^3 on 128x128: 809 against 686 for 3 stages).
+#ifndef MMM_T1_DEEP_STAGES
+#define MMM_T1_DEEP_STAGES 3
+#endif
+using DeepTile128 = Tile<128, 128, 2, 2, 64, MMM_T1_DEEP_STAGES, 1, MMM_T1_MF>;
 // The folded direct-to-LDS kernel: the 256x256 tile's waves and ring.
 #ifndef MMM_FOLD_MF
 #define MMM_FOLD_MF 16
@@ -1623,6 +1632,12 @@ static bool persistent_ok(const GemmProblem& p) {
   return (p.K + TP::BK - 1) / TP::BK >= TP::STAGES + 1;
 }
 
+// Workgroups of a non-persistent tile launch (whole tiles plus the split tiles' K ranges).
+static int64_t launch_blocks(const GemmProblem& p, int bm, int bn) {
+  const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+  return p.k_splits > 1 ? tiles - p.split_tiles + (int64_t)p.split_tiles * p.k_splits : tiles;
+}
+
 bool gemm_nn_persistent(const GemmProblem& p0, int tile_id) {
   if (!MMM_PERSIST || tile_id != kTile256x256) return false;
   GemmProblem p = p0;
@@ -1688,8 +1703,9 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
       return dma_ok(p, 256) ? launch_nn<DmaTile<256, 128>, false>(p, stream)
                             : launch_nn<RegTile<256, 128>, true>(p, stream);
     case kTile128x128:
-      return dma_ok(p, 128) ? launch_nn<DmaTile<128, 128>, false>(p, stream)
-                            : launch_nn<RegTile<128, 128>, true>(p, stream);
+      if (!dma_ok(p, 128)) return launch_nn<RegTile<128, 128>, true>(p, stream);
+      return launch_blocks(p, 128, 128) <= 256 ? launch_nn<DeepTile128, false>(p, stream)
+                                                : launch_nn<DmaTile<128, 128>, false>(p, stream);
     default:
       return hipErrorInvalidValue;
   }
