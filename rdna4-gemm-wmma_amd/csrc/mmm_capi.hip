@@ -135,12 +135,12 @@ constexpr double kPartialRoundBoost = MMM_PARTIAL_ROUND_BOOST;
 // at 8192^3, each tile forced: 256x256 1.0, 128x256 0.84, 256x128 0.80, 128x128 0.78) plus a
 // fixed per-round cost (prologue, epilogue).  With a K split (gemm_nn_split) the split tiles'
 // round runs K / splits, and the reduction's traffic and launch are added.
+#ifndef MMM_T0_EFF
+#define MMM_T0_EFF 0.45
+#endif
 static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
-  static const struct {
-    int bm, bn;
-    double eff;
-  } shape[4] = {{256, 256, 1.0}, {128, 256, 0.84}, {256, 128, 0.80}, {128, 128, 0.78}};
-  const int bm = shape[tile].bm, bn = shape[tile].bn;
+  static const double eff[kTileCount] = {1.0, 0.84, 0.80, 0.78, MMM_T0_EFF};
+  const int bm = tile_bm(tile), bn = tile_bn(tile);
   const TileSplit sp = gemm_nn_split(p, tile);
   const double tiles = (double)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
   const double per_cu_flops = 4.8e12;  // sustained MFMA rate of one CU under load (256x256 at 8192^3)
@@ -150,7 +150,7 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
   // TFLOP/s on 144 256x256 tiles against 811 on the 128x256 tile the full-load rate preferred).
   auto round = [&](double k, double active) {
     const double boost = 1.0 + kPartialRoundBoost * (1.0 - std::min(active, 256.0) / 256.0);
-    return 2.0 * bm * bn * k / (per_cu_flops * shape[tile].eff * boost) + 3e-6;
+    return 2.0 * bm * bn * k / (per_cu_flops * eff[tile] * boost) + 3e-6;
   };
   auto rounds = [&](double n, double k) {  // n workgroups of K depth k, in rounds of 256
     const double full = std::floor(n / 256.0), rest = n - full * 256.0;
@@ -174,7 +174,7 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
 static int pick_tile(const GemmProblem& p) {
   int best = kTile256x256, s = 1;
   double best_cost = 1e300;
-  for (int tile : {kTile256x256, kTile128x256, kTile256x128, kTile128x128}) {
+  for (int tile : {kTile256x256, kTile128x256, kTile256x128, kTile128x128, kTile64x64}) {
     const double c = tile_cost(p, tile, &s);
     if (c < best_cost * 0.97) {
       best_cost = c;
@@ -184,8 +184,6 @@ static int pick_tile(const GemmProblem& p) {
   return best;
 }
 
-static int tile_rows_of(int tile) { return tile == kTile256x256 || tile == kTile256x128 ? 256 : 128; }
-static int tile_cols_of(int tile) { return tile == kTile256x256 || tile == kTile128x256 ? 256 : 128; }
 
 // What mmm_gemm_f16f32 launches for a validated problem.
 struct GemmPlan {
@@ -233,6 +231,7 @@ static int tile_from_params(int wave_m, int wave_n, int waves_i, int waves_j) {
   if (wave_m == 2 && wave_n == 4) return kTile128x256;
   if (wave_m == 4 && wave_n == 2) return kTile256x128;
   if (wave_m == 2 && wave_n == 2) return kTile128x128;
+  if (wave_m == 1 && wave_n == 1) return kTile64x64;
   return -1;
 }
 
@@ -397,10 +396,10 @@ hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const floa
   *plan = mmm_gemm_plan{};
   plan->kernel = pl.kind;
   if (pl.tile >= 0) {
-    static const int params[4][4] = {{4, 4, 2, 2}, {2, 4, 2, 2}, {4, 2, 2, 2}, {2, 2, 2, 2}};
+    static const int params[kTileCount][4] = {{4, 4, 2, 2}, {2, 4, 2, 2}, {4, 2, 2, 2}, {2, 2, 2, 2}, {1, 1, 2, 2}};
     plan->wave_m = params[pl.tile][0], plan->wave_n = params[pl.tile][1];
     plan->waves_i = params[pl.tile][2], plan->waves_j = params[pl.tile][3];
-    plan->block_m = tile_rows_of(pl.tile), plan->block_n = tile_cols_of(pl.tile);
+    plan->block_m = tile_bm(pl.tile), plan->block_n = tile_bn(pl.tile);
     plan->tile_rows = pl.tile_rows;
     plan->tile_workgroups = (int64_t)((pl.tile_rows + plan->block_m - 1) / plan->block_m) *
                             ((N + plan->block_n - 1) / plan->block_n);

@@ -125,6 +125,14 @@ struct Tile {
   // distinct bank groups).  16x16 fragments: those 32 lanes read rows k .. k+3 and k+8 .. k+11
   // (2 chunks each), so rows with bit 3 set also flip chunk bit 1 ({2, 4, 8, 14}).
   static __device__ __forceinline__ int swz_bk(int k) {
+    if constexpr (CB == 8) {
+      // Rows of 128 B (BN = 64): rows k and k+1 fill one 256-byte bank window, so rows 0..3
+      // take the window's four 64-byte quarters with {0, 0, 4, 4}; 16x16 fragments read rows
+      // k and k+8 at the same two chunks, so bit 3 of k flips chunk bit 1 as for wider rows.
+      const int s = (k & 2) << 1;
+      if constexpr (MF == 16) return s ^ (((k >> 3) & 1) << 1);
+      else return s;
+    }
     const int s = (0xCA60 >> (4 * (k & 3))) & 15;
     if constexpr (MF == 16) return s ^ (((k >> 3) & 1) << 1);
     else return s;
@@ -134,7 +142,7 @@ struct Tile {
   static_assert(BK == 32 || BK == 64, "K step must be 32 or 64");
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32x32");
   static_assert(FN <= 4 && KSTEPS * APAR <= 4, "at most 4 B fragments and 4 A offsets per wave");
-  static_assert(CB >= 16, "B swizzle needs rows of at least 16 chunks (BN >= 128)");
+  static_assert(CB == 8 || CB >= 16, "B swizzle: rows of 8 chunks (BN = 64) or at least 16 (BN >= 128)");
   static_assert((BM * CA) % NT == 0 && (BK * CB) % NT == 0, "chunks must divide evenly over threads");
   static_assert(STAGES >= 2 && OCC * STAGES * STAGE <= 160 * 1024, "LDS rings must fit the 160 KB LDS");
 };
@@ -1515,6 +1523,19 @@ template <int BM, int BN>
 struct DmaCfg {  // 128x128
   using T = Tile<BM, BN, 2, 2, 64, 2, 2, MMM_T1_MF>;
 };
+// 64x64: for grids too small to fill the chip with 128x128 tiles (1024^3 is 64 of those, 256
+// of these).  Four waves of 32x32 (2 x 2 16x16x32 fragments each) on a 3-stage ring (48 KB).
+// Measured on MI355X against the 128x128 tile (interleaved runs, same box): 1024^3 139 -> 200
+// TFLOP/s, 512^3 23.8 -> 30.4, 768^3 67 -> 96, 1024^2 x 2048 207 -> 297; it loses where 128x128
+// tiles fill a round or split well (1536^3 333 vs 365, 2048^3 515 vs 640).  8 stages (K = 512
+// in flight at once) ran 3-7% slower than 3 or 4; two workgroups per CU at 2 stages, slower still.
+#ifndef MMM_T0_STAGES
+#define MMM_T0_STAGES 3
+#endif
+template <>
+struct DmaCfg<64, 64> {
+  using T = Tile<64, 64, 2, 2, 64, MMM_T0_STAGES, 1, 16>;
+};
 template <>
 struct DmaCfg<256, 256> {
   using T = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1, MMM_DMA_MF>;
@@ -1570,7 +1591,7 @@ static bool tail_aligned(const GemmProblem& p) {
 }
 
 bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id) {
-  return dma_ok(p, tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128);
+  return dma_ok(p, tile_bm(tile_id));
 }
 
 // K split for a tile launch whose last round of 256 workgroups (one per CU) is less than half
@@ -1581,8 +1602,7 @@ bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id) {
 // reduction reads them and writes C) and launch.  Direct-to-LDS path only.
 TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
   if (!gemm_nn_direct_to_lds(p, tile_id)) return {1, 0};
-  const int bm = tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128;
-  const int bn = tile_id == kTile256x256 || tile_id == kTile128x256 ? 256 : 128;
+  const int bm = tile_bm(tile_id), bn = tile_bn(tile_id);
   const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
   // workgroups one round holds: one per CU, times the tile's workgroups per CU when counted
   const int occ = MMM_SPLIT_OCC ? (tile_id == kTile256x256 ? 1 : tile_id == kTile128x128 ? 2 : MMM_T2_OCC) : 1;
@@ -1612,8 +1632,7 @@ int gemm_nn_splits(const GemmProblem& p, int tile_id) { return gemm_nn_split(p, 
 size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id) {
   const TileSplit sp = gemm_nn_split(p, tile_id);
   if (sp.splits < 2) return 0;
-  const size_t bm = tile_id == kTile256x256 || tile_id == kTile256x128 ? 256 : 128;
-  const size_t bn = tile_id == kTile256x256 || tile_id == kTile128x256 ? 256 : 128;
+  const size_t bm = tile_bm(tile_id), bn = tile_bn(tile_id);
   return (size_t)sp.tiles * sp.splits * bm * bn * 4;
 }
 
@@ -1706,6 +1725,8 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
       if (!dma_ok(p, 128)) return launch_nn<RegTile<128, 128>, true>(p, stream);
       return launch_blocks(p, 128, 128) <= 256 ? launch_nn<DeepTile128, false>(p, stream)
                                                 : launch_nn<DmaTile<128, 128>, false>(p, stream);
+    case kTile64x64:
+      return dma_ok(p, 64) ? launch_nn<DmaTile<64, 64>, false>(p, stream) : launch_nn<RegTile<64, 64>, true>(p, stream);
     default:
       return hipErrorInvalidValue;
   }

@@ -194,7 +194,7 @@ def test_exact_integer(mm, cuda, shape):
     assert np.array_equal(C, truth), f"max |diff| {np.abs(C - truth).max()}"
 
 
-@pytest.mark.parametrize("tile", ["256x256", "128x256", "256x128", "128x128"])
+@pytest.mark.parametrize("tile", ["256x256", "128x256", "256x128", "128x128", "64x64"])
 @pytest.mark.parametrize("K", [264, 263])
 def test_exact_every_tile(mm, cuda, tile, K):
     """Every instantiated tile, on both the direct-to-LDS (K=264) and generic (K=263) paths."""
@@ -391,7 +391,7 @@ def test_stream_graph_capture(mm, cuda, rows, ws):
 
 # shapes whose launch splits K: streaming (16 and 40 rows), one small round of tiles, a partly
 # filled last round (with a gathered K tail), and the 128x128 tile
-WS_SHAPES = [(16, 8192, 2048), (40, 4096, 4096), (1024, 1024, 8192), (4357, 4095, 4111), (300, 264, 2048)]
+WS_SHAPES = [(16, 8192, 2048), (40, 4096, 4096), (1024, 1024, 8192), (4357, 4095, 4111), (300, 264, 4096)]
 
 
 @pytest.mark.parametrize("shape", WS_SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -474,7 +474,8 @@ def test_exact_tail_split(mm, cuda, case):
 
 
 # (M, N, K, tile or None) -> K splits of the tile kernel
-TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((65, 4096, 4096, None), 8), ((300, 264, 2048, None), 4),
+TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((65, 4096, 4096, None), 8), ((300, 264, 2048, "128x128"), 4),
+               ((65, 128, 4096, None), 8), ((100, 200, 3000, "64x64"), 8),
                ((100, 200, 1001, None), 1), ((256, 512, 4096, "256x256"), 8), ((256, 512, 2048, "256x128"), 4),
                ((200, 300, 3000, "128x256"), 5), ((2000, 2000, 512, None), 1)]
 
@@ -494,7 +495,8 @@ def test_exact_tile_splits(mm, cuda, case):
 
 # Grids of several rounds of workgroups, on every tile, with row/column edges and a K tail.
 LARGE_GRIDS = [((8192, 4096, 128), "256x256"), ((8190, 4104, 200), "256x256"), ((8192, 4096, 520), "256x128"),
-           ((4096, 8192, 64), "128x256"), ((4096, 4096, 192), "128x128"), ((4000, 4100, 136), "128x128")]
+           ((4096, 8192, 64), "128x256"), ((4096, 4096, 192), "128x128"), ((4000, 4100, 136), "128x128"),
+           ((2048, 2048, 192), "64x64"), ((2000, 1100, 136), "64x64")]
 
 
 @pytest.mark.parametrize("case", LARGE_GRIDS, ids=lambda c: "x".join(map(str, c[0])) + "-" + c[1])
@@ -550,7 +552,7 @@ def test_concurrent_host_threads(mm, cuda):
     import threading
 
     rng = np.random.default_rng(12)
-    cases = [_exact_case(rng, *shp) for shp in [(16, 8192, 2048), (1024, 512, 4096), (8, 4096, 4096), (300, 264, 2048)]]
+    cases = [_exact_case(rng, *shp) for shp in [(16, 8192, 2048), (1024, 512, 4096), (8, 4096, 4096), (300, 264, 4096)]]
     dev = [(to_dev(cuda, A), to_dev(cuda, B), truth) for A, B, truth in cases]
     results, errors = {}, []
 
@@ -773,7 +775,7 @@ def test_fill_normal_matches_oracle(mm, cuda, orc):
 
 
 # ------------------------------------------------------------------------------ bound launchers
-@pytest.mark.parametrize("shape,ws", [((16, 8192, 2048), None), ((16, 4095, 4111), False), ((300, 264, 2048), None),
+@pytest.mark.parametrize("shape,ws", [((16, 8192, 2048), None), ((16, 4095, 4111), False), ((300, 264, 4096), None),
                                       ((1024, 1024, 1024), None)],
                          ids=["skinny-split", "skinny-no-workspace", "tile-split", "tile"])
 def test_bind_gemm(mm, cuda, shape, ws):

@@ -262,6 +262,10 @@ def test_gemm_plan(mm):
     p = mm.gemm_plan(32, 28672, 8192)  # 224 strips fill the chip unsplit
     assert p["stream_splits"] == 1 and p["stream_workgroups"] == 224
     assert mm.gemm_plan(65, 8192, 8192)["kernel"] == "tile"
+    # grids too small for 128x128 tiles to fill the chip take 64x64 tiles (1024^3: 256 of them)
+    p = mm.gemm_plan(1024, 1024, 1024)
+    assert (p["block_m"], p["block_n"], p["wave_m"], p["wave_n"], p["tile_workgroups"]) == (64, 64, 1, 1, 256)
+    assert mm.gemm_plan(2048, 2048, 2048)["block_m"] == 128  # a full round of 128x128 tiles
     # under-filled last round: 576 tiles = 2 rounds + 64; those 64 run as 4 K ranges each
     p = mm.gemm_plan(6144, 6144, 6144)
     assert (p["block_m"], p["tile_splits"], p["tile_split_tiles"], p["tile_workgroups"]) == (256, 4, 64, 576)
