@@ -111,7 +111,9 @@ hipError_t mmm_gemm_workspace_f16f32(const mmm_half* A, const mmm_half* B, const
  *   (4,4,2,2) 256x256 -- 8 waves (2 x 4) of 128x64, v_mfma_f32_16x16x32_f16, 64-deep K steps;
  *   (2,4,2,2) 128x256, (4,2,2,2) 256x128 -- 4 waves, v_mfma_f32_32x32x16_f16, 32-deep K steps;
  *   (2,2,2,2) 128x128 -- 4 waves, v_mfma_f32_32x32x16_f16, 64-deep K steps;
- *   (1,1,2,2) 64x64 -- 4 waves, v_mfma_f32_16x16x32_f16, 64-deep K steps.
+ *   (1,1,2,2) 64x64 -- 4 waves, v_mfma_f32_16x16x32_f16, 64-deep K steps;
+ *   (3,3,2,2) 192x192 -- 8 waves (2 x 4) of 96x48, v_mfma_f32_16x16x32_f16, 64-deep K steps
+ *             (direct-to-LDS problems; others run the 128x128 register-staged kernel).
  * Other parameter sets return hipErrorInvalidValue.  The workspace (NULL allowed) serves the
  * tile's K split as in mmm_gemm_f16f32_ws.
  */

@@ -30,7 +30,7 @@ inline hipError_t WMMA_Swizzled_Full(const mmm_half* A, const mmm_half* B, float
   // gfx950 instantiations (32x32 MFMA tiles per wave, 2x2 waves): block tile -> parameters
   constexpr int wm = BLOCK_M / 64, wn = BLOCK_N / 64;
   constexpr bool have = ((BLOCK_M == 128 || BLOCK_M == 256) && (BLOCK_N == 128 || BLOCK_N == 256)) ||
-                        (BLOCK_M == 64 && BLOCK_N == 64);
+                        (BLOCK_M == 64 && BLOCK_N == 64) || (BLOCK_M == 192 && BLOCK_N == 192);
   if constexpr (have)
     return mmm_gemm_f16f32_tiled(A, B, C, DIM_I, DIM_J, DIM_K, DIM_K, DIM_J, DIM_J, wm, wn, 2, 2, nullptr, 0, stream);
   else

@@ -132,14 +132,21 @@ constexpr double kPartialRoundBoost = MMM_PARTIAL_ROUND_BOOST;
 
 // Estimated time of a tile launch, in seconds: rounds of 256 concurrent workgroups (one per
 // CU) times the MFMA time of one tile's K range at the tile's relative efficiency (measured
-// at 8192^3, each tile forced: 256x256 1.0, 128x256 0.84, 256x128 0.80, 128x128 0.78) plus a
-// fixed per-round cost (prologue, epilogue).  With a K split (gemm_nn_split) the split tiles'
-// round runs K / splits, and the reduction's traffic and launch are added.
+// at 8192^3, each tile forced: 256x256 1.0, 128x256 0.84, 256x128 0.80, 128x128 0.78; 192x192
+// 0.85 and 64x64 0.40 there, priced at 0.90 and 0.45, which pick the faster tile on the shapes
+// measured for them: 192x192 on 3072^3, 3072^2 x 8192 and 4357 x 4095 x 4111, 256x256 on
+// 2304^2 x 8192, 4608^2 x 8192, 6144^3, 6144^2 x 2048 and 3000 x 5000 x 1000; 64x64 on 256^3
+// to 1024^2 x 2048, 128x128 from 1536^3) plus a fixed per-round cost (prologue, epilogue).
+// With a K split (gemm_nn_split) the split tiles' round runs K / splits, and the reduction's
+// traffic and launch are added.
 #ifndef MMM_T0_EFF
 #define MMM_T0_EFF 0.45
 #endif
+#ifndef MMM_T3_EFF
+#define MMM_T3_EFF 0.90
+#endif
 static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
-  static const double eff[kTileCount] = {1.0, 0.84, 0.80, 0.78, MMM_T0_EFF};
+  static const double eff[kTileCount] = {1.0, 0.84, 0.80, 0.78, MMM_T0_EFF, MMM_T3_EFF};
   const int bm = tile_bm(tile), bn = tile_bn(tile);
   const TileSplit sp = gemm_nn_split(p, tile);
   const double tiles = (double)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
@@ -174,7 +181,8 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
 static int pick_tile(const GemmProblem& p) {
   int best = kTile256x256, s = 1;
   double best_cost = 1e300;
-  for (int tile : {kTile256x256, kTile128x256, kTile256x128, kTile128x128, kTile64x64}) {
+  for (int tile : {kTile256x256, kTile128x256, kTile256x128, kTile128x128, kTile64x64, kTile192x192}) {
+    if (tile == kTile192x192 && !gemm_nn_direct_to_lds(p, tile)) continue;  // direct-to-LDS only
     const double c = tile_cost(p, tile, &s);
     if (c < best_cost * 0.97) {
       best_cost = c;
@@ -232,6 +240,7 @@ static int tile_from_params(int wave_m, int wave_n, int waves_i, int waves_j) {
   if (wave_m == 4 && wave_n == 2) return kTile256x128;
   if (wave_m == 2 && wave_n == 2) return kTile128x128;
   if (wave_m == 1 && wave_n == 1) return kTile64x64;
+  if (wave_m == 3 && wave_n == 3) return kTile192x192;
   return -1;
 }
 
@@ -396,7 +405,8 @@ hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const floa
   *plan = mmm_gemm_plan{};
   plan->kernel = pl.kind;
   if (pl.tile >= 0) {
-    static const int params[kTileCount][4] = {{4, 4, 2, 2}, {2, 4, 2, 2}, {4, 2, 2, 2}, {2, 2, 2, 2}, {1, 1, 2, 2}};
+    static const int params[kTileCount][4] = {{4, 4, 2, 2}, {2, 4, 2, 2}, {4, 2, 2, 2},
+                                              {2, 2, 2, 2}, {1, 1, 2, 2}, {3, 3, 2, 2}};
     plan->wave_m = params[pl.tile][0], plan->wave_n = params[pl.tile][1];
     plan->waves_i = params[pl.tile][2], plan->waves_j = params[pl.tile][3];
     plan->block_m = tile_bm(pl.tile), plan->block_n = tile_bn(pl.tile);

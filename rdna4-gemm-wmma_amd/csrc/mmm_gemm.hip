@@ -125,10 +125,12 @@ struct Tile {
   // distinct bank groups).  16x16 fragments: those 32 lanes read rows k .. k+3 and k+8 .. k+11
   // (2 chunks each), so rows with bit 3 set also flip chunk bit 1 ({2, 4, 8, 14}).
   static __device__ __forceinline__ int swz_bk(int k) {
-    if constexpr (CB == 8) {
-      // Rows of 128 B (BN = 64): rows k and k+1 fill one 256-byte bank window, so rows 0..3
-      // take the window's four 64-byte quarters with {0, 0, 4, 4}; 16x16 fragments read rows
-      // k and k+8 at the same two chunks, so bit 3 of k flips chunk bit 1 as for wider rows.
+    if constexpr (CB == 8 || CB == 24) {
+      // Rows of 128 or 384 B (BN = 64, 192): rows k and k+1 start half a 256-byte bank window
+      // apart, so {0, 0, 4, 4} by k % 4 puts rows k..k+3 on the four distinct 64-byte quarters
+      // of their windows; 16x16 fragments read rows k and k+8 at the same two chunks, so bit 3
+      // of k flips chunk bit 1 as for wider rows.  XOR values below 8 keep every chunk inside
+      // its group of 8, so a 24-chunk row stays a permutation of itself.
       const int s = (k & 2) << 1;
       if constexpr (MF == 16) return s ^ (((k >> 3) & 1) << 1);
       else return s;
@@ -140,9 +142,15 @@ struct Tile {
   static constexpr int SWZ_B_ROWS = MF == 16 ? 16 : 4;  // swz_bk depends on k % SWZ_B_ROWS
   static_assert(MF == 32 || (MF == 16 && BK == 64), "MFMA shape (16x16 fragments with 64-deep stages)");
   static_assert(BK == 32 || BK == 64, "K step must be 32 or 64");
-  static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be a multiple of 32x32");
+  static_assert(TM % 32 == 0 && (TN % 32 == 0 || (MF == 16 && TN % 16 == 0)),
+                "wave tile must be a multiple of 32x32 (32 x 16 with 16x16 fragments)");
   static_assert(FN <= 4 && KSTEPS * APAR <= 4, "at most 4 B fragments and 4 A offsets per wave");
-  static_assert(CB == 8 || CB >= 16, "B swizzle: rows of 8 chunks (BN = 64) or at least 16 (BN >= 128)");
+  static_assert(CB == 8 || CB == 24 || CB >= 16, "B swizzle: rows of 8 or 24 chunks or at least 16");
+  // B staging: chunk slot s = r*NT + w*64 + lane of a stage's [BK][CB] chunk grid is row s / CB.
+  // When CB divides 64, a wave's slots are whole rows, rows advance by NT / CB per r and the
+  // logical chunk is the same for every r (one base offset plus a uniform step per r);
+  // otherwise (BN = 192) each r has its own row and chunk.
+  static constexpr bool B_UNIFORM = 64 % CB == 0;
   static_assert((BM * CA) % NT == 0 && (BK * CB) % NT == 0, "chunks must divide evenly over threads");
   static_assert(STAGES >= 2 && OCC * STAGES * STAGE <= 160 * 1024, "LDS rings must fit the 160 KB LDS");
 };
@@ -519,11 +527,25 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   // and RPB = NT/CB rows of B, so slot rows are row0 + r*RP; RPA is a multiple of the rows
   // the A swizzle depends on and RPB of 4, so the logical chunk is the same every round.
   constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
-  static_assert(RPA % T::SWZ_A_ROWS == 0 && RPB % T::SWZ_B_ROWS == 0, "round strides must preserve the swizzle");
+  static_assert(RPA % T::SWZ_A_ROWS == 0 && (!T::B_UNIFORM || RPB % T::SWZ_B_ROWS == 0),
+                "round strides must preserve the swizzle");
+  static_assert(!GENERIC || T::B_UNIFORM, "the register-staged path uses the uniform B map");
   const int a_row0 = w * (64 / T::CA) + lane / T::CA;
   const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
-  const int b_row0 = w * (64 / T::CB) + lane / T::CB;
-  const int b_nc = 8 * ((lane % T::CB) ^ T::swz_bk(b_row0));
+  const int b_row0 = T::B_UNIFORM ? w * (64 / T::CB) + lane / T::CB : 0;
+  const int b_nc = T::B_UNIFORM ? 8 * ((lane % T::CB) ^ T::swz_bk(b_row0)) : 0;
+  // B row and column of slot r (any CB)
+  auto b_row_of = [&](int r) {
+    if constexpr (T::B_UNIFORM) return b_row0 + r * RPB;
+    else return (r * T::NT + w * 64 + lane) / T::CB;
+  };
+  auto b_col_of = [&](int r) {
+    if constexpr (T::B_UNIFORM) return b_nc;
+    else {
+      const int sl = r * T::NT + w * 64 + lane;
+      return 8 * ((sl % T::CB) ^ T::swz_bk(sl / T::CB));
+    }
+  };
 
   // ---- fragment read offsets (bytes within a stage).  MF = 32: lane l reads row l % 32 of
   // A, k chunk l / 32 of each 16-deep step; B rows 8*(l/32) + (l/4)%4 (+4), columns
@@ -566,6 +588,11 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
     const uint32_t a_goff = (uint32_t)((a_row0 * lda + a_kc) * 2);
     const uint32_t b_goff = (uint32_t)((b_row0 * ldb + b_nc) * 2);
     const uint32_t a_rstep = (uint32_t)(RPA * lda * 2), b_rstep = (uint32_t)(RPB * ldb * 2);
+    uint32_t b_goffr[T::B_UNIFORM ? 1 : T::RB];  // per-slot B offsets (non-uniform map)
+    if constexpr (!T::B_UNIFORM) {
+#pragma unroll
+      for (int r = 0; r < T::RB; ++r) b_goffr[r] = (uint32_t)((b_row_of(r) * ldb + b_col_of(r)) * 2);
+    }
 
     // DMA of K tile t into ring slot `stage`: RA + RB buffer_load_dwordx4 ... lds per thread.
     // Each range ends at the operand's last element (row M-1, column K-1 of A; row K-1,
@@ -603,7 +630,8 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       if (j < T::RA)
         dma_b128(d.a_dst + j * T::NT * 16, d.ra, d.a_base + j * a_rstep);
       else
-        dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, d.rb, b_goff + (j - T::RA) * b_rstep);
+        dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, d.rb,
+                 T::B_UNIFORM ? b_goff + (j - T::RA) * b_rstep : b_goffr[T::B_UNIFORM ? 0 : j - T::RA]);
     };
     auto issue = [&](int t, int stage) {
       const TileDma d = prep(t, stage);
@@ -635,7 +663,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       }
 #pragma unroll
       for (int r = 0; r < T::RB; ++r) {
-        const int k = k0 + b_row0 + r * RPB, n = n0 + b_nc;
+        const int k = k0 + b_row_of(r), n = n0 + b_col_of(r);
         half8 v = {};
         if (k < K) {
           const _Float16* src = Bh + (int64_t)k * ldb + n;
@@ -1536,6 +1564,15 @@ template <>
 struct DmaCfg<64, 64> {
   using T = Tile<64, 64, 2, 2, 64, MMM_T0_STAGES, 1, 16>;
 };
+// 192x192: 16 x 16 tiles fill one round exactly at 3072 x 3072, where 256x256 tiles leave 112
+// of the 256 CUs idle.  Eight waves of 96x48 (6 x 3 16x16x32 fragments), a 3-stage ring of
+// 48 KB stages; rows of 24 chunks use the per-slot B staging map.  Measured on MI355X
+// (interleaved runs, same box): 3072^3 763 -> 1007 TFLOP/s against the 256x256 tile, 3072^2 x
+// 8192 963 -> 1159, 4357 x 4095 x 4111 805 -> 885; 8192^3 1172 against 1380 (per-CU rate 0.85).
+template <>
+struct DmaCfg<192, 192> {
+  using T = Tile<192, 192, 2, 4, 64, 3, 1, 16>;
+};
 template <>
 struct DmaCfg<256, 256> {
   using T = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1, MMM_DMA_MF>;
@@ -1727,6 +1764,10 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
                                                 : launch_nn<DmaTile<128, 128>, false>(p, stream);
     case kTile64x64:
       return dma_ok(p, 64) ? launch_nn<DmaTile<64, 64>, false>(p, stream) : launch_nn<RegTile<64, 64>, true>(p, stream);
+    case kTile192x192:
+      // the register-staged path has no 192x192 instantiation: 128x128 tiles compute the same C
+      return dma_ok(p, 192) ? launch_nn<DmaTile<192, 192>, false>(p, stream)
+                            : launch_nn<RegTile<128, 128>, true>(p, stream);
     default:
       return hipErrorInvalidValue;
   }

@@ -38,11 +38,15 @@ struct FoldProblem {
   int64_t cm[2], cn[2];  // C strides for (m_hi, m_lo), (n_hi, n_lo)
 };
 
-enum TileId { kTile256x256 = 0, kTile128x256 = 1, kTile256x128 = 2, kTile128x128 = 3, kTile64x64 = 4 };
-constexpr int kTileCount = 5;
+enum TileId { kTile256x256 = 0, kTile128x256 = 1, kTile256x128 = 2, kTile128x128 = 3, kTile64x64 = 4, kTile192x192 = 5 };
+constexpr int kTileCount = 6;
 // Block tile of each TileId (rows x columns of C).
-constexpr int tile_bm(int tile) { return tile == kTile256x256 || tile == kTile256x128 ? 256 : tile == kTile64x64 ? 64 : 128; }
-constexpr int tile_bn(int tile) { return tile == kTile256x256 || tile == kTile128x256 ? 256 : tile == kTile64x64 ? 64 : 128; }
+constexpr int tile_bm(int tile) {
+  return tile == kTile256x256 || tile == kTile256x128 ? 256 : tile == kTile64x64 ? 64 : tile == kTile192x192 ? 192 : 128;
+}
+constexpr int tile_bn(int tile) {
+  return tile == kTile256x256 || tile == kTile128x256 ? 256 : tile == kTile64x64 ? 64 : tile == kTile192x192 ? 192 : 128;
+}
 
 // Effective rate of a K split's partial-tile traffic (written by the split workgroups, read back
 // with C written by the reduction), as the tile planner prices it.  The partials of an

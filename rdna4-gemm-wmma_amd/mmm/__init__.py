@@ -169,7 +169,7 @@ def _check_f16(name: str, t) -> None:
 
 # Tile parameters (WAVE_M, WAVE_N, WAVES_I, WAVES_J) of the instantiated block tiles.
 TILES = {"256x256": (4, 4, 2, 2), "128x256": (2, 4, 2, 2), "256x128": (4, 2, 2, 2), "128x128": (2, 2, 2, 2),
-         "64x64": (1, 1, 2, 2)}
+         "64x64": (1, 1, 2, 2), "192x192": (3, 3, 2, 2)}
 
 # The most workspace any K split uses (the library plans its splits within this).
 MAX_WORKSPACE_BYTES = 64 << 20

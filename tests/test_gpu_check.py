@@ -180,7 +180,7 @@ def test_reference_contraction_every_output(mm, cuda):
     assert bad == 0, f"{bad} outputs out of tolerance (worst {worst:.3g})"
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "64x64"])
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "64x64", "192x192"])
 def test_every_tile_every_output(mm, cuda, tile):
     M, N, K = 2000, 1500, 1032
     A = cuda.empty((M, K), dtype=cuda.float16, device="cuda")

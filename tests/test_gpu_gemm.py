@@ -194,7 +194,7 @@ def test_exact_integer(mm, cuda, shape):
     assert np.array_equal(C, truth), f"max |diff| {np.abs(C - truth).max()}"
 
 
-@pytest.mark.parametrize("tile", ["256x256", "128x256", "256x128", "128x128", "64x64"])
+@pytest.mark.parametrize("tile", ["256x256", "128x256", "256x128", "128x128", "64x64", "192x192"])
 @pytest.mark.parametrize("K", [264, 263])
 def test_exact_every_tile(mm, cuda, tile, K):
     """Every instantiated tile, on both the direct-to-LDS (K=264) and generic (K=263) paths."""
@@ -391,7 +391,7 @@ def test_stream_graph_capture(mm, cuda, rows, ws):
 
 # shapes whose launch splits K: streaming (16 and 40 rows), one small round of tiles, a partly
 # filled last round (with a gathered K tail), and the 128x128 tile
-WS_SHAPES = [(16, 8192, 2048), (40, 4096, 4096), (1024, 1024, 8192), (4357, 4095, 4111), (300, 264, 4096)]
+WS_SHAPES = [(16, 8192, 2048), (40, 4096, 4096), (1024, 1024, 8192), (4357, 4095, 8191), (300, 264, 4096)]
 
 
 @pytest.mark.parametrize("shape", WS_SHAPES, ids=lambda s: "x".join(map(str, s)))
@@ -449,10 +449,28 @@ def test_exact_persistent(mm, cuda, case):
 # (M, N, K) -> (tile, K splits, split tiles): the last round of 256 workgroups is less than half
 # full, so its tiles run as K ranges while the rest run over all of K (0 split tiles: declined,
 # the reduction would cost more than the round it saves)
-TAIL_SPLITS = [((6144, 6144, 2048), ("256x256", 4, 64)), ((3072, 3072, 8192), ("128x256", 8, 32)),
+TAIL_SPLITS = [((6144, 6144, 2048), ("256x256", 4, 64)), ((2560, 3584, 4096), ("128x256", 8, 24)),
                ((4608, 4608, 8192), ("256x256", 3, 68)), ((7168, 7168, 7168), ("256x256", 14, 16)),
-               ((4357, 4095, 4111), ("256x256", 8, 32)), ((2304, 2304, 8192), ("256x256", 3, 81)),
+               ((4357, 4095, 8191), ("256x256", 8, 32)), ((2304, 2304, 8192), ("256x256", 3, 81)),
                ((6150, 6144, 1030), ("256x256", 1, 0))]
+
+
+@pytest.mark.parametrize("shape", [(3072, 3072, 3072), (3072, 3072, 8192), (3000, 3070, 1031)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_exact_192_full_round(mm, cuda, shape):
+    """Shapes the library runs as one round of 192x192 tiles (16 x 16 of them at 3072^2; edges
+    and a gathered K tail in the last case): exact against the on-device fp64 truth."""
+    M, N, K = shape
+    plan = mm.gemm_plan(M, N, K)
+    assert (plan["kernel"], plan["block_m"], plan["block_n"], plan["tile_splits"]) == ("tile", 192, 192, 1)
+    g = cuda.Generator(device="cuda").manual_seed(M + N + K)
+    A = cuda.randint(-4, 5, (M, K), device="cuda", generator=g).half()
+    B = cuda.randint(-4, 5, (K, N), device="cuda", generator=g).half()
+    T, _ = mm.gemm_truth(A, B, with_scale=False)
+    for _ in range(2):
+        C = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+        mm.gemm(A, B, C)
+        assert cuda.equal(C.double(), T), f"{int((C.double() != T).sum())} mismatches"
 
 
 @pytest.mark.parametrize("case", TAIL_SPLITS, ids=lambda c: "x".join(map(str, c[0])))
@@ -475,7 +493,7 @@ def test_exact_tail_split(mm, cuda, case):
 
 # (M, N, K, tile or None) -> K splits of the tile kernel
 TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((65, 4096, 4096, None), 8), ((300, 264, 2048, "128x128"), 4),
-               ((65, 128, 4096, None), 8), ((100, 200, 3000, "64x64"), 8),
+               ((65, 128, 4096, None), 8), ((100, 200, 3000, "64x64"), 5), ((400, 500, 3000, "192x192"), 5),
                ((100, 200, 1001, None), 1), ((256, 512, 4096, "256x256"), 8), ((256, 512, 2048, "256x128"), 4),
                ((200, 300, 3000, "128x256"), 5), ((2000, 2000, 512, None), 1)]
 
@@ -496,7 +514,8 @@ def test_exact_tile_splits(mm, cuda, case):
 # Grids of several rounds of workgroups, on every tile, with row/column edges and a K tail.
 LARGE_GRIDS = [((8192, 4096, 128), "256x256"), ((8190, 4104, 200), "256x256"), ((8192, 4096, 520), "256x128"),
            ((4096, 8192, 64), "128x256"), ((4096, 4096, 192), "128x128"), ((4000, 4100, 136), "128x128"),
-           ((2048, 2048, 192), "64x64"), ((2000, 1100, 136), "64x64")]
+           ((2048, 2048, 192), "64x64"), ((2000, 1100, 136), "64x64"), ((6144, 3072, 192), "192x192"),
+           ((4000, 4100, 136), "192x192")]
 
 
 @pytest.mark.parametrize("case", LARGE_GRIDS, ids=lambda c: "x".join(map(str, c[0])) + "-" + c[1])
