@@ -824,11 +824,12 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
 
   // staging map and fragment offsets: as gemm_nn_kernel
   constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
-  static_assert(RPA % T::SWZ_A_ROWS == 0 && RPB % T::SWZ_B_ROWS == 0, "round strides must preserve the swizzle");
+  static_assert(RPA % T::SWZ_A_ROWS == 0 && (!T::B_UNIFORM || RPB % T::SWZ_B_ROWS == 0),
+                "round strides must preserve the swizzle");
   const int a_row0 = w * (64 / T::CA) + lane / T::CA;
   const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
-  const int b_row0 = w * (64 / T::CB) + lane / T::CB;
-  const int b_nc = 8 * ((lane % T::CB) ^ T::swz_bk(b_row0));
+  const int b_row0 = T::B_UNIFORM ? w * (64 / T::CB) + lane / T::CB : 0;
+  const int b_nc = T::B_UNIFORM ? 8 * ((lane % T::CB) ^ T::swz_bk(b_row0)) : 0;
   uint32_t a_off[4] = {0, 0, 0, 0};
 #pragma unroll
   for (int kk = 0; kk < T::KSTEPS; ++kk)
@@ -855,6 +856,14 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
   uint32_t a_goff = (uint32_t)((a_row0 * lda + a_kc) * 2);
   uint32_t b_goff = (uint32_t)((b_row0 * ldb + b_nc) * 2);
   const uint32_t a_rstep = (uint32_t)(RPA * lda * 2), b_rstep = (uint32_t)(RPB * ldb * 2);
+  uint32_t b_goffr[T::B_UNIFORM ? 1 : T::RB];  // per-slot B offsets (non-uniform map, as gemm_nn_kernel)
+  if constexpr (!T::B_UNIFORM) {
+#pragma unroll
+    for (int r = 0; r < T::RB; ++r) {
+      const int sl = r * T::NT + w * 64 + lane;
+      b_goffr[r] = (uint32_t)(((sl / T::CB) * ldb + 8 * ((sl % T::CB) ^ T::swz_bk(sl / T::CB))) * 2);
+    }
+  }
   const int64_t b_step = (int64_t)T::BK * ldb * 2;
   // per-tile running load state (K tiles are prepared in order from 0)
   const char* a_ptr;
@@ -865,6 +874,10 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
     // first loads are recomputed from them rather than kept live across the K loop (which
     // runs at the register limit).
     asm volatile("" : "+v"(a_goff), "+v"(b_goff), "+v"(a_kc_t));
+    if constexpr (!T::B_UNIFORM) {
+#pragma unroll
+      for (int r = 0; r < T::RB; ++r) asm volatile("" : "+v"(b_goffr[r]));
+    }
     a_ptr = (const char*)(p.A + (int64_t)tm0 * lda);
     b_ptr = (const char*)(p.B + tn0);
     a_left = ((int64_t)(p.M - 1 - tm0) * lda + K) * 2;
@@ -891,7 +904,8 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
     if (j < T::RA)
       dma_b128(d.a_dst + j * T::NT * 16, d.ra, d.a_base + j * a_rstep);
     else
-      dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, d.rb, b_goff + (j - T::RA) * b_rstep);
+      dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, d.rb,
+               T::B_UNIFORM ? b_goff + (j - T::RA) * b_rstep : b_goffr[T::B_UNIFORM ? 0 : j - T::RA]);
   };
   auto issue = [&](int t, int stage) {
     const TileDma d = prep(t, stage);
@@ -1565,7 +1579,9 @@ struct DmaCfg<64, 64> {
   using T = Tile<64, 64, 2, 2, 64, MMM_T0_STAGES, 1, 16>;
 };
 // 192x192: 16 x 16 tiles fill one round exactly at 3072 x 3072, where 256x256 tiles leave 112
-// of the 256 CUs idle.  Eight waves of 96x48 (6 x 3 16x16x32 fragments), a 3-stage ring of
+// of the 256 CUs idle, and whole multiples of 256 tiles run as the persistent grid (6144^2 x
+// 2048: 1024 tiles, four rounds, 1006 -> 1047 TFLOP/s over one workgroup per tile, against 926
+// for 256x256 tiles' 2.25 rounds; 3072 x 6144 x 2048 996 -> 1030, against 888).  Eight waves of 96x48 (6 x 3 16x16x32 fragments), a 3-stage ring of
 // 48 KB stages; rows of 24 chunks use the per-slot B staging map.  Measured on MI355X
 // (interleaved runs, same box): 3072^3 763 -> 1007 TFLOP/s against the 256x256 tile, 3072^2 x
 // 8192 963 -> 1159, 4357 x 4095 x 4111 805 -> 885; 8192^3 1172 against 1380 (per-CU rate 0.85).
@@ -1673,16 +1689,19 @@ size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id) {
   return (size_t)sp.tiles * sp.splits * bm * bn * 4;
 }
 
-// The persistent kernel's conditions: whole interior 256x256 tiles over more than one round of
-// 256 workgroups, aligned operands (no gathered K tile), 4-byte-aligned C, and at
-// least S + 1 K tiles.  Measured against one workgroup per tile (same box): 8192^3 +1%,
-// 8192^2 x 2048 +3.7%, 16384 x 8192 x 1024 +3.8%.
+// The persistent kernel's conditions: whole interior tiles (256x256, or 192x192 without a K
+// split) over more than one round of 256 workgroups, aligned operands (no gathered K tile),
+// 4-byte-aligned C, and at least S + 1 K tiles.  Measured against one workgroup per tile (same
+// box): 8192^3 +1%, 8192^2 x 2048 +3.7%, 16384 x 8192 x 1024 +3.8%; 192x192 at 6144^2 x 2048 +4%.
 #ifndef MMM_PERSIST
 #define MMM_PERSIST 1
 #endif
+#ifndef MMM_PERSIST_192
+#define MMM_PERSIST_192 1
+#endif
+template <class TP = DmaTile<256, 256>>
 static bool persistent_ok(const GemmProblem& p) {
-  using TP = DmaTile<256, 256>;
-  if (!dma_ok(p, 256) || p.tail_regs || !p.c_vec4) return false;
+  if (!dma_ok(p, TP::BM) || p.tail_regs || !p.c_vec4) return false;
   if (p.M % TP::BM || p.N % TP::BN) return false;
   if ((int64_t)(p.M / TP::BM) * (p.N / TP::BN) <= 256) return false;
   return (p.K + TP::BK - 1) / TP::BK >= TP::STAGES + 1;
@@ -1695,11 +1714,12 @@ static int64_t launch_blocks(const GemmProblem& p, int bm, int bn) {
 }
 
 bool gemm_nn_persistent(const GemmProblem& p0, int tile_id) {
-  if (!MMM_PERSIST || tile_id != kTile256x256) return false;
+  if (!MMM_PERSIST || (tile_id != kTile256x256 && tile_id != kTile192x192)) return false;
   GemmProblem p = p0;
   p.c_vec4 = (uintptr_t)p.C % 4 == 0;
   p.tail_regs = !tail_aligned(p);
   p.k_splits = gemm_nn_split(p, tile_id).splits;
+  if (tile_id == kTile192x192) return MMM_PERSIST_192 && p.k_splits <= 1 && persistent_ok<DmaTile<192, 192>>(p);
   return persistent_ok(p);
 }
 
@@ -1765,6 +1785,18 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
     case kTile64x64:
       return dma_ok(p, 64) ? launch_nn<DmaTile<64, 64>, false>(p, stream) : launch_nn<RegTile<64, 64>, true>(p, stream);
     case kTile192x192:
+      if (MMM_PERSIST && MMM_PERSIST_192 && p.k_splits <= 1 && persistent_ok<DmaTile<192, 192>>(p)) {
+        using TP = DmaTile<192, 192>;
+        const int tiles_m = p.M / TP::BM, tiles_n = p.N / TP::BN;
+        const bool nt = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 && p.K >= kNtMinK;
+        if (nt)
+          hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
+                             tiles_n);
+        else
+          hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, false>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
+                             tiles_n);
+        return hipGetLastError();
+      }
       // the register-staged path has no 192x192 instantiation: 128x128 tiles compute the same C
       return dma_ok(p, 192) ? launch_nn<DmaTile<192, 192>, false>(p, stream)
                             : launch_nn<RegTile<128, 128>, true>(p, stream);

@@ -420,16 +420,16 @@ def test_workspace_entry_point(mm, cuda, shape):
         assert bool((ws[need.value:] == 0x5A).all()), "wrote past the queried workspace size"
 
 
-# (M, N, K, C row padding): whole interior 256x256 tiles over several rounds run on the persistent
-# kernel (256 workgroups looping over tiles, next tile's loads issued before this tile's stores)
+# (M, N, K, C row padding): whole interior 256x256 (or 192x192) tiles over several rounds run on the
+# persistent kernel (256 workgroups looping over tiles, next tile's loads issued before this tile's stores)
 PERSISTENT = [(8192, 8192, 8192, 0), (8192, 8192, 2048, 0), (4608, 4096, 192, 0), (2560, 16384, 1024, 0),
-              (4608, 4096, 576, 3)]
+              (4608, 4096, 576, 3), (6144, 6144, 2048, 0), (3072, 6144, 1024, 3)]
 
 
 @pytest.mark.parametrize("case", PERSISTENT, ids=lambda c: "x".join(map(str, c[:3])) + f"-pad{c[3]}")
 def test_exact_persistent(mm, cuda, case):
-    """The persistent tile kernel: exact against the on-device fp64 truth (integer inputs), three
-    calls in a row, with a padded C row stride in one case."""
+    """The persistent tile kernel (256x256 tiles, and 192x192 in the last two cases): exact against
+    the on-device fp64 truth (integer inputs), three calls in a row, with padded C row strides."""
     M, N, K, pad = case
     plan = mm.gemm_plan(M, N, K, ldc=N + pad)
     assert plan["kernel"] == "tile" and plan["tile_persistent"] == 1
@@ -449,7 +449,7 @@ def test_exact_persistent(mm, cuda, case):
 # (M, N, K) -> (tile, K splits, split tiles): the last round of 256 workgroups is less than half
 # full, so its tiles run as K ranges while the rest run over all of K (0 split tiles: declined,
 # the reduction would cost more than the round it saves)
-TAIL_SPLITS = [((6144, 6144, 2048), ("256x256", 4, 64)), ((2560, 3584, 4096), ("128x256", 8, 24)),
+TAIL_SPLITS = [((6144, 6144, 4096), ("256x256", 4, 64)), ((2560, 3584, 4096), ("128x256", 8, 24)),
                ((4608, 4608, 8192), ("256x256", 3, 68)), ((7168, 7168, 7168), ("256x256", 14, 16)),
                ((4357, 4095, 8191), ("256x256", 8, 32)), ((2304, 2304, 8192), ("256x256", 3, 81)),
                ((6150, 6144, 1030), ("256x256", 1, 0))]
