@@ -1,10 +1,12 @@
 """On-device cross-check kernels (mmm_gemm_naive_f16f32, mmm_gemm_truth_f64,
 mmm_contract5d_truth_f64) and full-output validation of every configuration with them.
 
-The cross-check kernels are pinned bit for bit against the CPU oracle on small shapes:
-  * the fp32 naive kernel against the oracle's GEMM_Naive restatement (mmm.cpp:52-62);
+The cross-check kernels are pinned bit for bit against the CPU oracle:
+  * the fp32 naive kernel against the oracle's GEMM_Naive restatement (mmm.cpp:52-62), on small
+    shapes;
   * the fp64 truth and scale against the oracle's fp64 loops (products of fp16 values are
-    exact in fp64 and both sum in ascending k, so they agree exactly).
+    exact in fp64 and both sum in ascending k, so they agree exactly), on small shapes in full
+    and at every configuration's full size on a sampled sub-grid.
 Pinned that way, they validate every element of the full-size outputs on the device with the
 tolerance |C - T| <= 1e-3 * S, S = sum_k |a*b|, instead of a sampled sub-grid.
 """
@@ -67,6 +69,24 @@ def test_truth_matches_oracle_bitwise(mm, cuda, orc, shape):
     Tw, Sw = orc.gemm_f64(A, B)
     assert np.array_equal(T.cpu().numpy(), Tw)
     assert np.array_equal(S.cpu().numpy(), Sw)
+
+
+@pytest.mark.parametrize("shape", [(4097, 4095, 4111), (8192, 2048, 2048), (16, 8192, 8192), (8192, 8192, 8192)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_truth_matches_oracle_at_full_size(mm, cuda, orc, shape):
+    """The fp64 truth kernel at the configurations' full sizes, bit for bit against the oracle on a
+    sampled sub-grid (first, last and spread rows and columns): the every-output checks of those
+    configurations rest on this kernel, so it is pinned at their sizes, not only at small ones."""
+    M, N, K = shape
+    A = orc.uniform_f16((M, K), 29, 0)
+    B = orc.uniform_f16((K, N), 29, 1)
+    T, S = mm.gemm_truth(to_dev(cuda, A), to_dev(cuda, B))
+    rows = np.unique(np.r_[0, 1, M - 1, np.linspace(0, M - 1, 24).astype(np.int64)])
+    cols = np.unique(np.r_[0, N - 1, np.linspace(0, N - 1, 40).astype(np.int64)])
+    Tw, Sw = orc.gemm_f64(A, B, rows=rows, cols=cols)
+    r, c = cuda.as_tensor(rows, device="cuda"), cuda.as_tensor(cols, device="cuda")
+    assert np.array_equal(T[r][:, c].cpu().numpy(), Tw)
+    assert np.array_equal(S[r][:, c].cpu().numpy(), Sw)
 
 
 def test_truth_without_scale(mm, cuda, orc):
