@@ -130,8 +130,9 @@ __global__ __launch_bounds__(256) void read_ceiling_kernel(const u32x4* src, int
 }
 
 // HBM read ceiling, direct to LDS (the tile kernels' staging path): each wave streams 1 KB
-// pieces (64 lanes x 16 bytes, buffer_load_dwordx4 ... lds) into an 8-slot LDS ring, grid-stride
-// over the waves, keeping at most 8 loads in flight.  Nothing reads the ring.
+// pieces (64 lanes x 16 bytes, buffer_load_dwordx4 ... lds, non-temporal like the register
+// probe's loads) into an 8-slot LDS ring, grid-stride over the waves, keeping at most 8 loads in
+// flight.  Nothing reads the ring.
 __global__ __launch_bounds__(256) void read_lds_ceiling_kernel(const void* src, uint32_t bytes, uint32_t* out) {
   __shared__ __attribute__((aligned(1024))) char ring[4 * 8 * 1024];
   const int lane = threadIdx.x & 63;
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(256) void read_lds_ceiling_kernel(const void* src, 
     const uint32_t voff = piece * 1024 + lane * 16;
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds\n\ts_waitcnt vmcnt(7)"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds\n\ts_waitcnt vmcnt(7)"
                  :
                  : "s"(ring_base + slot * 1024), "v"(voff), "s"(rsrc)
                  : "memory", "m0");

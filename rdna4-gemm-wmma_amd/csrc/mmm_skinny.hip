@@ -82,6 +82,14 @@ __device__ __forceinline__ void dma_b128(uint32_t lds_addr, i32x4 rsrc, uint32_t
                : "s"(lds_addr), "v"(voff), "s"(rsrc)
                : "memory", "m0");
 }
+// The same load with the non-temporal policy, for a B operand streamed once from HBM: its lines
+// are not kept in the caches for reuse, so the stream does not evict what the next lines need.
+__device__ __forceinline__ void dma_b128_nt(uint32_t lds_addr, i32x4 rsrc, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 template <int N>
@@ -348,7 +356,8 @@ struct Wide {
   __device__ static __forceinline__ int swz_b(int k) { return ((0xCA60 >> (4 * (k & 3))) & 15) ^ (((k >> 3) & 1) << 1); }
 };
 
-template <int MR>
+// NTB: B's loads are non-temporal (launch_wide: B of at least kNtStreamBytes).
+template <int MR, bool NTB>
 __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p, int strips, int splits,
                                                                   float* partials) {
   using W = Wide<MR>;
@@ -405,7 +414,13 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     }
     const uint32_t bk = (uint32_t)((int64_t)k0 * ldb * 2);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) dma_b128(dst + ABYTES + i * 1024, rb_full, bk + ((i >> 1) & 1 ? b_goff1 : b_goff0) + i * b_rstep);
+    for (int i = 0; i < NB; ++i) {
+      const uint32_t voff = bk + ((i >> 1) & 1 ? b_goff1 : b_goff0) + i * b_rstep;
+      if constexpr (NTB)
+        dma_b128_nt(dst + ABYTES + i * 1024, rb_full, voff);
+      else
+        dma_b128(dst + ABYTES + i * 1024, rb_full, voff);
+    }
   };
   // globally last K slot of an unaligned problem: gathered element by element (same layout)
   const _Float16* Ah = (const _Float16*)p.A;
@@ -593,9 +608,21 @@ bool skinny_ok(const GemmProblem& p) {
   return true;
 }
 
+// B operands this large are streamed with non-temporal loads.  Measured on MI355X (interleaved,
+// three B buffers rotating): 16 x 8192 x 8192 32.9 -> 30.8 us per call, 32 x 8192 x 8192 34.8 ->
+// 32.7, 64 x 14336 x 4096 (112 MiB) 36.6 -> 35.4; with 64 MiB of B (16 x 4096 x 8192: three
+// buffers fit the 256 MB Infinity Cache) 17.5 -> 18.4, slower, so smaller B keeps cached loads.
+// The in-workgroup kernel's 64-byte strips ran 30-40% slower with them (not used there).
+constexpr int64_t kNtStreamBytes = 96ll << 20;
+
 template <int MR>
 static hipError_t launch_wide(const GemmProblem& p, int strips, int splits, float* ws, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm_stream_wide_kernel<MR>, dim3(strips * splits), dim3(256), 0, stream, p, strips, splits, ws);
+  if ((int64_t)p.K * p.N * 2 >= kNtStreamBytes)
+    hipLaunchKernelGGL((gemm_stream_wide_kernel<MR, true>), dim3(strips * splits), dim3(256), 0, stream, p, strips,
+                       splits, ws);
+  else
+    hipLaunchKernelGGL((gemm_stream_wide_kernel<MR, false>), dim3(strips * splits), dim3(256), 0, stream, p, strips,
+                       splits, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   constexpr int ROWS = 16 * MR;
