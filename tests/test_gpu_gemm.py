@@ -178,7 +178,7 @@ def test_config5_skinny_full(orc, mm, cuda):
 EXACT_SHAPES = [
     (256, 256, 256),   # aligned, direct-to-LDS path, one tile
     (300, 264, 200),   # direct-to-LDS path with M/N edge tiles, K tail of 8
-    (257, 129, 77),    # generic path (odd K and N)
+    (257, 129, 77),    # odd K and N: gathered last K tile
     (513, 1000, 1032), # several tiles, K tail 8
     (33, 40, 16),      # smaller than one tile
     (1, 1, 1),
@@ -197,12 +197,48 @@ def test_exact_integer(mm, cuda, shape):
 @pytest.mark.parametrize("tile", ["256x256", "128x256", "256x128", "128x128", "64x64", "192x192"])
 @pytest.mark.parametrize("K", [264, 263])
 def test_exact_every_tile(mm, cuda, tile, K):
-    """Every instantiated tile, on both the direct-to-LDS (K=264) and generic (K=263) paths."""
+    """Every instantiated tile, with whole K tiles (K=264) and a last K tile gathered through VGPRs
+    (K=263, odd N): the direct-to-LDS path (the register-staged one has its own test)."""
     M, N = 333, (520 if K % 8 == 0 else 517)
     rng = np.random.default_rng(K)
     A, B, truth = _int_inputs(rng, M, N, K)
     C = mm.gemm(to_dev(cuda, A), to_dev(cuda, B), tile=tile).cpu().numpy()
     assert np.array_equal(C, truth)
+
+
+def _odd_copy(cuda, X):
+    """X's bytes on the device at an odd byte address: (buffer, address).  fp16 data there can only
+    be read by the register-staged kernels (the direct-to-LDS loads need 2-byte alignment)."""
+    raw = np.ascontiguousarray(X).view(np.uint8).ravel()
+    buf = cuda.zeros(raw.size + 1, dtype=cuda.uint8, device="cuda")
+    buf[1:].copy_(cuda.from_numpy(raw))
+    return buf, buf.data_ptr() + 1
+
+
+@pytest.mark.parametrize("tile", [None, "256x256", "192x192", "128x256", "256x128", "128x128", "64x64"])
+def test_exact_register_staged_path(mm, cuda, tile):
+    """A and B at odd byte addresses: the planner sends them to the register-staged kernels
+    (element-wise masked loads through VGPRs) on every tile; exact on integer inputs."""
+    import ctypes as C
+
+    M, N, K = 333, 517, 263
+    assert mm.gemm_plan(M, N, K, A=3)["direct_to_lds"] == 0
+    A, B, truth = _int_inputs(np.random.default_rng(263), M, N, K)
+    abuf, pa = _odd_copy(cuda, A)
+    bbuf, pb = _odd_copy(cuda, B)
+    Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    L = mm.lib()
+    st = C.c_void_p(cuda.cuda.current_stream().cuda_stream)
+    if tile is None:
+        e = L.mmm_gemm_f16f32(C.c_void_p(pa), C.c_void_p(pb), C.c_void_p(Cd.data_ptr()), M, N, K, K, N, N, st)
+    else:
+        wm, wn, wi, wj = mm.TILES[tile]
+        e = L.mmm_gemm_f16f32_tiled(C.c_void_p(pa), C.c_void_p(pb), C.c_void_p(Cd.data_ptr()), M, N, K, K, N, N,
+                                    wm, wn, wi, wj, None, 0, st)
+    assert e == 0
+    got = Cd.cpu().numpy()
+    del abuf, bbuf
+    assert np.array_equal(got, truth), f"{int((got != truth).sum())} mismatches"
 
 
 @pytest.mark.parametrize("tile", [None, "128x128"])
