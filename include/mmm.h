@@ -109,11 +109,13 @@ hipError_t mmm_gemm_workspace_f16f32(const mmm_half* A, const mmm_half* B, const
  * workgroup along M and N (the reference counts 16x16 WMMA tiles).  They select the block tile
  * only; each block tile's waves, MFMA shape and K step are the library's own:
  *   (4,4,2,2) 256x256 -- 8 waves (2 x 4) of 128x64, v_mfma_f32_16x16x32_f16, 64-deep K steps;
- *   (2,4,2,2) 128x256, (4,2,2,2) 256x128 -- 4 waves, v_mfma_f32_32x32x16_f16, 32-deep K steps;
- *   (2,2,2,2) 128x128 -- 4 waves, v_mfma_f32_32x32x16_f16, 64-deep K steps;
+ *   (2,4,2,2) 128x256, (4,2,2,2) 256x128 -- 8 waves (2 x 4, 4 x 2) of 64x64, v_mfma_f32_16x16x32_f16,
+ *             64-deep K steps;
+ *   (2,2,2,2) 128x128 -- 8 waves (2 x 4) of 64x32, v_mfma_f32_16x16x32_f16, 64-deep K steps;
  *   (1,1,2,2) 64x64 -- 4 waves, v_mfma_f32_16x16x32_f16, 64-deep K steps;
- *   (3,3,2,2) 192x192 -- 8 waves (2 x 4) of 96x48, v_mfma_f32_16x16x32_f16, 64-deep K steps
- *             (direct-to-LDS problems; others run the 128x128 register-staged kernel).
+ *   (3,3,2,2) 192x192 -- 8 waves (2 x 4) of 96x48, v_mfma_f32_16x16x32_f16, 64-deep K steps.
+ * Those are the direct-to-LDS kernels.  Problems with odd (1-byte-aligned) fp16 addresses run
+ * register-staged versions of 4 waves with v_mfma_f32_32x32x16_f16 (192x192: the 128x128 one).
  * Other parameter sets return hipErrorInvalidValue.  The workspace (NULL allowed) serves the
  * tile's K split as in mmm_gemm_f16f32_ws.
  */

@@ -142,14 +142,28 @@ constexpr double kPartialRoundBoost = MMM_PARTIAL_ROUND_BOOST;
 #ifndef MMM_T0_EFF
 #define MMM_T0_EFF 0.45
 #endif
+#ifndef MMM_T1_EFF
+#define MMM_T1_EFF 0.76
+#endif
+#ifndef MMM_T2_EFF
+#define MMM_T2_EFF 0.82
+#endif
 #ifndef MMM_T3_EFF
 #define MMM_T3_EFF 0.90
 #endif
+// The 128x128 tile in an unsplit launch of one round runs its 3-stage ring (DeepTile128), faster
+// per CU than the 2-stage multi-round version the 0.76 was measured on: priced at 0.80, which
+// picks it at 512 x 8192 x 8192 (867-919 TFLOP/s against 842-876 for a 4-way K split of 64
+// 256x256 tiles, the estimate that tied at 0.76).
+#ifndef MMM_T1_DEEP_EFF
+#define MMM_T1_DEEP_EFF 0.80
+#endif
 static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
-  static const double eff[kTileCount] = {1.0, 0.84, 0.80, 0.78, MMM_T0_EFF, MMM_T3_EFF};
+  static const double eff_of[kTileCount] = {1.0, MMM_T2_EFF, MMM_T2_EFF, MMM_T1_EFF, MMM_T0_EFF, MMM_T3_EFF};
   const int bm = tile_bm(tile), bn = tile_bn(tile);
   const TileSplit sp = gemm_nn_split(p, tile);
   const double tiles = (double)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
+  const double tile_eff = tile == kTile128x128 && sp.splits <= 1 && tiles <= 256.0 ? MMM_T1_DEEP_EFF : eff_of[tile];
   const double per_cu_flops = 4.8e12;  // sustained MFMA rate of one CU under load (256x256 at 8192^3)
   // A round with `active` of its 256 slots busy runs each CU faster: the chip is then below its
   // power cap and keeps a higher clock.  Fitted to the forced-tile times of the 23-shape sweep
@@ -157,7 +171,7 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
   // TFLOP/s on 144 256x256 tiles against 811 on the 128x256 tile the full-load rate preferred).
   auto round = [&](double k, double active) {
     const double boost = 1.0 + kPartialRoundBoost * (1.0 - std::min(active, 256.0) / 256.0);
-    return 2.0 * bm * bn * k / (per_cu_flops * eff[tile] * boost) + 3e-6;
+    return 2.0 * bm * bn * k / (per_cu_flops * tile_eff * boost) + 3e-6;
   };
   // A persistent grid overlaps each tile's epilogue with the next tile's first loads, so its
   // rounds after the first cost 1 us instead of 3 (fitted: it picks the persistent 192x192 grid
@@ -187,7 +201,7 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
 static int pick_tile(const GemmProblem& p) {
   int best = kTile256x256, s = 1;
   double best_cost = 1e300;
-  for (int tile : {kTile256x256, kTile128x256, kTile256x128, kTile128x128, kTile64x64, kTile192x192}) {
+  for (int tile : {kTile256x256, kTile256x128, kTile128x256, kTile128x128, kTile64x64, kTile192x192}) {
     if (tile == kTile192x192 && !gemm_nn_direct_to_lds(p, tile)) continue;  // direct-to-LDS only
     const double c = tile_cost(p, tile, &s);
     if (c < best_cost * 0.97) {

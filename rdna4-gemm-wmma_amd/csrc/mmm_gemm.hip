@@ -1547,23 +1547,20 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
 // 256x128 / 128x256 tiles: 4 waves; K step, ring depth and workgroups per CU
 // (measured at 8192^3: 32 x 3 stages with two workgroups per CU 1031-1064 TFLOP/s vs
 // 64 x 2 with one 868-908; two independent workgroups per CU desynchronise their barriers)
-#ifndef MMM_T2_BK
-#define MMM_T2_BK 32
-#endif
-#ifndef MMM_T2_STAGES
-#define MMM_T2_STAGES 3
-#endif
-#ifndef MMM_T2_OCC
-#define MMM_T2_OCC 2
-#endif
-// MFMA shape of the 128x128 tile: 32x32x16 (16x16x32 measured 2-7% slower at the 1024..3072
-// sizes this tile serves, faster only at 8192^3, where the 256x256 tile runs)
-#ifndef MMM_T1_MF
-#define MMM_T1_MF 32
-#endif
+// The 128-wide tiles run eight 16x16x32 waves (two per SIMD) like the 256x256 tile.  Measured on
+// MI355X against the four-wave 32x32x16 versions they replace (interleaved runs, same box):
+//   128x256 (2 x 4 waves of 64x64, 3 x 48 KB ring): 2048 x 4096 x 4096 858 -> 939 TFLOP/s,
+//     8192 x 1024 x 8192 1022 -> 1136, 1024 x 8192 x 8192 1030 -> 1145, 4096^3 1063 -> 1106,
+//     8192^3 1120 -> 1136, 3072^3 830 -> 827;
+//   256x128 (4 x 2 waves of 64x64, 3 x 48 KB ring): 2048 x 4096 x 4096 926 -> 1039,
+//     8192 x 1024 x 8192 1023 -> 1160, 4096^3 1008 -> 1109, 8192^3 1034 -> 1137;
+//   128x128 in multi-round grids (2 x 4 waves of 64x32, 2 x 32 KB ring, two workgroups per CU):
+//     4096^3 971 -> 1007, 6144^2 x 2048 918 -> 952, 8192^3 1032 -> 1048, 3072^3 738 -> 764.
+// With four waves a one-round launch holds one wave per SIMD, and nothing covers a wave's
+// barrier and LDS waits.
 template <int BM, int BN>
 struct DmaCfg {  // 128x128
-  using T = Tile<BM, BN, 2, 2, 64, 2, 2, MMM_T1_MF>;
+  using T = Tile<BM, BN, 2, 4, 64, 2, 2, 16>;
 };
 // 64x64: for grids too small to fill the chip with 128x128 tiles (1024^3 is 64 of those, 256
 // of these).  Four waves of 32x32 (2 x 2 16x16x32 fragments each) on a 3-stage ring (48 KB).
@@ -1581,10 +1578,11 @@ struct DmaCfg<64, 64> {
 // 192x192: 16 x 16 tiles fill one round exactly at 3072 x 3072, where 256x256 tiles leave 112
 // of the 256 CUs idle, and whole multiples of 256 tiles run as the persistent grid (6144^2 x
 // 2048: 1024 tiles, four rounds, 1006 -> 1047 TFLOP/s over one workgroup per tile, against 926
-// for 256x256 tiles' 2.25 rounds; 3072 x 6144 x 2048 996 -> 1030, against 888).  Eight waves of 96x48 (6 x 3 16x16x32 fragments), a 3-stage ring of
-// 48 KB stages; rows of 24 chunks use the per-slot B staging map.  Measured on MI355X
-// (interleaved runs, same box): 3072^3 763 -> 1007 TFLOP/s against the 256x256 tile, 3072^2 x
-// 8192 963 -> 1159, 4357 x 4095 x 4111 805 -> 885; 8192^3 1172 against 1380 (per-CU rate 0.85).
+// for 256x256 tiles' 2.25 rounds; 3072 x 6144 x 2048 996 -> 1030, against 888).  Eight waves of
+// 96x48 (6 x 3 16x16x32 fragments), a 3-stage ring of 48 KB stages; rows of 24 chunks use the
+// per-slot B staging map.  Measured on MI355X (interleaved runs, same box): 3072^3 763 -> 1007
+// TFLOP/s against the 256x256 tile, 3072^2 x 8192 963 -> 1159, 4357 x 4095 x 4111 805 -> 885;
+// 8192^3 1172 against 1380 (per-CU rate 0.85).
 template <>
 struct DmaCfg<192, 192> {
   using T = Tile<192, 192, 2, 4, 64, 3, 1, 16>;
@@ -1595,23 +1593,21 @@ struct DmaCfg<256, 256> {
 };
 template <>
 struct DmaCfg<256, 128> {
-  using T = Tile<256, 128, 2, 2, MMM_T2_BK, MMM_T2_STAGES, MMM_T2_OCC>;
+  using T = Tile<256, 128, 4, 2, 64, 3, 1, 16>;
 };
 template <>
 struct DmaCfg<128, 256> {
-  using T = Tile<128, 256, 2, 2, MMM_T2_BK, MMM_T2_STAGES, MMM_T2_OCC>;
+  using T = Tile<128, 256, 2, 4, 64, 3, 1, 16>;
 };
 template <int BM, int BN>
 using DmaTile = typename DmaCfg<BM, BN>::T;
 // The 128x128 tile in a launch of at most one round (one workgroup per CU): no second
-// workgroup on the CU covers the load latency, so the ring is one stage deeper.  Measured on
-// MI355X (interleaved runs, same box): 2048^3 567 -> 624 TFLOP/s, 2048^2 x 4096 720 -> 791,
-// 1024^2 x 8192 (K split) 508 -> 540; 4 stages no better than 3.  Grids of more rounds keep two
-// workgroups per CU on the 2-stage ring (3072^3 on 128x128: 809 against 686 for 3 stages).
-#ifndef MMM_T1_DEEP_STAGES
-#define MMM_T1_DEEP_STAGES 3
-#endif
-using DeepTile128 = Tile<128, 128, 2, 2, 64, MMM_T1_DEEP_STAGES, 1, MMM_T1_MF>;
+// workgroup on the CU covers the load latency, so the ring is one stage deeper (3 x 32 KB).
+// Measured on MI355X (interleaved runs, same box), first with four waves: 2048^3 567 -> 624
+// TFLOP/s, 2048^2 x 4096 720 -> 791, 1024^2 x 8192 (K split) 508 -> 540, 4 stages no better
+// than 3; then eight waves of 16x16x32 instead of four of 32x32x16: 2048^3 601 -> 645, 2048^2 x
+// 4096 760 -> 822, 1024^2 x 8192 538 -> 564, 512 x 8192 x 8192 783 -> 852.
+using DeepTile128 = Tile<128, 128, 2, 4, 64, 3, 1, 16>;
 // The folded direct-to-LDS kernel: the 256x256 tile's waves and ring.
 #ifndef MMM_FOLD_MF
 #define MMM_FOLD_MF 16
@@ -1658,7 +1654,7 @@ TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
   const int bm = tile_bm(tile_id), bn = tile_bn(tile_id);
   const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
   // workgroups one round holds: one per CU, times the tile's workgroups per CU when counted
-  const int occ = MMM_SPLIT_OCC ? (tile_id == kTile256x256 ? 1 : tile_id == kTile128x128 ? 2 : MMM_T2_OCC) : 1;
+  const int occ = MMM_SPLIT_OCC ? (tile_id == kTile128x128 ? 2 : 1) : 1;
   const int64_t slots = 256 * occ;
   const int64_t last = tiles - (tiles - 1) / slots * slots;  // tiles in the last round (1 .. slots)
   if (last * 2 >= slots) return {1, 0};
