@@ -414,8 +414,18 @@ SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 204
                 (6144, 6144, 2048)]
 
 
+# transformer-layer GEMMs (tokens x out-features x in-features): attention and MLP projections of
+# 4k-14k-wide layers at 128-16384 tokens (--sweep PATH --shapes llm)
+SWEEP_SHAPES_LLM = [(2048, 4096, 4096), (4096, 11008, 4096), (4096, 4096, 11008), (4096, 14336, 4096),
+                    (4096, 4096, 14336), (8192, 6144, 4096), (4096, 28672, 8192), (4096, 8192, 28672),
+                    (16384, 4096, 4096), (2048, 14336, 4096), (1024, 8192, 8192), (512, 8192, 8192),
+                    (256, 4096, 4096), (128, 14336, 4096), (8192, 8192, 4096), (8192, 1024, 8192)]
+
+
 def parse_shapes(text: str):
-    """"MxNxK,MxNxK,..." -> [(M, N, K), ...]"""
+    """"MxNxK,MxNxK,..." -> [(M, N, K), ...]; "llm" -> SWEEP_SHAPES_LLM"""
+    if text.strip().lower() == "llm":
+        return list(SWEEP_SHAPES_LLM)
     shapes = []
     for item in text.split(","):
         dims = tuple(int(x) for x in item.lower().split("x"))
@@ -447,10 +457,17 @@ def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool
         pick = plan["kernel"] if plan["kernel"] != "tile" else f"{plan['block_m']}x{plan['block_n']}"
         if plan["kernel"] == "tile+stream":
             pick = f"{plan['block_m']}x{plan['block_n']} + stream {plan['stream_rows']}"
-        # every launcher bound once (checks, marshalling and hipBLASLt's planning outside the timing);
-        # the pick is timed before and after the forced tiles and the two runs averaged, so the
-        # clock drift across a row does not favour either side
+        # every launcher bound once (checks, marshalling and hipBLASLt's planning outside the timing).
+        # The chip's power controller takes tens of milliseconds to settle after the load changes,
+        # so each shape first runs its pick for at least 100 ms untimed; the pick is then timed
+        # before and after the forced tiles and the two runs averaged, so the clock drift across a
+        # row does not favour either side.
         auto_launch = mmm.bind_gemm(A, B, Cm)
+        t_end = time.perf_counter() + 0.1
+        while time.perf_counter() < t_end:
+            for _ in range(10):
+                auto_launch()
+            torch.cuda.synchronize()
         auto = tf(auto_launch)
         per_tile = {t: tf(mmm.bind_gemm(A, B, Cm, tile=t)) for t in tiles}
         auto = 0.5 * (auto + tf(auto_launch))
@@ -487,7 +504,8 @@ def main() -> int:
     ap.add_argument("--report", metavar="PATH", help="measure every workload and write a JSON report to PATH")
     ap.add_argument("--sweep", metavar="PATH", help="time every tile against the library's pick over a shape "
                                                      "grid and write a markdown table to PATH")
-    ap.add_argument("--shapes", metavar="MxNxK,...", help="the problems --sweep runs (default: the built-in list)")
+    ap.add_argument("--shapes", metavar="MxNxK,...", help="the problems --sweep runs: a list, or `llm` for the "
+                                                          "transformer-layer set (default: the built-in list)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
