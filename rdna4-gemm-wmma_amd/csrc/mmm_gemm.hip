@@ -1544,9 +1544,6 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
 #ifndef MMM_DMA_MF
 #define MMM_DMA_MF 16
 #endif
-// 256x128 / 128x256 tiles: 4 waves; K step, ring depth and workgroups per CU
-// (measured at 8192^3: 32 x 3 stages with two workgroups per CU 1031-1064 TFLOP/s vs
-// 64 x 2 with one 868-908; two independent workgroups per CU desynchronise their barriers)
 // The 128-wide tiles run eight 16x16x32 waves (two per SIMD) like the 256x256 tile.  Measured on
 // MI355X against the four-wave 32x32x16 versions they replace (interleaved runs, same box):
 //   128x256 (2 x 4 waves of 64x64, 3 x 48 KB ring): 2048 x 4096 x 4096 858 -> 939 TFLOP/s,
