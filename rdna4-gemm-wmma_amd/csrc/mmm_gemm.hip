@@ -222,9 +222,13 @@ __device__ __forceinline__ void wait_tiles(int n) {
 
 __device__ __forceinline__ uint32_t lds_addr_of(const char LDS_AS* p) { return (uint32_t)(uintptr_t)p; }
 
+// A buffer descriptor's record count for `bytes` readable bytes: 0 if none, at most kOobOffset.
+// Compared in 32-bit halves, which stay scalar; a 64-bit compare against the constant is a
+// vector compare, and held the constant in two VGPRs for the whole kernel.
 __device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
-  if (bytes <= 0) return 0u;
-  return bytes > (int64_t)kOobOffset ? kOobOffset : (uint32_t)bytes;
+  const uint32_t hi = (uint32_t)((uint64_t)bytes >> 32), lo = (uint32_t)bytes;
+  if ((int32_t)hi < 0) return 0u;
+  return (hi != 0u || lo > kOobOffset) ? kOobOffset : lo;
 }
 
 // One pass over an LDS stage: KSTEPS K-steps of FM x FN MFMAs.  `after_first_reads` runs
@@ -331,6 +335,92 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
 }
 
 __device__ __forceinline__ void block_sync() { __syncthreads(); }
+
+// ---- C stores as whole 128-byte lines (16x16x32 tiles).  A 16x16 accumulator block gives lane
+// l row l % 16 and columns 4*(l/16) .. +3, so one float4 store of a block writes 16 rows x 64
+// bytes: half lines.  Blocks nb and nb+1 of a row of blocks cover 32 columns; lanes l and l ^ 8
+// (rows r and r + 8) trade their block-(nb+1) values (one DPP move per register), after which
+// one store writes rows 0-7 and the next rows 8-15, each row 32 columns: one 128-byte line.
+// Used with non-temporal and write-through stores (MMM_C_LINES 2; 1: every store policy, 0:
+// none).  Measured on MI355X (interleaved runs, same box, exact results), against half lines:
+// 8192^3 +0.6-0.9%, 12288^2 x 4096 +1.4%, 16384^2 x 4096 +1.0%, 8192 x 2048 x 2048 +1.4%,
+// 4096^3 +0.8%, 6144^3 +0.4%; with plain (L2-allocating) stores it lost up to 2% on short-K
+// persistent grids (8192^2 x 2048 -1.6%, 16384 x 8192 x 1024 -2.0%).
+#ifndef MMM_C_LINES
+#define MMM_C_LINES 2
+#endif
+enum CStore { kStorePlain = 0, kStoreNonTemporal = 1, kStoreWriteThrough = 2 };
+
+// System-scope write-through 16-byte store (sc0 sc1), as inline asm.  The compiler does not see
+// a store in inline asm, so it does not add the wait states a VALU write of the store's data
+// registers needs after a VMEM store of more than 8 bytes (2 on gfx950); the s_nop supplies them.
+// Without it the next VALU write could replace the data before the store read it (seen as
+// wrong C values when the epilogue reused the registers at once).
+#define WT_STORE_X4 "global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1"
+
+template <int POLICY>
+__device__ __forceinline__ void store_c4(float* dst, f32x4 v) {
+  if constexpr (POLICY == kStoreNonTemporal)
+    __builtin_nontemporal_store(v, (f32x4*)dst);
+  else if constexpr (POLICY == kStoreWriteThrough)
+    asm volatile(WT_STORE_X4 ::"v"(dst), "v"(v) : "memory");
+  else
+    *(f32x4*)dst = v;
+}
+
+// Lane l's result is lane (l ^ 8)'s x (DPP row_ror:8 within each 16-lane row).  Called
+// unconditionally: a cross-lane move inside one arm of a lane-dependent ?: runs with the other
+// lanes switched off and reads nothing from them.  Written per element: a loop over a vector's
+// elements here compiled to one DPP move reused for all four.
+__device__ __forceinline__ float from_lane_xor8(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+}
+__device__ __forceinline__ f32x4 from_lane_xor8(f32x4 v) {
+  return f32x4{from_lane_xor8(v.x), from_lane_xor8(v.y), from_lane_xor8(v.z), from_lane_xor8(v.w)};
+}
+
+// The lane index read afresh (v_mbcnt in asm, which the compiler cannot hoist out of a loop):
+// values derived from it are rebuilt where they are used instead of being kept live.
+__device__ __forceinline__ int lane_id_fresh() {
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  return lane;
+}
+
+template <class T>
+constexpr bool c_lines_ok() {
+  return MMM_C_LINES != 0 && T::MF == 16 && T::FN % 2 == 0;
+}
+template <class T, int POLICY>
+constexpr bool use_c_lines() {
+  return c_lines_ok<T>() && (MMM_C_LINES == 1 || POLICY != kStorePlain);
+}
+
+// The wave's whole TM x TN accumulator tile to C at `c` (the wave tile's first element; rows
+// ldc floats apart), every 32-column pair of blocks as 16 row lines.  The lane's row and column
+// offsets are built here from a fresh lane index: kept from before a persistent kernel's tile
+// loop they would stay live across its K loop, which runs at the register limit (they spilled).
+template <class T, int POLICY>
+__device__ __forceinline__ void store_wave_tile_lines(float* c, int64_t ldc, const AccT<T> (&acc)[T::FM][T::FN]) {
+  static_assert(c_lines_ok<T>(), "16x16 blocks in column pairs");
+  const int lane = lane_id_fresh();
+  const bool lo = (lane & 8) == 0;
+  float* r0 = c + (int64_t)(lane & 7) * ldc + 4 * (lane >> 4) + (lo ? 0 : 16);        // rows 0-7
+  float* r1 = c + (int64_t)((lane & 7) + 8) * ldc + 4 * (lane >> 4) + (lo ? 16 : 0);  // rows 8-15
+#pragma unroll
+  for (int mb = 0; mb < T::FM; ++mb) {
+#pragma unroll
+    for (int nb = 0; nb < T::FN; nb += 2) {
+      // rows 0-7: lanes 0-7 keep block nb, lanes 8-15 take block nb + 1 of lanes 0-7;
+      // rows 8-15: lanes 8-15 keep block nb, lanes 0-7 take block nb + 1 of lanes 8-15
+      const f32x4 traded = from_lane_xor8(acc[mb][nb + 1]);
+      const f32x4 rows_lo = lo ? acc[mb][nb] : traded, rows_hi = lo ? traded : acc[mb][nb];
+      store_c4<POLICY>(r0 + (int64_t)16 * mb * ldc + 16 * nb, rows_lo);
+      store_c4<POLICY>(r1 + (int64_t)16 * mb * ldc + 16 * nb, rows_hi);
+      __builtin_amdgcn_sched_barrier(0);  // one pair at a time: the traded values stay few
+    }
+  }
+}
 
 // Measurement: thread 0 of workgroup 0 writes the shader-clock counter (s_memtime) and the 100 MHz
 // real-time counter (s_memrealtime) to clk[at], clk[at + 1] when the caller asked for them.
@@ -623,7 +713,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       // K tail: a chunk at or past K gets kOobOffset added, which puts it beyond the
       // descriptor's range so it reads as zero (no select: keeps the loads branch-free).
       const uint32_t a_dead = (uint32_t)(K - 1 - (k0 + a_kc)) >> 31;
-      d.a_base = a_goff + a_dead * kOobOffset;
+      d.a_base = a_goff + ((0u - a_dead) & kOobOffset);
       return d;
     };
     auto dma_one = [&](const TileDma& d, int j) {
@@ -753,6 +843,11 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   };
   if (nsplit > 1) {  // K split: the whole tile (rows/columns past M/N included) to the partials
     float* part = p.partials + ((int64_t)j * nsplit + q) * (T::BM * T::BN);
+    if constexpr (use_c_lines<T, kStorePlain>()) {
+      store_wave_tile_lines<T, kStorePlain>(part + wm * T::TM * T::BN + wn * T::TN, T::BN, acc);
+      record_clock(p.clk, 2);
+      return;
+    }
 #pragma unroll
     for (int mb = 0; mb < T::FM; ++mb) {
       float* prow = part + (wm * T::TM + T::MF * mb + (lane % T::MF)) * T::BN + wn * T::TN;
@@ -769,6 +864,14 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   float* C = p.C;
   const int64_t ldc = p.ldc;
   const bool vec_ok = p.c_vec4;
+  constexpr int POLICY = WT ? kStoreWriteThrough : kStorePlain;
+  if constexpr (use_c_lines<T, POLICY>()) {
+    if (vec_ok && m0 + T::BM <= M && n0 + T::BN <= N) {  // interior tile (uniform)
+      store_wave_tile_lines<T, POLICY>(C + (int64_t)(m0 + wm * T::TM) * ldc + n0 + wn * T::TN, ldc, acc);
+      record_clock(p.clk, 2);
+      return;
+    }
+  }
 #pragma unroll
   for (int mb = 0; mb < T::FM; ++mb) {
     const int m = m0 + wm * T::TM + T::MF * mb + (lane % T::MF);
@@ -782,7 +885,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         f32x4 v = {acc[mb][nb][4 * q + 0], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2], acc[mb][nb][4 * q + 3]};
         if (vec_ok && n + 3 < N) {
           if constexpr (WT)
-            asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(crow + n), "v"(v) : "memory");
+            asm volatile(WT_STORE_X4 ::"v"(crow + n), "v"(v) : "memory");
           else
             *(f32x4*)(crow + n) = v;
         } else {
@@ -826,58 +929,64 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
   constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
   static_assert(RPA % T::SWZ_A_ROWS == 0 && (!T::B_UNIFORM || RPB % T::SWZ_B_ROWS == 0),
                 "round strides must preserve the swizzle");
-  const int a_row0 = w * (64 / T::CA) + lane / T::CA;
-  const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
-  const int b_row0 = T::B_UNIFORM ? w * (64 / T::CB) + lane / T::CB : 0;
-  const int b_nc = T::B_UNIFORM ? 8 * ((lane % T::CB) ^ T::swz_bk(b_row0)) : 0;
-  uint32_t a_off[4] = {0, 0, 0, 0};
+  // Fragment offsets (as gemm_nn_kernel), rebuilt at every tile from a freshly read lane index:
+  // kept from the kernel's start they would be live through the epilogue, whose line stores
+  // need the registers.
+  uint32_t a_off[4], b_off[4];
+  auto frag_offsets = [&]() {
+    const int ln = lane_id_fresh();
 #pragma unroll
-  for (int kk = 0; kk < T::KSTEPS; ++kk)
+    for (int q = 0; q < 4; ++q) a_off[q] = b_off[q] = 0;
 #pragma unroll
-    for (int ph = 0; ph < T::APAR; ++ph) {
-      const int m = wm * T::TM + ph * T::MF + (lane % T::MF);
-      const int chunk = (T::KK / 8) * kk + lane / T::MF;
-      a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
-    }
-  uint32_t b_off[4] = {0, 0, 0, 0};
-  {
-    const int k = 8 * (lane / T::MF) + ((lane >> 2) & 3);
+    for (int kk = 0; kk < T::KSTEPS; ++kk)
+#pragma unroll
+      for (int ph = 0; ph < T::APAR; ++ph) {
+        const int m = wm * T::TM + ph * T::MF + (ln % T::MF);
+        const int chunk = (T::KK / 8) * kk + ln / T::MF;
+        a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
+      }
+    const int k = 8 * (ln / T::MF) + ((ln >> 2) & 3);
 #pragma unroll
     for (int nb = 0; nb < T::FN; ++nb) {
-      const int n = T::MF == 32 ? wn * T::TN + 32 * nb + 16 * ((lane >> 4) & 1) + 4 * (lane & 3)
-                                : wn * T::TN + 16 * nb + 4 * (lane & 3);
+      const int n = T::MF == 32 ? wn * T::TN + 32 * nb + 16 * ((ln >> 4) & 1) + 4 * (ln & 3)
+                                : wn * T::TN + 16 * nb + 4 * (ln & 3);
       b_off[nb] = k * T::BN * 2 + (((n >> 3) ^ T::swz_bk(k)) * 16) + (n & 7) * 2;
     }
-  }
+  };
 
   const int KT = (K + T::BK - 1) / T::BK;
   char LDS_AS* lds_base = (char LDS_AS*)lds;
-  int a_kc_t = a_kc;  // a_kc for the K-tail test, made opaque per tile like the offset bases
-  uint32_t a_goff = (uint32_t)((a_row0 * lda + a_kc) * 2);
-  uint32_t b_goff = (uint32_t)((b_row0 * ldb + b_nc) * 2);
   const uint32_t a_rstep = (uint32_t)(RPA * lda * 2), b_rstep = (uint32_t)(RPB * ldb * 2);
-  uint32_t b_goffr[T::B_UNIFORM ? 1 : T::RB];  // per-slot B offsets (non-uniform map, as gemm_nn_kernel)
-  if constexpr (!T::B_UNIFORM) {
+  // Per-lane load offset bases (as gemm_nn_kernel; b_goffr: per-slot B offsets of a non-uniform
+  // map), rebuilt at every tile from a freshly read lane index, so that they are not live
+  // through a tile's last K step and epilogue, which run at the register limit.
+  int a_kc_t;  // a_kc, for the K-tail test
+  uint32_t a_goff, b_goff;
+  uint32_t b_goffr[T::B_UNIFORM ? 1 : T::RB];
+  auto dma_bases = [&]() {
+    const int ln = lane_id_fresh();
+    const int ar0 = w * (64 / T::CA) + ln / T::CA;
+    a_kc_t = 8 * ((ln % T::CA) ^ T::swz_a(ar0));
+    a_goff = (uint32_t)((ar0 * lda + a_kc_t) * 2);
+    if constexpr (T::B_UNIFORM) {
+      const int br0 = w * (64 / T::CB) + ln / T::CB;
+      b_goff = (uint32_t)((br0 * ldb + 8 * ((ln % T::CB) ^ T::swz_bk(br0))) * 2);
+    } else {
+      b_goff = 0;
 #pragma unroll
-    for (int r = 0; r < T::RB; ++r) {
-      const int sl = r * T::NT + w * 64 + lane;
-      b_goffr[r] = (uint32_t)(((sl / T::CB) * ldb + 8 * ((sl % T::CB) ^ T::swz_bk(sl / T::CB))) * 2);
+      for (int r = 0; r < T::RB; ++r) {
+        const int sl = r * T::NT + w * 64 + ln;
+        b_goffr[r] = (uint32_t)(((sl / T::CB) * ldb + 8 * ((sl % T::CB) ^ T::swz_bk(sl / T::CB))) * 2);
+      }
     }
-  }
+  };
   const int64_t b_step = (int64_t)T::BK * ldb * 2;
   // per-tile running load state (K tiles are prepared in order from 0)
   const char* a_ptr;
   const char* b_ptr;
   int64_t a_left, b_left;
   auto start_tile = [&](int tm0, int tn0) {
-    // The per-lane offset bases pass through an empty asm each tile, so the offsets of a tile's
-    // first loads are recomputed from them rather than kept live across the K loop (which
-    // runs at the register limit).
-    asm volatile("" : "+v"(a_goff), "+v"(b_goff), "+v"(a_kc_t));
-    if constexpr (!T::B_UNIFORM) {
-#pragma unroll
-      for (int r = 0; r < T::RB; ++r) asm volatile("" : "+v"(b_goffr[r]));
-    }
+    dma_bases();
     a_ptr = (const char*)(p.A + (int64_t)tm0 * lda);
     b_ptr = (const char*)(p.B + tn0);
     a_left = ((int64_t)(p.M - 1 - tm0) * lda + K) * 2;
@@ -897,7 +1006,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
     d.a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
     d.b_dst = d.a_dst + T::A_BYTES;
     const uint32_t a_dead = (uint32_t)(K - 1 - (k0 + a_kc_t)) >> 31;
-    d.a_base = a_goff + a_dead * kOobOffset;
+    d.a_base = a_goff + ((0u - a_dead) & kOobOffset);
     return d;
   };
   auto dma_one = [&](const TileDma& d, int j) {
@@ -927,6 +1036,9 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
     for (int i = 0; i < T::FM; ++i)
 #pragma unroll
       for (int jj = 0; jj < T::FN; ++jj) acc[i][jj] = AccT<T>{};
+    frag_offsets();
+    // again after the previous tile's line-store epilogue, which they need not live through
+    if constexpr (use_c_lines<T, NT ? kStoreNonTemporal : kStorePlain>()) dma_bases();
     cross_stage<T, false, NST>(lds_base, KT, false, a_off, b_off, acc, prep, dma_one, issue, pre);
     const int nb = b + (int)gridDim.x;
     int nm0 = 0, nn0 = 0;
@@ -940,6 +1052,10 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
       __builtin_amdgcn_sched_barrier(0);  // the loads go out before the stores below
     }
     // epilogue: interior tile, NST 16-byte stores per thread
+    if constexpr (use_c_lines<T, NT ? kStoreNonTemporal : kStorePlain>()) {
+      store_wave_tile_lines<T, NT ? kStoreNonTemporal : kStorePlain>(
+          p.C + (int64_t)(m0 + wm * T::TM) * p.ldc + n0 + wn * T::TN, p.ldc, acc);
+    } else
 #pragma unroll
     for (int mb = 0; mb < T::FM; ++mb) {
       float* crow = p.C + (int64_t)(m0 + wm * T::TM + T::MF * mb + (lane % T::MF)) * p.ldc + n0 + wn * T::TN;
@@ -1075,7 +1191,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_split_kernel
     d.a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
     d.b_dst = d.a_dst + T::A_BYTES;
     const uint32_t a_dead = (uint32_t)(K - 1 - (k0 + a_kc_t)) >> 31;
-    d.a_base = a_goff + a_dead * kOobOffset;
+    d.a_base = a_goff + ((0u - a_dead) & kOobOffset);
     return d;
   };
   auto dma_one = [&](const TileDma& d, int j) {
@@ -1119,6 +1235,10 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_split_kernel
     float* base = split_item ? p.partials + ((int64_t)cur.j * ksplit + cur.q) * (T::BM * T::BN)
                              : p.C + (int64_t)cur.m0 * p.ldc + cur.n0;
     const int64_t ld = split_item ? T::BN : p.ldc;
+    if constexpr (use_c_lines<T, NT ? kStoreNonTemporal : kStorePlain>()) {
+      store_wave_tile_lines<T, NT ? kStoreNonTemporal : kStorePlain>(base + (int64_t)wm * T::TM * ld + wn * T::TN, ld,
+                                                                      acc);
+    } else
 #pragma unroll
     for (int mb = 0; mb < T::FM; ++mb) {
       float* crow = base + (int64_t)(wm * T::TM + T::MF * mb + (lane % T::MF)) * ld + wn * T::TN;
