@@ -405,6 +405,8 @@ def steady_state(name, torch, mmm, seconds: float):
 
 
 # shapes of the tile sweep (--sweep): squares, the configs, and tall / wide / deep / shallow cases
+# rounds of the sweep: every column is timed once per round, in a rotated order
+SWEEP_ROUNDS = 3
 SWEEP_SHAPES = [(256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (4096, 4096, 4096),
                 (6144, 6144, 6144), (8192, 8192, 8192), (8192, 2048, 2048), (2048, 8192, 2048), (4097, 4095, 4111),
                 (16384, 1024, 4096), (1024, 16384, 4096), (8192, 8192, 1024), (1024, 1024, 8192), (3000, 5000, 1000),
@@ -457,32 +459,38 @@ def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool
         pick = plan["kernel"] if plan["kernel"] != "tile" else f"{plan['block_m']}x{plan['block_n']}"
         if plan["kernel"] == "tile+stream":
             pick = f"{plan['block_m']}x{plan['block_n']} + stream {plan['stream_rows']}"
-        # every launcher bound once (checks, marshalling and hipBLASLt's planning outside the timing).
+        # every launcher bound once (checks, marshalling and hipBLASLt's planning outside the timing)
+        launchers = {"pick": mmm.bind_gemm(A, B, Cm)}
+        launchers.update({t: mmm.bind_gemm(A, B, Cm, tile=t) for t in tiles})
+        if with_witness:
+            try:
+                launchers["hipblaslt"] = mmm.bind_witness_hipblaslt(A, B, Cm)
+            except Exception as e:  # witness library absent or hipBLASLt refused the shape
+                _log(f"[sweep] hipBLASLt unavailable for {M}x{N}x{K}: {e}")
         # The chip's power controller takes tens of milliseconds to settle after the load changes,
-        # so each shape first runs its pick for at least 100 ms untimed; the pick is then timed
-        # before and after the forced tiles and the two runs averaged, so the clock drift across a
-        # row does not favour either side.
-        auto_launch = mmm.bind_gemm(A, B, Cm)
+        # so each shape first runs its pick for at least 100 ms untimed.  Then SWEEP_ROUNDS rounds
+        # time every column once, each round in a rotated order, and a column's figure is its
+        # median over the rounds: no column always runs right after the warm-up or a slow neighbour.
         t_end = time.perf_counter() + 0.1
         while time.perf_counter() < t_end:
             for _ in range(10):
-                auto_launch()
+                launchers["pick"]()
             torch.cuda.synchronize()
-        auto = tf(auto_launch)
-        per_tile = {t: tf(mmm.bind_gemm(A, B, Cm, tile=t)) for t in tiles}
-        auto = 0.5 * (auto + tf(auto_launch))
+        names = list(launchers)
+        got = {n: [] for n in names}
+        for r in range(SWEEP_ROUNDS):
+            for n in names[r % len(names):] + names[:r % len(names)]:
+                got[n].append(tf(launchers[n]))
+        med = {n: statistics.median(v) for n, v in got.items()}
+        auto = med["pick"]
+        per_tile = {t: med[t] for t in tiles}
         best = max(per_tile, key=per_tile.get)
-        wit = float("nan")
-        if with_witness:
-            try:
-                wit = tf(mmm.bind_witness_hipblaslt(A, B, Cm))
-            except Exception as e:  # witness library absent or hipBLASLt refused the shape
-                _log(f"[sweep] hipBLASLt unavailable for {M}x{N}x{K}: {e}")
+        wit = med.get("hipblaslt", float("nan"))
         row = (f"| {M} x {N} x {K} | {pick} | {auto:.1f} | " + " | ".join(f"{per_tile[t]:.1f}" for t in tiles) +
                f" | {best} | {auto / per_tile[best]:.2f} | {wit:.1f} |")
         lines.append(row)
         _log("[sweep] " + row)
-        del A, B, Cm
+        del A, B, Cm, launchers
         torch.cuda.empty_cache()
     with open(path, "w") as f:
         f.write("\n".join(lines) + "\n")

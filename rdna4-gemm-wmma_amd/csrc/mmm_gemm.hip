@@ -1600,7 +1600,8 @@ __global__ __launch_bounds__(256) void reduce_tiles_kernel(GemmProblem p, int ti
   }
 }
 
-// Shortest K for which the multi-round kernels store C non-temporally (see their launches).
+// Shortest K for which the multi-round kernels store C non-temporally in half lines (see their
+// launches).
 constexpr int kNtMinK = 4096;
 
 template <class T, bool GENERIC>
@@ -1853,12 +1854,15 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
         using TP = DmaTile<256, 256>;
         // Non-temporal C stores: the persistent grid stores a tile's C while its next tile's
         // operand loads run, and L2-allocating stores would evict the operand panels other
-        // workgroups of the XCD are about to read.  That wins when each tile's K loop is long;
-        // with short K the slower-draining non-temporal stores weigh more (measured on MI355X:
-        // 12288^2 x 4096 +6.7%, 8192^3 +1.6-2.8%, 6144^3 -0.6%, 8192^2 x 2048 -7.1%,
-        // 16384 x 8192 x 1024 -9.3%).  16-byte-aligned C rows only.
+        // workgroups of the XCD are about to read.  As half-line stores that won only when each
+        // tile's K loop is long (measured on MI355X: 12288^2 x 4096 +6.7%, 8192^3 +1.6-2.8%,
+        // 8192^2 x 2048 -7.1%, 16384 x 8192 x 1024 -9.3%); as whole lines (store_wave_tile_lines)
+        // they win at every K (against L2-allocating half lines: 8192^2 x 2048 +8%, 12288^2 x
+        // 2048 +5.2%, 8192^2 x 1024 +4.2-4.8%, 16384 x 8192 x 1024 +4.2%).  16-byte-aligned C
+        // rows only.
         const int tiles_m = p.M / TP::BM, tiles_n = p.N / TP::BN;
-        const bool nt = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 && p.K >= kNtMinK;
+        const bool nt = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 &&
+                        (use_c_lines<TP, kStoreNonTemporal>() || p.K >= kNtMinK);
         if (p.k_splits <= 1) {
           if (nt)
             hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
@@ -1901,7 +1905,8 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
       if (MMM_PERSIST && MMM_PERSIST_192 && p.k_splits <= 1 && persistent_ok<DmaTile<192, 192>>(p)) {
         using TP = DmaTile<192, 192>;
         const int tiles_m = p.M / TP::BM, tiles_n = p.N / TP::BN;
-        const bool nt = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 && p.K >= kNtMinK;
+        const bool nt = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 &&
+                        (use_c_lines<TP, kStoreNonTemporal>() || p.K >= kNtMinK);
         if (nt)
           hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
                              tiles_n);
