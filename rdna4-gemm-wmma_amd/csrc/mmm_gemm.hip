@@ -1614,15 +1614,17 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
   if (split_tiles < 0 || split_tiles > tiles) return hipErrorInvalidValue;
   const int64_t blocks = tiles - split_tiles + split_tiles * splits;
   if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-  // A one-round grid writes all of C after its last K step, with nothing left to overlap.  When
-  // C is larger than the eight XCDs' L2 (32 MB), write-back stores end in dirty-line evictions
-  // anyway, and system-scope write-through stores drain the burst faster (measured on MI355X,
-  // 256x256 tile, no K split: 8192 x 2048 x 2048 +3.1%, 4096^3 +1.3%).  Not where C fits the L2
-  // (2048^3 -4.7%, 1024^3 -7.5%), with a K split (3072^3 on 128x256 -8.8%) or for rows of an
-  // odd ldc (-9%).
-  const bool wt = splits == 1 && blocks <= 256 * T::OCC && (double)p.M * p.N * 4.0 > 32.0 * (1 << 20) &&
-                  ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0;
-  if constexpr (!GENERIC && T::BM == 256 && T::BN == 256) {
+  // A one-round grid writes all of C after its last K step, with nothing left to overlap, and
+  // system-scope write-through stores (sc0 sc1) drain that burst faster.  As half lines they won
+  // only where C outgrew the eight XCDs' L2 (32 MB; 256x256 tile: 8192 x 2048 x 2048 +3.1%,
+  // 4096^3 +1.3%, but 2048^3 -4.7%, 1024^3 -7.5%); as whole lines (store_wave_tile_lines) they win
+  // at every size measured on MI355X, against L2-allocating half lines: 2048^2 x 1024 +11%,
+  // 2048^3 +6.7%, 1536^3 +5%, 2048^2 x 4096 +4.4%, 8192 x 1024 x 8192 +2.8%, 1024 x 8192 x 8192
+  // +2.1%, 1024^3 +1.5-2.3%, 512^3 +-0.  Not with a K split (as
+  // half lines: 3072^3 on 128x256 -8.8%) or for rows of an odd ldc (-9%).
+  const bool wt = splits == 1 && blocks <= 256 * T::OCC && ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 &&
+                  (c_lines_ok<T>() || (double)p.M * p.N * 4.0 > 32.0 * (1 << 20));
+  if constexpr (!GENERIC && (c_lines_ok<T>() || (T::BM == 256 && T::BN == 256))) {
     if (wt)
       hipLaunchKernelGGL((gemm_nn_kernel<T, false, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
                          tiles_n);
