@@ -577,9 +577,9 @@ struct NoHook {
 //                  by unaligned buffer loads; the last K tile of an unaligned problem is gathered
 //                  through VGPRs (tail_regs).
 // GENERIC = true : element-wise masked loads through VGPRs; any shape and alignment.
-// WT = true: C rows (16-byte aligned) are written with system-scope write-through stores
-//            (sc0 sc1), for one-round grids (see launch_nn).
-template <class T, bool GENERIC, bool WT = false>
+// CPOL: how C's 16-byte pieces are stored (CStore): plain, non-temporal or system-scope
+//       write-through (sc0 sc1); the last two for 16-byte-aligned C rows only (see launch_nn).
+template <class T, bool GENERIC, int CPOL = kStorePlain>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
   record_clock(p.clk, 0);
@@ -864,10 +864,9 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   float* C = p.C;
   const int64_t ldc = p.ldc;
   const bool vec_ok = p.c_vec4;
-  constexpr int POLICY = WT ? kStoreWriteThrough : kStorePlain;
-  if constexpr (use_c_lines<T, POLICY>()) {
+  if constexpr (use_c_lines<T, CPOL>()) {
     if (vec_ok && m0 + T::BM <= M && n0 + T::BN <= N) {  // interior tile (uniform)
-      store_wave_tile_lines<T, POLICY>(C + (int64_t)(m0 + wm * T::TM) * ldc + n0 + wn * T::TN, ldc, acc);
+      store_wave_tile_lines<T, CPOL>(C + (int64_t)(m0 + wm * T::TM) * ldc + n0 + wn * T::TN, ldc, acc);
       record_clock(p.clk, 2);
       return;
     }
@@ -884,10 +883,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         const int n = n0 + wn * T::TN + col_of(nb, q);
         f32x4 v = {acc[mb][nb][4 * q + 0], acc[mb][nb][4 * q + 1], acc[mb][nb][4 * q + 2], acc[mb][nb][4 * q + 3]};
         if (vec_ok && n + 3 < N) {
-          if constexpr (WT)
-            asm volatile(WT_STORE_X4 ::"v"(crow + n), "v"(v) : "memory");
-          else
-            *(f32x4*)(crow + n) = v;
+          store_c4<CPOL>(crow + n, v);
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
@@ -1622,12 +1618,15 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
   // 2048^3 +6.7%, 1536^3 +5%, 2048^2 x 4096 +4.4%, 8192 x 1024 x 8192 +2.8%, 1024 x 8192 x 8192
   // +2.1%, 1024^3 +1.5-2.3%, 512^3 +-0.  Not with a K split (as
   // half lines: 3072^3 on 128x256 -8.8%) or for rows of an odd ldc (-9%).
-  const bool wt = splits == 1 && blocks <= 256 * T::OCC && ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 &&
+  const bool c16 = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0;
+  const bool wt = splits == 1 && blocks <= 256 * T::OCC && c16 &&
                   (c_lines_ok<T>() || (double)p.M * p.N * 4.0 > 32.0 * (1 << 20));
+  // (Multi-round grids keep plain stores: non-temporal whole lines there measured -4.6% at
+  // 5000^3, -1% at 4096^3 on 256x128, +7% at 8192^2 x 2048 on 256x128, +-0 elsewhere.)
   if constexpr (!GENERIC && (c_lines_ok<T>() || (T::BM == 256 && T::BN == 256))) {
     if (wt)
-      hipLaunchKernelGGL((gemm_nn_kernel<T, false, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
-                         tiles_n);
+      hipLaunchKernelGGL((gemm_nn_kernel<T, false, kStoreWriteThrough>), dim3((unsigned)blocks), dim3(T::NT), 0, stream,
+                         p, tiles_m, tiles_n);
     else
       hipLaunchKernelGGL((gemm_nn_kernel<T, false>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
                          tiles_n);
