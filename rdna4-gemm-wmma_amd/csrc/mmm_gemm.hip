@@ -843,8 +843,12 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   };
   if (nsplit > 1) {  // K split: the whole tile (rows/columns past M/N included) to the partials
     float* part = p.partials + ((int64_t)j * nsplit + q) * (T::BM * T::BN);
-    if constexpr (use_c_lines<T, kStorePlain>()) {
-      store_wave_tile_lines<T, kStorePlain>(part + wm * T::TM * T::BN + wn * T::TN, T::BN, acc);
+    // Whole lines, written through (sc0 sc1): reduce_tiles_kernel, next on the stream, reads
+    // them on other XCDs.  Measured on MI355X (interleaved, against L2-allocating half lines):
+    // 256 x 4096 x 4096 +9.2%, 1024^2 x 8192 +5.9%, 1024 x 2048 x 4096 +4.7%, 128 x 14336 x 4096
+    // +3.3%, 1536^2 x 12288 +2.6%, 2304^2 x 8192 +1.9%; non-temporal lines -4% to +6%.
+    if constexpr (c_lines_ok<T>()) {
+      store_wave_tile_lines<T, kStoreWriteThrough>(part + wm * T::TM * T::BN + wn * T::TN, T::BN, acc);
       record_clock(p.clk, 2);
       return;
     }
