@@ -336,7 +336,8 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
 
 __device__ __forceinline__ void block_sync() { __syncthreads(); }
 
-// ---- C stores as whole 128-byte lines (16x16x32 tiles).  A 16x16 accumulator block gives lane
+// ---- C stores as whole 128-byte lines (16x16x32 tiles; the 192x192 tile's third block of a row
+// as half lines).  A 16x16 accumulator block gives lane
 // l row l % 16 and columns 4*(l/16) .. +3, so one float4 store of a block writes 16 rows x 64
 // bytes: half lines.  Blocks nb and nb+1 of a row of blocks cover 32 columns; lanes l and l ^ 8
 // (rows r and r + 8) trade their block-(nb+1) values (one DPP move per register), after which
@@ -389,7 +390,12 @@ __device__ __forceinline__ int lane_id_fresh() {
 
 template <class T>
 constexpr bool c_lines_ok() {
-  return MMM_C_LINES != 0 && T::MF == 16 && T::FN % 2 == 0;
+  return MMM_C_LINES != 0 && T::MF == 16 && T::FN >= 2;
+}
+// every store of the tile a whole line (an even number of blocks per row)
+template <class T>
+constexpr bool c_lines_all() {
+  return c_lines_ok<T>() && T::FN % 2 == 0;
 }
 template <class T, int POLICY>
 constexpr bool use_c_lines() {
@@ -397,12 +403,13 @@ constexpr bool use_c_lines() {
 }
 
 // The wave's whole TM x TN accumulator tile to C at `c` (the wave tile's first element; rows
-// ldc floats apart), every 32-column pair of blocks as 16 row lines.  The lane's row and column
+// ldc floats apart), every 32-column pair of blocks as 16 row lines (an odd last block as half
+// lines).  The lane's row and column
 // offsets are built here from a fresh lane index: kept from before a persistent kernel's tile
 // loop they would stay live across its K loop, which runs at the register limit (they spilled).
 template <class T, int POLICY>
 __device__ __forceinline__ void store_wave_tile_lines(float* c, int64_t ldc, const AccT<T> (&acc)[T::FM][T::FN]) {
-  static_assert(c_lines_ok<T>(), "16x16 blocks in column pairs");
+  static_assert(c_lines_ok<T>(), "16x16 blocks, at least two per row");
   const int lane = lane_id_fresh();
   const bool lo = (lane & 8) == 0;
   float* r0 = c + (int64_t)(lane & 7) * ldc + 4 * (lane >> 4) + (lo ? 0 : 16);        // rows 0-7
@@ -410,7 +417,7 @@ __device__ __forceinline__ void store_wave_tile_lines(float* c, int64_t ldc, con
 #pragma unroll
   for (int mb = 0; mb < T::FM; ++mb) {
 #pragma unroll
-    for (int nb = 0; nb < T::FN; nb += 2) {
+    for (int nb = 0; nb + 1 < T::FN; nb += 2) {
       // rows 0-7: lanes 0-7 keep block nb, lanes 8-15 take block nb + 1 of lanes 0-7;
       // rows 8-15: lanes 8-15 keep block nb, lanes 0-7 take block nb + 1 of lanes 8-15
       const f32x4 traded = from_lane_xor8(acc[mb][nb + 1]);
@@ -419,6 +426,9 @@ __device__ __forceinline__ void store_wave_tile_lines(float* c, int64_t ldc, con
       store_c4<POLICY>(r1 + (int64_t)16 * mb * ldc + 16 * nb, rows_hi);
       __builtin_amdgcn_sched_barrier(0);  // one pair at a time: the traded values stay few
     }
+    if constexpr (T::FN % 2 != 0)  // the odd last block: lane l's row l % 16, 16 rows x 64 bytes
+      store_c4<POLICY>(c + (int64_t)(16 * mb + (lane & 15)) * ldc + 16 * (T::FN - 1) + 4 * (lane >> 4),
+                       acc[mb][T::FN - 1]);
   }
 }
 
@@ -1867,7 +1877,7 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
         // rows only.
         const int tiles_m = p.M / TP::BM, tiles_n = p.N / TP::BN;
         const bool nt = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 &&
-                        (use_c_lines<TP, kStoreNonTemporal>() || p.K >= kNtMinK);
+                        (c_lines_all<TP>() || p.K >= kNtMinK);
         if (p.k_splits <= 1) {
           if (nt)
             hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
@@ -1910,8 +1920,11 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
       if (MMM_PERSIST && MMM_PERSIST_192 && p.k_splits <= 1 && persistent_ok<DmaTile<192, 192>>(p)) {
         using TP = DmaTile<192, 192>;
         const int tiles_m = p.M / TP::BM, tiles_n = p.N / TP::BN;
+        // non-temporal C as for the 256x256 tile; this tile's third block of a row is stored as
+        // half lines, and at short K its non-temporal stores lose (6144^2 x 2048 -2.9%,
+        // 3072 x 6144 x 2048 -3.7% with them at every K; long K: 6144^3 +1.2%)
         const bool nt = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0 &&
-                        (use_c_lines<TP, kStoreNonTemporal>() || p.K >= kNtMinK);
+                        (c_lines_all<TP>() || p.K >= kNtMinK);
         if (nt)
           hipLaunchKernelGGL((gemm_nn_persistent_kernel<TP, true>), dim3(256), dim3(TP::NT), 0, stream, p, tiles_m,
                              tiles_n);
