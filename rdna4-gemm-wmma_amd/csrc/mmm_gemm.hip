@@ -878,7 +878,9 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   float* C = p.C;
   const int64_t ldc = p.ldc;
   const bool vec_ok = p.c_vec4;
-  if constexpr (use_c_lines<T, CPOL>()) {
+  // Interior tiles store whole lines with every store policy here (plain ones too: the ragged
+  // configuration +0.7-1%, other plain grids +-0.5%).
+  if constexpr (c_lines_ok<T>()) {
     if (vec_ok && m0 + T::BM <= M && n0 + T::BN <= N) {  // interior tile (uniform)
       store_wave_tile_lines<T, CPOL>(C + (int64_t)(m0 + wm * T::TM) * ldc + n0 + wn * T::TN, ldc, acc);
       record_clock(p.clk, 2);
