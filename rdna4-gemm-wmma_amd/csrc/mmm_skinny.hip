@@ -539,8 +539,8 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     const float sum = ((part[(0 * ROWS + row) * PS + col] + part[(1 * ROWS + row) * PS + col]) +
                        part[(2 * ROWS + row) * PS + col]) +
                       part[(3 * ROWS + row) * PS + col];
-    if (mine)
-      mine[idx] = sum;
+    if (mine)  // written through (sc0 sc1): the reduction reads them on other XCDs (+0.2-1.4% per call)
+      asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(mine + idx), "v"(sum) : "memory");
     else if (row < M && n0 + col < N)
       p.C[(int64_t)row * p.ldc + n0 + col] = sum;
   }
