@@ -288,3 +288,57 @@ def test_gemm_plan(mm):
         mm.gemm_plan(64, 64, 64, lda=32)
     with pytest.raises(mm.MMMError):
         mm.gemm_plan(-1, 64, 64)
+
+
+@pytest.mark.parametrize("fm,fn", [(8, 4), (4, 4), (2, 2), (6, 3)])
+def test_line_store_lane_map(fm, fn):
+    """The whole-line C epilogue (store_wave_tile_lines in mmm_gemm.hip), restated lane by lane:
+    a 16x16x32 accumulator block gives lane l row l % 16 and columns 4*(l//16) .. +3; lanes l and
+    l ^ 8 trade their block-(nb+1) values, lanes with (l & 8) == 0 store rows 0-7 of the pair
+    from block nb and rows 8-15 from the traded values, the others the reverse.  Every element of
+    the wave tile is written exactly once with its own value, and each paired store instruction
+    covers 8 rows x 32 consecutive floats (whole 128-byte lines); an odd last block (fn = 3, the
+    192x192 tile) is stored as before, 16 rows x 16 floats."""
+    ldc = 1000  # any row pitch
+    lanes = np.arange(64)
+    # acc[mb][nb][e] of lane l holds the value C[16 mb + l % 16][16 nb + 4 (l // 16) + e]
+    def value(r, c):
+        return r * 100000 + c
+    acc = np.zeros((fm, fn, 64, 4), dtype=np.int64)
+    for mb in range(fm):
+        for nb in range(fn):
+            for e in range(4):
+                acc[mb, nb, :, e] = value(16 * mb + lanes % 16, 16 * nb + 4 * (lanes // 16) + e)
+    written = {}
+    lo = (lanes & 8) == 0
+    r0 = (lanes & 7) * ldc + 4 * (lanes >> 4) + np.where(lo, 0, 16)
+    r1 = ((lanes & 7) + 8) * ldc + 4 * (lanes >> 4) + np.where(lo, 16, 0)
+    for mb in range(fm):
+        for nb in range(0, fn - 1, 2):
+            traded = acc[mb, nb + 1][lanes ^ 8]
+            rows_lo = np.where(lo[:, None], acc[mb, nb], traded)
+            rows_hi = np.where(lo[:, None], traded, acc[mb, nb])
+            for base, data in ((r0, rows_lo), (r1, rows_hi)):
+                addr = base + 16 * mb * ldc + 16 * nb
+                cols = set()
+                for l in range(64):
+                    for e in range(4):
+                        a = int(addr[l]) + e
+                        assert a not in written
+                        written[a] = int(data[l, e])
+                        cols.add(a)
+                rows = {a // ldc for a in cols}
+                assert len(rows) == 8  # 8 rows ...
+                for rr in rows:  # ... of 32 consecutive floats each
+                    rc = sorted(a % ldc for a in cols if a // ldc == rr)
+                    assert rc == list(range(rc[0], rc[0] + 32))
+        if fn % 2:
+            nb = fn - 1
+            for l in range(64):
+                for e in range(4):
+                    a = (16 * mb + l % 16) * ldc + 16 * nb + 4 * (l // 16) + e
+                    assert a not in written
+                    written[a] = int(acc[mb, nb, l, e])
+    assert len(written) == fm * 16 * fn * 16
+    for a, v in written.items():
+        assert v == value(a // ldc, a % ldc)
