@@ -336,17 +336,18 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const cha
 
 __device__ __forceinline__ void block_sync() { __syncthreads(); }
 
-// ---- C stores as whole 128-byte lines (16x16x32 tiles; the 192x192 tile's third block of a row
-// as half lines).  A 16x16 accumulator block gives lane
-// l row l % 16 and columns 4*(l/16) .. +3, so one float4 store of a block writes 16 rows x 64
+// ---- C stores as whole 128-byte lines (16x16x32 tiles).  A 16x16 accumulator block gives lane l
+// row l % 16 and columns 4*(l/16) .. +3, so one float4 store of a block writes 16 rows x 64
 // bytes: half lines.  Blocks nb and nb+1 of a row of blocks cover 32 columns; lanes l and l ^ 8
 // (rows r and r + 8) trade their block-(nb+1) values (one DPP move per register), after which
-// one store writes rows 0-7 and the next rows 8-15, each row 32 columns: one 128-byte line.
-// Used with non-temporal and write-through stores (MMM_C_LINES 2; 1: every store policy, 0:
-// none).  Measured on MI355X (interleaved runs, same box, exact results), against half lines:
-// 8192^3 +0.6-0.9%, 12288^2 x 4096 +1.4%, 16384^2 x 4096 +1.0%, 8192 x 2048 x 2048 +1.4%,
-// 4096^3 +0.8%, 6144^3 +0.4%; with plain (L2-allocating) stores it lost up to 2% on short-K
-// persistent grids (8192^2 x 2048 -1.6%, 16384 x 8192 x 1024 -2.0%).
+// one store writes rows 0-7 and the next rows 8-15, each row 32 columns: one 128-byte line (the
+// 192x192 tile's odd third block of a row stays half lines).  gemm_nn_kernel stores its interior
+// tiles this way with every store policy; the persistent kernels with non-temporal stores only
+// (MMM_C_LINES 2; 1: with plain stores too, 0: nowhere).  Measured on MI355X (interleaved runs,
+// same box, exact results), against half lines: 8192^3 +0.6-0.9%, 12288^2 x 4096 +1.4%,
+// 16384^2 x 4096 +1.0%, 8192 x 2048 x 2048 +1.4%, 4096^3 +0.8%, 6144^3 +0.4%; with plain
+// (L2-allocating) stores the persistent grids lost up to 2% at short K (8192^2 x 2048 -1.6%,
+// 16384 x 8192 x 1024 -2.0%).
 #ifndef MMM_C_LINES
 #define MMM_C_LINES 2
 #endif
@@ -404,9 +405,9 @@ constexpr bool use_c_lines() {
 
 // The wave's whole TM x TN accumulator tile to C at `c` (the wave tile's first element; rows
 // ldc floats apart), every 32-column pair of blocks as 16 row lines (an odd last block as half
-// lines).  The lane's row and column
-// offsets are built here from a fresh lane index: kept from before a persistent kernel's tile
-// loop they would stay live across its K loop, which runs at the register limit (they spilled).
+// lines).  The lane's row and column offsets are built here from a fresh lane index: kept from
+// before a persistent kernel's tile loop they would stay live across its K loop, which runs at
+// the register limit (they spilled).
 template <class T, int POLICY>
 __device__ __forceinline__ void store_wave_tile_lines(float* c, int64_t ldc, const AccT<T> (&acc)[T::FM][T::FN]) {
   static_assert(c_lines_ok<T>(), "16x16 blocks, at least two per row");
@@ -1632,8 +1633,8 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
   // 4096^3 +1.3%, but 2048^3 -4.7%, 1024^3 -7.5%); as whole lines (store_wave_tile_lines) they win
   // at every size measured on MI355X, against L2-allocating half lines: 2048^2 x 1024 +11%,
   // 2048^3 +6.7%, 1536^3 +5%, 2048^2 x 4096 +4.4%, 8192 x 1024 x 8192 +2.8%, 1024 x 8192 x 8192
-  // +2.1%, 1024^3 +1.5-2.3%, 512^3 +-0.  Not with a K split (as
-  // half lines: 3072^3 on 128x256 -8.8%) or for rows of an odd ldc (-9%).
+  // +2.1%, 1024^3 +1.5-2.3%, 512^3 +-0.  Not with a K split (as half lines: 3072^3 on 128x256
+  // -8.8%) or for rows of an odd ldc (-9%).
   const bool c16 = ((uintptr_t)p.C & 15) == 0 && p.ldc % 4 == 0;
   const bool wt = splits == 1 && blocks <= 256 * T::OCC && c16 &&
                   (c_lines_ok<T>() || (double)p.M * p.N * 4.0 > 32.0 * (1 << 20));
