@@ -132,11 +132,13 @@ constexpr double kPartialRoundBoost = MMM_PARTIAL_ROUND_BOOST;
 
 // Estimated time of a tile launch, in seconds: rounds of 256 concurrent workgroups (one per
 // CU) times the MFMA time of one tile's K range at the tile's relative efficiency (measured
-// at 8192^3, each tile forced: 256x256 1.0, 128x256 0.84, 256x128 0.80, 128x128 0.78; 192x192
-// 0.85 and 64x64 0.40 there, priced at 0.90 and 0.45, which pick the faster tile on the shapes
-// measured for them: 192x192 on 3072^3, 3072^2 x 8192 and 4357 x 4095 x 4111, 256x256 on
-// 2304^2 x 8192, 4608^2 x 8192, 6144^3, 6144^2 x 2048 and 3000 x 5000 x 1000; 64x64 on 256^3
-// to 1024^2 x 2048, 128x128 from 1536^3) plus a fixed per-round cost (prologue, epilogue).
+// at 8192^3, each tile forced: 256x256 1.0, 128x256 0.82, 256x128 0.84, 128x128 0.75; 192x192
+// 0.82 and 64x64 0.38 there, priced at 0.91 and 0.45, which pick the faster tile on the shapes
+// measured for them: 192x192 on 3072^3, 3072^2 x 8192, 4357 x 4095 x 4111 and the 4-way K split
+// of 1536^2 x 12288 (937 TFLOP/s against 864 for a 7-way split of 256x256 tiles; at 0.90 the
+// estimates were 2.6% apart and the larger tile kept it), 256x256 on 2304^2 x 8192, 4608^2 x
+// 8192, 6144^3, 6144^2 x 2048 and 3000 x 5000 x 1000; 64x64 on 256^3 to 1024^2 x 2048, 128x128
+// from 1536^3) plus a fixed per-round cost (prologue, epilogue).
 // With a K split (gemm_nn_split) the split tiles' round runs K / splits, and the reduction's
 // traffic and launch are added.
 #ifndef MMM_T0_EFF
@@ -149,7 +151,7 @@ constexpr double kPartialRoundBoost = MMM_PARTIAL_ROUND_BOOST;
 #define MMM_T2_EFF 0.82
 #endif
 #ifndef MMM_T3_EFF
-#define MMM_T3_EFF 0.90
+#define MMM_T3_EFF 0.91
 #endif
 // The 128x128 tile in an unsplit launch of one round runs its 3-stage ring (DeepTile128), faster
 // per CU than the 2-stage multi-round version the 0.76 was measured on: priced at 0.80, which
