@@ -11,8 +11,8 @@
 // library's own tile choice (mmm_gemm_f16f32), which is also what WMMA_Auto does.
 //
 // The reference's launched parameters, <2,2,4,4>, name a 128x128 block (mmm.cpp:1462-1465), so
-// this spelling runs the library's 128x128 tile: at 8192^3 on MI355X that tile measured 1044.0
-// TFLOP/s against 1363.9 for the 256x256 tile the library picks itself (same box).  Call sites
+// this spelling runs the library's 128x128 tile: at 8192^3 on MI355X that tile measured 1031.0
+// TFLOP/s against 1372.2 for the 256x256 tile the library picks itself (same box).  Call sites
 // that do not need the reference's exact tile should use WMMA_Auto.
 #ifndef MMM_HPP
 #define MMM_HPP
