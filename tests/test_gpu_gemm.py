@@ -425,6 +425,32 @@ def test_stream_graph_capture(mm, cuda, rows, ws):
         assert np.array_equal(mm.gemm(A, B).cpu().numpy(), truth)
 
 
+@pytest.mark.parametrize("shape", [(2048, 2048, 2048), (8192, 4096, 512), (1024, 1024, 8192), (3000, 3070, 1031)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_tile_graph_capture(mm, cuda, shape):
+    """The tile kernels' store paths captured into a HIP graph: one round with write-through
+    whole-line stores (2048^3), a persistent grid with non-temporal whole-line stores (8192 x 4096
+    x 512, two rounds), a K split with write-through partial tiles and the reduction launch
+    (1024^2 x 8192), and the 192x192 tile with edge tiles (3000 x 3070 x 1031).  Every replay, with
+    eager work and synchronisation in between, equals the eager result bit for bit."""
+    M, N, K = shape
+    A = cuda.empty((M, K), dtype=cuda.float16, device="cuda")
+    B = cuda.empty((K, N), dtype=cuda.float16, device="cuda")
+    mm.fill_uniform(A, 11, 0)
+    mm.fill_uniform(B, 11, 1)
+    eager = mm.gemm(A, B)
+    C = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
+    g = cuda.cuda.CUDAGraph()
+    with cuda.cuda.graph(g):
+        mm.gemm(A, B, C)
+    for i in range(3):
+        C.fill_(float("nan"))
+        g.replay()
+        cuda.cuda.synchronize()
+        assert cuda.equal(C, eager), f"replay {i}"
+        assert cuda.equal(mm.gemm(A, B), eager)
+
+
 # shapes whose launch splits K: streaming (16 and 40 rows), one small round of tiles, a partly
 # filled last round (with a gathered K tail), and the 128x128 tile
 WS_SHAPES = [(16, 8192, 2048), (40, 4096, 4096), (1024, 1024, 8192), (4357, 4095, 8191), (300, 264, 4096)]
