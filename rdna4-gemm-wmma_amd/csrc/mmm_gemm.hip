@@ -223,12 +223,9 @@ __device__ __forceinline__ void wait_tiles(int n) {
 __device__ __forceinline__ uint32_t lds_addr_of(const char LDS_AS* p) { return (uint32_t)(uintptr_t)p; }
 
 // A buffer descriptor's record count for `bytes` readable bytes: 0 if none, at most kOobOffset.
-// Compared in 32-bit halves, which stay scalar; a 64-bit compare against the constant is a
-// vector compare, and held the constant in two VGPRs for the whole kernel.
 __device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
-  const uint32_t hi = (uint32_t)((uint64_t)bytes >> 32), lo = (uint32_t)bytes;
-  if ((int32_t)hi < 0) return 0u;
-  return (hi != 0u || lo > kOobOffset) ? kOobOffset : lo;
+  if (bytes <= 0) return 0u;
+  return bytes > (int64_t)kOobOffset ? kOobOffset : (uint32_t)bytes;
 }
 
 // One pass over an LDS stage: KSTEPS K-steps of FM x FN MFMAs.  `after_first_reads` runs
