@@ -903,3 +903,62 @@ def test_bind_contract(mm, cuda, orc):
         Out.fill_(float("nan"))
         launch()
         assert np.array_equal(Out.cpu().numpy(), truth)
+
+
+def _fold_case(rng, ext, order_a, order_b, order_c):
+    """Integer-valued operands laid out with the given axis orders over the sub-indices
+    mh, ml (rows), nh, nl (columns), kh, kl (reduction), and the descriptor that addresses them in
+    place (element strides read off the arrays)."""
+    import mmm
+
+    def make(order, dtype, fill=True):
+        shape = tuple(ext[a] for a in order)
+        x = rng.integers(-4, 5, size=shape).astype(dtype) if fill else np.zeros(shape, dtype)
+        return x, {a: x.strides[i] // x.itemsize for i, a in enumerate(order)}
+
+    A, sa = make(order_a, np.float16)
+    B, sb = make(order_b, np.float16)
+    Cz, sc = make(order_c, np.float32, fill=False)
+    d = mmm.ContractDesc()
+    d.m_ext[0], d.m_ext[1] = ext["mh"], ext["ml"]
+    d.n_ext[0], d.n_ext[1] = ext["nh"], ext["nl"]
+    d.k_ext[0], d.k_ext[1] = ext["kh"], ext["kl"]
+    d.a_m_stride[0], d.a_m_stride[1] = sa["mh"], sa["ml"]
+    d.a_k_stride[0], d.a_k_stride[1] = sa["kh"], sa["kl"]
+    d.b_k_stride[0], d.b_k_stride[1] = sb["kh"], sb["kl"]
+    d.b_n_stride[0], d.b_n_stride[1] = sb["nh"], sb["nl"]
+    d.c_m_stride[0], d.c_m_stride[1] = sc["mh"], sc["ml"]
+    d.c_n_stride[0], d.c_n_stride[1] = sc["nh"], sc["nl"]
+    spec = lambda order: "".join({"mh": "a", "ml": "b", "nh": "c", "nl": "d", "kh": "e", "kl": "f"}[x] for x in order)
+    truth = np.einsum(f"{spec(order_a)},{spec(order_b)}->{spec(order_c)}", A.astype(np.int64), B.astype(np.int64))
+    return d, A, B, Cz.shape, truth.astype(np.float32)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_contraction_random_folds_exact(mm, cuda, seed):
+    """Random 2-level folds: every operand's four sub-indices in a random memory order (the generic
+    gathering kernel, or the direct-to-LDS fold kernel when the K sub-index happens to be
+    contiguous in both operands), integer inputs, bit-exact against an int64 einsum."""
+    rng = np.random.default_rng(1000 + seed)
+    ext = {"mh": int(rng.integers(2, 6)), "ml": int(rng.integers(3, 40)), "nh": int(rng.integers(2, 6)),
+           "nl": int(rng.integers(3, 40)), "kh": int(rng.integers(1, 5)), "kl": int(rng.integers(1, 80))}
+    order_a = list(rng.permutation(["mh", "ml", "kh", "kl"]))
+    order_b = list(rng.permutation(["kh", "kl", "nh", "nl"]))
+    order_c = list(rng.permutation(["mh", "ml", "nh", "nl"]))
+    d, A, B, cshape, truth = _fold_case(rng, ext, order_a, order_b, order_c)
+    Cd = cuda.full(cshape, float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(d, to_dev(cuda, A), to_dev(cuda, B), Cd)
+    got = Cd.cpu().numpy()
+    assert np.array_equal(got, truth), f"{ext} {order_a} {order_b} {order_c}: {int((got != truth).sum())} mismatches"
+
+
+def test_contraction_fold_dma_path_exact(mm, cuda):
+    """A fold whose K sub-index is contiguous in both operands, in whole 64-deep tiles (the
+    direct-to-LDS fold kernel) with permuted M and N sub-indices and a permuted C."""
+    rng = np.random.default_rng(77)
+    ext = {"mh": 5, "ml": 72, "nh": 3, "nl": 100, "kh": 3, "kl": 128}
+    d, A, B, cshape, truth = _fold_case(rng, ext, ["kh", "mh", "ml", "kl"], ["nl", "kh", "nh", "kl"],
+                                        ["nh", "mh", "nl", "ml"])
+    Cd = cuda.full(cshape, float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(d, to_dev(cuda, A), to_dev(cuda, B), Cd)
+    assert np.array_equal(Cd.cpu().numpy(), truth)
