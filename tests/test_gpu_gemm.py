@@ -962,3 +962,29 @@ def test_contraction_fold_dma_path_exact(mm, cuda):
     Cd = cuda.full(cshape, float("nan"), dtype=cuda.float32, device="cuda")
     mm.contract(d, to_dev(cuda, A), to_dev(cuda, B), Cd)
     assert np.array_equal(Cd.cpu().numpy(), truth)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_exact_random_views(mm, cuda, seed):
+    """Random shapes (1..700 per side, some past 256 for multi-tile grids), random row pitches of
+    A, B and C, random element offsets of each base (2- to 16-byte alignment), and the planner's
+    tile or a random forced one: bit-exact on integer inputs, nothing written outside C's view."""
+    rng = np.random.default_rng(4242 + seed)
+    M, N, K = (int(x) for x in rng.integers(1, 701, size=3))
+    A, B, truth = _int_inputs(rng, M, N, K)
+    pa, pb, pc = (int(x) for x in rng.integers(0, 12, size=3))
+    oa, ob, oc = (int(x) for x in rng.integers(0, 8, size=3))
+    Abig = np.zeros((M, K + pa + oa), dtype=np.float16)
+    Abig[:, oa:oa + K] = A
+    Bbig = np.zeros((K, N + pb + ob), dtype=np.float16)
+    Bbig[:, ob:ob + N] = B
+    Ad = to_dev(cuda, Abig)[:, oa:oa + K]
+    Bd = to_dev(cuda, Bbig)[:, ob:ob + N]
+    Cbig = cuda.full((M, N + pc + oc), -1.0, dtype=cuda.float32, device="cuda")
+    Cv = Cbig[:, oc:oc + N]
+    tile = [None, None, "256x256", "192x192", "128x256", "256x128", "128x128", "64x64"][seed % 8]
+    mm.gemm(Ad, Bd, Cv, tile=tile)
+    C = Cbig.cpu().numpy()
+    where = f"{M}x{N}x{K} pads {pa},{pb},{pc} offsets {oa},{ob},{oc} tile {tile}"
+    assert np.array_equal(C[:, oc:oc + N], truth), where
+    assert np.all(C[:, :oc] == -1.0) and np.all(C[:, oc + N:] == -1.0), "wrote outside the C view: " + where
