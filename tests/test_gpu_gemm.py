@@ -988,3 +988,28 @@ def test_exact_random_views(mm, cuda, seed):
     where = f"{M}x{N}x{K} pads {pa},{pb},{pc} offsets {oa},{ob},{oc} tile {tile}"
     assert np.array_equal(C[:, oc:oc + N], truth), where
     assert np.all(C[:, :oc] == -1.0) and np.all(C[:, oc + N:] == -1.0), "wrote outside the C view: " + where
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_exact_random_skinny(mm, cuda, seed):
+    """Random M <= 64 problems (the streaming kernels and the tile+stream split), random N and K,
+    row pitches and base offsets, with the wrapper's workspace or none: bit-exact, confined to C."""
+    rng = np.random.default_rng(777 + seed)
+    M = int(rng.integers(1, 65))
+    N, K = (int(x) for x in rng.integers(1, 3001, size=2))
+    A, B, truth = _int_inputs(rng, M, N, K)
+    pa, pb, pc = (int(x) for x in rng.integers(0, 12, size=3))
+    oa, ob, oc = (int(x) for x in rng.integers(0, 8, size=3))
+    Abig = np.zeros((M, K + pa + oa), dtype=np.float16)
+    Abig[:, oa:oa + K] = A
+    Bbig = np.zeros((K, N + pb + ob), dtype=np.float16)
+    Bbig[:, ob:ob + N] = B
+    Ad = to_dev(cuda, Abig)[:, oa:oa + K]
+    Bd = to_dev(cuda, Bbig)[:, ob:ob + N]
+    Cbig = cuda.full((M, N + pc + oc), -1.0, dtype=cuda.float32, device="cuda")
+    ws = None if seed % 2 == 0 else False
+    mm.gemm(Ad, Bd, Cbig[:, oc:oc + N], workspace=ws)
+    C = Cbig.cpu().numpy()
+    where = f"{M}x{N}x{K} pads {pa},{pb},{pc} offsets {oa},{ob},{oc} workspace {ws is None}"
+    assert np.array_equal(C[:, oc:oc + N], truth), where
+    assert np.all(C[:, :oc] == -1.0) and np.all(C[:, oc + N:] == -1.0), "wrote outside the C view: " + where
