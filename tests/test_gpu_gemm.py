@@ -1013,3 +1013,66 @@ def test_exact_random_skinny(mm, cuda, seed):
     where = f"{M}x{N}x{K} pads {pa},{pb},{pc} offsets {oa},{ob},{oc} workspace {ws is None}"
     assert np.array_equal(C[:, oc:oc + N], truth), where
     assert np.all(C[:, :oc] == -1.0) and np.all(C[:, oc + N:] == -1.0), "wrote outside the C view: " + where
+
+
+def _dev_ints(torch, gen, shape):
+    return torch.randint(-4, 5, shape, generator=gen, device="cuda", dtype=torch.int8).to(torch.float16)
+
+
+def _assert_exact_rows(torch, A, B, C, label, chunk=8192):
+    """C (a device view) equals the fp64 product A.B exactly, compared on the device in row chunks
+    (integer inputs: every value is an integer below 2^24, exact in fp32 and fp64)."""
+    Bd = B.double()
+    for r0 in range(0, A.shape[0], chunk):
+        want = (A[r0:r0 + chunk].double() @ Bd).float()
+        same = torch.equal(C[r0:r0 + chunk], want)
+        assert same, f"{label}: rows {r0}..{r0 + chunk} differ (max |d| {(C[r0:r0 + chunk] - want).abs().max().item()})"
+    del Bd
+
+
+@pytest.mark.parametrize("case", ["big_c", "big_c_persistent", "big_a", "big_b"])
+def test_large_operands_exact(mm, cuda, case):
+    """Operands and results past 2^31 elements (byte offsets past 4 GiB): per-tile buffer
+    descriptors rebased from 64-bit pointers, 64-bit C addressing, the element-wise K-tail
+    gather and the K-split partials, all bit-exact against a device fp64 product and confined to
+    C's view.  big_c: C of 66000 x 33008 floats (K = 40); big_c_persistent: C of 65792 x 33032
+    floats on the persistent 256 x 256 grid (K = 256); big_a: A of 66000 x 33001 halves (odd
+    rows, K tail gathered); big_b: B of 66000 x 33001 halves under M = 16 and M = 300."""
+    torch = cuda
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(20241202)
+    if case == "big_c":
+        shapes = [(66000, 33000, 40)]
+        A_all = _dev_ints(torch, gen, (66000, 40))
+        B = _dev_ints(torch, gen, (40, 33000))
+    elif case == "big_c_persistent":
+        shapes = [(65792, 33024, 256)]
+        assert mm.gemm_plan(*shapes[0])["tile_persistent"] == 1
+        A_all = _dev_ints(torch, gen, (65792, 256))
+        B = _dev_ints(torch, gen, (256, 33024))
+    elif case == "big_a":
+        shapes = [(66000, 72, 33001)]
+        A_all = _dev_ints(torch, gen, (66000, 33001))
+        B = _dev_ints(torch, gen, (33001, 72))
+    else:
+        shapes = [(16, 33001, 66000), (300, 33001, 66000)]
+        A_all = _dev_ints(torch, gen, (300, 66000))
+        B = _dev_ints(torch, gen, (66000, 33001))
+    try:
+        for M, N, K in shapes:
+            print(f"large operands {case}: {M}x{N}x{K}", flush=True)
+            A = A_all[:M]
+            off, pad = 4, 4
+            Cbuf = torch.full((M, N + off + pad), -1.0, dtype=torch.float32, device="cuda")
+            Cv = Cbuf[:, off:off + N]
+            mm.gemm(A, B, Cv)
+            torch.cuda.synchronize()
+            assert bool((Cbuf[:, :off] == -1.0).all()) and bool((Cbuf[:, off + N:] == -1.0).all()), \
+                f"{case} {M}x{N}x{K}: wrote outside the C view"
+            _assert_exact_rows(torch, A, B, Cv, f"{case} {M}x{N}x{K}")
+            del Cbuf, Cv
+        big = max(A_all.numel(), B.numel(), shapes[0][0] * (shapes[0][1] + 8))
+        assert big > 2 ** 31, f"{case}: no operand past 2^31 elements ({big})"
+    finally:
+        del A_all, B
+        torch.cuda.empty_cache()
