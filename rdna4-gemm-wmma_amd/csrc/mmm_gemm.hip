@@ -192,6 +192,16 @@ __device__ __forceinline__ void dma_b128(uint32_t lds_addr, i32x4 rsrc, uint32_t
                : "s"(lds_addr), "v"(voff), "s"(rsrc)
                : "memory", "m0");
 }
+
+// The same 16 bytes per lane from a 64-bit global address (global_load_lds_dwordx4, gfx950),
+// for operands whose per-lane offsets do not fit a buffer's 32 bits.  No range check: the
+// caller passes addresses inside the operand.
+__device__ __forceinline__ void dma_b128_flat(uint32_t lds_addr, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_addr), "v"(src)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Wait until at most N of this wave's vector-memory operations are outstanding (they
@@ -1449,10 +1459,17 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
 //    and read with ds_read_b128 fragments.
 //  * Rows past M and columns past N are pushed out of the descriptor range (read as zero);
 //    the host requires K to be a multiple of the tile depth.
+//  * LANEK: folds whose K tiles cross k_hi blocks (k_lo a multiple of 8 but not of 64, e.g. an
+//    rt_l of 120): each lane keeps its own chunk's (k_hi, k_rem) and offsets, advanced by one
+//    tile per step; a 16-byte chunk never crosses a block.  The host requires K % 64 == 0.
+//  * WIDE: operands whose offsets pass the buffer's 32 bits (a G of more than 1 GiB) are read
+//    through 64-bit per-lane addresses instead (global_load_lds_dwordx4).  Rows past M and
+//    columns past N then load row M-1 / column N-1: they feed only accumulators of rows and
+//    columns the epilogue never stores.
 //  * Output scattered through the C strides: lanes own consecutive m, so an output whose
 //    m_lo is contiguous (Out[m][b][r]) is written in 128-byte runs.
 // ------------------------------------------------------------------------------------
-template <class T, bool NT>
+template <class T, bool NT, bool WIDE, bool LANEK>
 __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProblem p, int tiles_m, int tiles_n,
                                                                       uint32_t a_bytes, uint32_t b_bytes) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
@@ -1472,16 +1489,25 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
 
   const int row0 = w * (64 / T::CA) + lane / T::CA;
   const int kc = 8 * ((lane % T::CA) ^ T::swz_a(row0));
-  uint32_t a_voff[T::RA], b_voff[RBK];
+  const int kc_row = LANEK ? 0 : kc;  // LANEK: the chunk's K offset is kept per lane, apart
+  uint32_t a_voff[WIDE ? 1 : T::RA], b_voff[WIDE ? 1 : RBK];
+  const char* a_src[WIDE ? T::RA : 1];
+  const char* b_src[WIDE ? RBK : 1];
 #pragma unroll
   for (int r = 0; r < T::RA; ++r) {
     const int m = m0 + row0 + r * RPA;
-    a_voff[r] = m < M ? (uint32_t)((fold_off(m, p.m_lo, p.am[0], p.am[1]) + kc) * 2) : kOobOffset;
+    if constexpr (WIDE)
+      a_src[r] = (const char*)p.A + (fold_off(m < M ? m : M - 1, p.m_lo, p.am[0], p.am[1]) + kc_row) * 2;
+    else
+      a_voff[r] = m < M ? (uint32_t)((fold_off(m, p.m_lo, p.am[0], p.am[1]) + kc_row) * 2) : kOobOffset;
   }
 #pragma unroll
   for (int r = 0; r < RBK; ++r) {
     const int n = n0 + row0 + r * RPA;
-    b_voff[r] = n < N ? (uint32_t)((fold_off(n, p.n_lo, p.bn[0], p.bn[1]) + kc) * 2) : kOobOffset;
+    if constexpr (WIDE)
+      b_src[r] = (const char*)p.B + (fold_off(n < N ? n : N - 1, p.n_lo, p.bn[0], p.bn[1]) + kc_row) * 2;
+    else
+      b_voff[r] = n < N ? (uint32_t)((fold_off(n, p.n_lo, p.bn[0], p.bn[1]) + kc_row) * 2) : kOobOffset;
   }
 
   // fragment read offsets: A rows and K-major B columns share the layout (lane l reads row
@@ -1508,25 +1534,72 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
   const i32x4 rb = make_rsrc(p.B, b_bytes);
   // K tile t starts at k0 = t * BK = (k_hi, k_rem): uniform offsets k_hi * ak0 + k_rem (A) and
   // k_hi * bk0 + k_rem (B), advanced per tile (tiles are prepared in order).
+  using KOff = std::conditional_t<WIDE, int64_t, uint32_t>;
   struct FoldDma {
-    uint32_t a_dst, b_dst, ka, kb;
+    uint32_t a_dst, b_dst;
+    KOff ka, kb;
   };
+  // LANEK: k_rem is this lane's chunk position inside its k_hi block; the row offsets (or
+  // addresses) carry the chunk's K offset and advance by one K tile per prep (tiles are
+  // prepared in order, and each tile's loads are issued before the next prep).
   int k_hi = 0, k_rem = 0;
+  KOff a_wrap = 0, b_wrap = 0;
+  if constexpr (LANEK) {
+    k_hi = kc / p.k_lo, k_rem = kc - k_hi * p.k_lo;
+    const int64_t ka0 = ((int64_t)k_hi * p.ak[0] + k_rem) * 2, kb0 = ((int64_t)k_hi * p.bk[0] + k_rem) * 2;
+#pragma unroll
+    for (int r = 0; r < T::RA; ++r) {
+      if constexpr (WIDE) a_src[r] += ka0;
+      else a_voff[r] += (uint32_t)ka0;
+    }
+#pragma unroll
+    for (int r = 0; r < RBK; ++r) {
+      if constexpr (WIDE) b_src[r] += kb0;
+      else b_voff[r] += (uint32_t)kb0;
+    }
+    a_wrap = (KOff)((p.ak[0] - p.k_lo) * 2), b_wrap = (KOff)((p.bk[0] - p.k_lo) * 2);
+  }
   auto prep = [&](int t, int stage) {
     FoldDma d;
-    d.ka = (uint32_t)(((int64_t)k_hi * p.ak[0] + k_rem) * 2);
-    d.kb = (uint32_t)(((int64_t)k_hi * p.bk[0] + k_rem) * 2);
-    k_rem += T::BK;
-    if (k_rem == p.k_lo) k_rem = 0, ++k_hi;
+    if constexpr (LANEK) {
+      d.ka = 0, d.kb = 0;
+      if (t > 0) {
+        KOff da = T::BK * 2, db = T::BK * 2;
+        k_rem += T::BK;
+        while (k_rem >= p.k_lo) k_rem -= p.k_lo, da += a_wrap, db += b_wrap;
+#pragma unroll
+        for (int r = 0; r < T::RA; ++r) {
+          if constexpr (WIDE) a_src[r] += da;
+          else a_voff[r] += da;
+        }
+#pragma unroll
+        for (int r = 0; r < RBK; ++r) {
+          if constexpr (WIDE) b_src[r] += db;
+          else b_voff[r] += db;
+        }
+      }
+    } else {
+      d.ka = (KOff)(((int64_t)k_hi * p.ak[0] + k_rem) * 2);
+      d.kb = (KOff)(((int64_t)k_hi * p.bk[0] + k_rem) * 2);
+      k_rem += T::BK;
+      if (k_rem == p.k_lo) k_rem = 0, ++k_hi;
+    }
     d.a_dst = lds_addr_of(lds_base) + stage * T::STAGE + w * 64 * 16;
     d.b_dst = d.a_dst + T::A_BYTES;
     return d;
   };
   auto dma_one = [&](const FoldDma& d, int j) {
-    if (j < T::RA)
-      dma_b128(d.a_dst + j * T::NT * 16, ra, a_voff[j] + d.ka);
-    else
-      dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, rb, b_voff[j - T::RA] + d.kb);
+    if constexpr (WIDE) {
+      if (j < T::RA)
+        dma_b128_flat(d.a_dst + j * T::NT * 16, a_src[j] + d.ka);
+      else
+        dma_b128_flat(d.b_dst + (j - T::RA) * T::NT * 16, b_src[j - T::RA] + d.kb);
+    } else {
+      if (j < T::RA)
+        dma_b128(d.a_dst + j * T::NT * 16, ra, a_voff[j] + d.ka);
+      else
+        dma_b128(d.b_dst + (j - T::RA) * T::NT * 16, rb, b_voff[j - T::RA] + d.kb);
+    }
   };
   auto issue_tile = [&](int t, int stage) {
     const FoldDma d = prep(t, stage);
@@ -1948,18 +2021,34 @@ static int64_t fold_extent(int64_t e_hi, int64_t e_lo, int64_t s_hi, int64_t s_l
   return (e_hi - 1) * s_hi + (e_lo - 1) * s_lo + (f_hi - 1) * t_hi + (f_lo - 1) * t_lo + 1;
 }
 
+template <bool NT, bool WIDE>
+static void launch_fold_dma(const FoldProblem& p, bool lanek, int tiles_m, int tiles_n, uint32_t a_bytes,
+                            uint32_t b_bytes, hipStream_t stream) {
+  using TD = FoldDmaTile;
+  const dim3 grid((unsigned)((int64_t)tiles_m * tiles_n)), block(TD::NT);
+  if (lanek)
+    hipLaunchKernelGGL((gemm_fold_dma_kernel<TD, NT, WIDE, true>), grid, block, 0, stream, p, tiles_m, tiles_n, a_bytes,
+                       b_bytes);
+  else
+    hipLaunchKernelGGL((gemm_fold_dma_kernel<TD, NT, WIDE, false>), grid, block, 0, stream, p, tiles_m, tiles_n, a_bytes,
+                       b_bytes);
+}
+
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream) {
-  // direct-to-LDS fold path: K contiguous in both operands, K tiles inside one k_hi block,
-  // 16-byte-aligned chunks, offsets within 32 bits
+  // direct-to-LDS fold path: K contiguous in both operands, 16-byte-aligned chunks; K tiles
+  // inside one k_hi block (k_lo % 64 == 0) or, per lane, crossing blocks (k_lo % 8 == 0,
+  // K % 64 == 0); buffer loads when the offsets fit 32 bits, else 64-bit addresses
   using TD = FoldDmaTile;
   const int m_hi = (p.M + p.m_lo - 1) / p.m_lo, n_hi = (p.N + p.n_lo - 1) / p.n_lo, k_hi = p.K / p.k_lo;
   const int64_t a_ext = fold_extent(m_hi, p.m_lo, p.am[0], p.am[1], k_hi, p.k_lo, p.ak[0], p.ak[1]);
   const int64_t b_ext = fold_extent(n_hi, p.n_lo, p.bn[0], p.bn[1], k_hi, p.k_lo, p.bk[0], p.bk[1]);
-  const bool fast = TD::BK == 64 && p.ak[1] == 1 && p.bk[1] == 1 && p.k_lo % TD::BK == 0 && p.K % p.k_lo == 0 &&
+  const bool lanek = p.k_lo % TD::BK != 0;
+  const bool fast = TD::BK == 64 && p.ak[1] == 1 && p.bk[1] == 1 && p.k_lo % 8 == 0 && p.K % p.k_lo == 0 &&
+                    p.K % TD::BK == 0 &&
                     p.am[0] % 8 == 0 && p.am[1] % 8 == 0 && p.bn[0] % 8 == 0 && p.bn[1] % 8 == 0 &&
                     p.ak[0] % 8 == 0 && p.bk[0] % 8 == 0 && ((uintptr_t)p.A & 15) == 0 && ((uintptr_t)p.B & 15) == 0 &&
-                    a_ext > 0 && b_ext > 0 && a_ext * 2 < (int64_t)kOobOffset / 2 && b_ext * 2 < (int64_t)kOobOffset / 2 &&
-                    p.M % p.m_lo == 0 && p.N % p.n_lo == 0;
+                    a_ext > 0 && b_ext > 0 && p.M % p.m_lo == 0 && p.N % p.n_lo == 0;
+  const bool wide = a_ext * 2 >= (int64_t)kOobOffset / 2 || b_ext * 2 >= (int64_t)kOobOffset / 2;
   if (fast) {
     const int tiles_m = (p.M + TD::BM - 1) / TD::BM;
     const int tiles_n = (p.N + TD::BN - 1) / TD::BN;
@@ -1968,12 +2057,18 @@ hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream) {
     // evict operand panels (measured on MI355X at the reference's M = N = K = 8192: +13-15%).  A
     // one-round grid writes all of C after its last K step, where L2-allocating stores drain
     // faster (plain-GEMM tiles: 4096^3 -5.5%, 8192 x 2048 x 2048 -6.7% with non-temporal stores).
-    if ((int64_t)tiles_m * tiles_n > 256 && p.K >= kNtMinK)
-      hipLaunchKernelGGL((gemm_fold_dma_kernel<TD, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(TD::NT), 0, stream,
-                         p, tiles_m, tiles_n, (uint32_t)(a_ext * 2), (uint32_t)(b_ext * 2));
+    const int64_t blocks = (int64_t)tiles_m * tiles_n;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const bool nt = blocks > 256 && p.K >= kNtMinK;
+    const uint32_t ab = wide ? 0u : (uint32_t)(a_ext * 2), bb = wide ? 0u : (uint32_t)(b_ext * 2);
+    if (wide && nt)
+      launch_fold_dma<true, true>(p, lanek, tiles_m, tiles_n, ab, bb, stream);
+    else if (wide)
+      launch_fold_dma<false, true>(p, lanek, tiles_m, tiles_n, ab, bb, stream);
+    else if (nt)
+      launch_fold_dma<true, false>(p, lanek, tiles_m, tiles_n, ab, bb, stream);
     else
-      hipLaunchKernelGGL((gemm_fold_dma_kernel<TD, false>), dim3((unsigned)(tiles_m * tiles_n)), dim3(TD::NT), 0,
-                         stream, p, tiles_m, tiles_n, (uint32_t)(a_ext * 2), (uint32_t)(b_ext * 2));
+      launch_fold_dma<false, false>(p, lanek, tiles_m, tiles_n, ab, bb, stream);
     return hipGetLastError();
   }
   using T = RegTile<128, 128>;

@@ -35,9 +35,9 @@ LDS_PER_CU = 160 * 1024
 # static instruction classes counted in each kernel body
 CLASSES = [
     ("mfma", re.compile(r"^\s*v_mfma_")),
-    ("dma_lds", re.compile(r"^\s*(buffer|global)_load_\w+.*\blds\b")),
+    ("dma_lds", re.compile(r"^\s*(buffer|global)_load_(lds_\w+|\w+.*\blds\b)")),
     ("ds_read", re.compile(r"^\s*ds_read")),
-    ("vmem_load", re.compile(r"^\s*(buffer|global)_load_(?!.*\blds\b)")),
+    ("vmem_load", re.compile(r"^\s*(buffer|global)_load_(?!lds_)(?!.*\blds\b)")),
     ("vmem_store", re.compile(r"^\s*(buffer|global)_store_")),
     ("barrier", re.compile(r"^\s*s_barrier\b")),
     ("waitcnt", re.compile(r"^\s*s_waitcnt\b")),

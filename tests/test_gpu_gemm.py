@@ -783,6 +783,26 @@ def test_contraction_reference_layout_dma_exact(mm, cuda, orc, dims):
     assert np.array_equal(Out.cpu().numpy(), truth.astype(np.float32))
 
 
+# rt_l a multiple of 8 but not of 64 (K tiles cross n blocks; each lane tracks its own chunk's
+# block): rt_l = 8 crosses eight blocks per K tile, 200 at most one; bt = 301 stores element by
+# element; rt = 6 rows of 6; 32 x 8448 x 64 runs two rounds of tiles
+@pytest.mark.parametrize("dims", [(8, 300, 64, 24, 8), (4, 520, 32, 8, 24), (8, 301, 64, 8, 40), (8, 300, 6, 8, 120),
+                                  (32, 8448, 64, 8, 72), (8, 300, 64, 8, 200)],
+                         ids=lambda d: "x".join(map(str, d)))
+def test_contraction_reference_layout_lane_k_exact(mm, cuda, orc, dims):
+    """Reference layout on the direct-to-LDS fold path with per-lane K blocks: bit-exact."""
+    mt, bt, rt, nt, rt_l = dims
+    assert rt_l % 8 == 0 and rt_l % 64 and nt * rt_l % 64 == 0
+    rng = np.random.default_rng(sum(dims) + 2)
+    G = rng.integers(-4, 5, size=(rt, nt, mt, rt_l)).astype(np.float16)
+    In = rng.integers(-4, 5, size=(bt, nt, rt_l)).astype(np.float16)
+    hA = orc.pack_reference_G(G).astype(np.float64)
+    truth = (hA @ In.reshape(bt, nt * rt_l).astype(np.float64).T).reshape(mt, rt, bt).transpose(0, 2, 1)
+    Out = cuda.full((mt, bt, rt), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), to_dev(cuda, G), to_dev(cuda, In), Out)
+    assert np.array_equal(Out.cpu().numpy(), truth.astype(np.float32))
+
+
 def test_contraction_reference_layout_dma_unaligned_out(mm, cuda, orc):
     """Out 4-byte but not 16-byte aligned."""
     mt, bt, rt, nt, rt_l = 8, 300, 64, 3, 128
@@ -1075,4 +1095,46 @@ def test_large_operands_exact(mm, cuda, case):
         assert big > 2 ** 31, f"{case}: no operand past 2^31 elements ({big})"
     finally:
         del A_all, B
+        torch.cuda.empty_cache()
+
+
+LARGE_CONTRACTIONS = {  # (mt, bt, rt, nt, rt_l)
+    "big_out": (128, 270000, 64, 2, 64),         # Out past 2^31 floats; 32-bit buffer loads
+    "big_g": (128, 64, 64, 2100, 128),           # G past 2^31 halves: 64-bit direct-to-LDS loads
+    "big_g_ragged": (129, 100, 64, 1100, 128),   # the same with partial tiles (M = 8256, N = 100)
+    "big_g_lane_k": (128, 64, 64, 2200, 120),    # rt_l = 120: K tiles cross n blocks, per-lane K
+    "big_g_regs": (128, 64, 64, 2700, 100),      # rt_l = 100: 8-element chunks cross n blocks,
+}                                                # the register-staged fold kernel
+
+
+@pytest.mark.parametrize("case", sorted(LARGE_CONTRACTIONS))
+def test_large_reference_contraction_exact(mm, cuda, case):
+    """The reference's tensor program (Out[m][b][r] = sum_{n,l} G[r][n][m][l] In[b][n][l],
+    mmmTensor.cpp:246-252) past 2^31 elements, bit-exact on integer inputs against a device fp64
+    product.  big_out: the direct-to-LDS fold kernel's scattered epilogue at offsets past 4 GiB;
+    big_g / big_g_ragged / big_g_lane_k: a G of more than 1 GiB, read through 64-bit per-lane
+    addresses (rows and columns of partial tiles clamped to the last valid one; K tiles crossing
+    n blocks); big_g_regs: the register-staged fold kernel on a G past 2^31 halves."""
+    torch = cuda
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    mt, bt, rt, nt, rt_l = LARGE_CONTRACTIONS[case]
+    print(f"large reference contraction {case}: mt {mt} bt {bt} rt {rt} nt {nt} rt_l {rt_l}", flush=True)
+    G = _dev_ints(torch, gen, (rt, nt, mt, rt_l))
+    In = _dev_ints(torch, gen, (bt, nt, rt_l))
+    assert max(G.numel(), mt * bt * rt) > 2 ** 31 or case == "big_g_ragged"
+    assert 16 * nt * rt_l < 2 ** 24  # every partial sum exact in fp32
+    try:
+        Out = torch.full((mt, bt, rt), -1.0, dtype=torch.float32, device="cuda")
+        mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), G, In, Out)
+        torch.cuda.synchronize()
+        Bt = In.reshape(bt, nt * rt_l).double().t()
+        step = 8
+        for m0 in range(0, mt, step):
+            ms = min(step, mt - m0)
+            A2 = G[:, :, m0:m0 + ms, :].permute(2, 0, 1, 3).reshape(ms * rt, nt * rt_l).double()
+            want = (A2 @ Bt).float().reshape(ms, rt, bt).permute(0, 2, 1)
+            assert torch.equal(Out[m0:m0 + ms], want), f"{case}: m {m0}..{m0 + ms} differ"
+    finally:
+        del G, In
         torch.cuda.empty_cache()
