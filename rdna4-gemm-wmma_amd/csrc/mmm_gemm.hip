@@ -1457,11 +1457,12 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
 //    DMA load at a per-lane row base plus a uniform tile offset.
 //  * B is K-major (Input[b][n][l]: column b of B is contiguous in k), staged [BN][64] like A
 //    and read with ds_read_b128 fragments.
-//  * Rows past M and columns past N are pushed out of the descriptor range (read as zero);
-//    the host requires K to be a multiple of the tile depth.
+//  * Rows past M and columns past N are pushed out of the descriptor range (read as zero).
 //  * LANEK: folds whose K tiles cross k_hi blocks (k_lo a multiple of 8 but not of 64, e.g. an
 //    rt_l of 120): each lane keeps its own chunk's (k_hi, k_rem) and offsets, advanced by one
-//    tile per step; a 16-byte chunk never crosses a block.  The host requires K % 64 == 0.
+//    tile per step; a 16-byte chunk never crosses a block.  K is then a multiple of 8 but may
+//    end inside the last K tile: that tile's chunks at or past K are pushed out of the
+//    descriptor range too.  Otherwise (and always with WIDE) K is a multiple of 64.
 //  * WIDE: operands whose offsets pass the buffer's 32 bits (a G of more than 1 GiB) are read
 //    through 64-bit per-lane addresses instead (global_load_lds_dwordx4).  Rows past M and
 //    columns past N then load row M-1 / column N-1: they feed only accumulators of rows and
@@ -1578,6 +1579,17 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
           else b_voff[r] += db;
         }
       }
+      if constexpr (!WIDE) {
+        // K tail (the last tile only; nothing is loaded after it, so the offsets may stay out
+        // of range; a chunk past K may sit in a k_hi block past the fold's, whose offset means
+        // nothing, so it is replaced, not moved)
+        if (t * T::BK + kc >= K) {
+#pragma unroll
+          for (int r = 0; r < T::RA; ++r) a_voff[r] = kOobOffset;
+#pragma unroll
+          for (int r = 0; r < RBK; ++r) b_voff[r] = kOobOffset;
+        }
+      }
     } else {
       d.ka = (KOff)(((int64_t)k_hi * p.ak[0] + k_rem) * 2);
       d.kb = (KOff)(((int64_t)k_hi * p.bk[0] + k_rem) * 2);
@@ -1606,7 +1618,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
 #pragma unroll
     for (int j = 0; j < T::LPT; ++j) dma_one(d, j);
   };
-  cross_stage<T, true>(lds_base, K / T::BK, false, a_off, b_off, acc, prep, dma_one, issue_tile);
+  cross_stage<T, true>(lds_base, (K + T::BK - 1) / T::BK, false, a_off, b_off, acc, prep, dma_one, issue_tile);
 
   // epilogue: lane owns row m and columns n .. n+3 of each accumulator group, scattered
   // through the C strides (MF = 32: m = l % 32, n = 32*nb + 8*q + 4*(l/32); MF = 16:
@@ -2036,19 +2048,20 @@ static void launch_fold_dma(const FoldProblem& p, bool lanek, int tiles_m, int t
 
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream) {
   // direct-to-LDS fold path: K contiguous in both operands, 16-byte-aligned chunks; K tiles
-  // inside one k_hi block (k_lo % 64 == 0) or, per lane, crossing blocks (k_lo % 8 == 0,
-  // K % 64 == 0); buffer loads when the offsets fit 32 bits, else 64-bit addresses
+  // inside one k_hi block (k_lo % 64 == 0) or, per lane, crossing blocks (k_lo % 8 == 0);
+  // buffer loads when the offsets fit 32 bits, else 64-bit addresses (K % 64 == 0: no range
+  // check masks a K tail there)
   using TD = FoldDmaTile;
   const int m_hi = (p.M + p.m_lo - 1) / p.m_lo, n_hi = (p.N + p.n_lo - 1) / p.n_lo, k_hi = p.K / p.k_lo;
   const int64_t a_ext = fold_extent(m_hi, p.m_lo, p.am[0], p.am[1], k_hi, p.k_lo, p.ak[0], p.ak[1]);
   const int64_t b_ext = fold_extent(n_hi, p.n_lo, p.bn[0], p.bn[1], k_hi, p.k_lo, p.bk[0], p.bk[1]);
   const bool lanek = p.k_lo % TD::BK != 0;
+  const bool wide = a_ext * 2 >= (int64_t)kOobOffset / 2 || b_ext * 2 >= (int64_t)kOobOffset / 2;
   const bool fast = TD::BK == 64 && p.ak[1] == 1 && p.bk[1] == 1 && p.k_lo % 8 == 0 && p.K % p.k_lo == 0 &&
-                    p.K % TD::BK == 0 &&
+                    (p.K % TD::BK == 0 || !wide) &&
                     p.am[0] % 8 == 0 && p.am[1] % 8 == 0 && p.bn[0] % 8 == 0 && p.bn[1] % 8 == 0 &&
                     p.ak[0] % 8 == 0 && p.bk[0] % 8 == 0 && ((uintptr_t)p.A & 15) == 0 && ((uintptr_t)p.B & 15) == 0 &&
                     a_ext > 0 && b_ext > 0 && p.M % p.m_lo == 0 && p.N % p.n_lo == 0;
-  const bool wide = a_ext * 2 >= (int64_t)kOobOffset / 2 || b_ext * 2 >= (int64_t)kOobOffset / 2;
   if (fast) {
     const int tiles_m = (p.M + TD::BM - 1) / TD::BM;
     const int tiles_n = (p.N + TD::BN - 1) / TD::BN;

@@ -785,14 +785,17 @@ def test_contraction_reference_layout_dma_exact(mm, cuda, orc, dims):
 
 # rt_l a multiple of 8 but not of 64 (K tiles cross n blocks; each lane tracks its own chunk's
 # block): rt_l = 8 crosses eight blocks per K tile, 200 at most one; bt = 301 stores element by
-# element; rt = 6 rows of 6; 32 x 8448 x 64 runs two rounds of tiles
+# element; rt = 6 rows of 6; 32 x 8448 x 64 runs two rounds of tiles.  The last five end K
+# inside the last K tile (K = 120, 24 -- one partial tile --, 360, 200 with a single n block,
+# and 72)
 @pytest.mark.parametrize("dims", [(8, 300, 64, 24, 8), (4, 520, 32, 8, 24), (8, 301, 64, 8, 40), (8, 300, 6, 8, 120),
-                                  (32, 8448, 64, 8, 72), (8, 300, 64, 8, 200)],
+                                  (32, 8448, 64, 8, 72), (8, 300, 64, 8, 200), (8, 300, 64, 5, 24), (8, 301, 64, 3, 8),
+                                  (32, 8448, 64, 3, 120), (8, 300, 6, 1, 200), (4, 40, 8, 3, 24)],
                          ids=lambda d: "x".join(map(str, d)))
 def test_contraction_reference_layout_lane_k_exact(mm, cuda, orc, dims):
     """Reference layout on the direct-to-LDS fold path with per-lane K blocks: bit-exact."""
     mt, bt, rt, nt, rt_l = dims
-    assert rt_l % 8 == 0 and rt_l % 64 and nt * rt_l % 64 == 0
+    assert rt_l % 8 == 0 and rt_l % 64
     rng = np.random.default_rng(sum(dims) + 2)
     G = rng.integers(-4, 5, size=(rt, nt, mt, rt_l)).astype(np.float16)
     In = rng.integers(-4, 5, size=(bt, nt, rt_l)).astype(np.float16)
