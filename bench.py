@@ -20,7 +20,8 @@ Extra objects on the line:
 
 Other workloads (parity configs, reported with --workload or --report, never the default):
 gemm256, ragged, contraction, skinny (and skinny_nows, the same problem without a workspace),
-contraction_ref.  One GPU only: --gpus above 1 exits with a message.
+contraction_ref (and contraction_ref_rtl120 / contraction_ref_big, its fold variants with K tiles
+crossing n blocks and with a G of 2 GiB).  One GPU only: --gpus above 1 exits with a message.
 """
 from __future__ import annotations
 
@@ -53,6 +54,10 @@ WORKLOADS = {
     "skinny_nows": (16, 8192, 8192, "gemm", 4, "uniform"),
     # the reference's own contraction (mmmTensor.cpp:20-28): G[r][n][m][l] x Input[b][n][l]
     "contraction_ref": (8192, 8192, 8192, "contraction_ref", 5, "uniform"),
+    # the same program with rt_l = 120 (K tiles cross n blocks) and with a G of 2 GiB (past the
+    # buffer loads' 32-bit offsets)
+    "contraction_ref_rtl120": (8192, 8192, 7680, "contraction_ref", 5, "uniform"),
+    "contraction_ref_big": (8192, 16384, 131072, "contraction_ref", 5, "uniform"),
     # known-size reference for the HBM byte counters: a 256 MiB fp32 device-to-device copy
     "copy": (8192, 8192, 1, "copy", 0, "uniform"),
     # measured ceilings (library probes): the 8192^3 tile kernel's MFMA stream with register-
@@ -70,11 +75,23 @@ DESCRIPTIONS = {
     "skinny_nows": "gemm_nn 16x8192x8192 fp16 row-major without a workspace, U[-1,1) seed 4, 3 rotating B buffers",
     "contraction_ref": "contract5d Out[m][b][r]=sum_nl G[r][n][m][l] In[b][n][l], mt=128 bt=8192 rt=64 nt=64 rt_l=128, "
                        "U[-1,1) seed 5",
+    "contraction_ref_rtl120": "contract5d Out[m][b][r]=sum_nl G[r][n][m][l] In[b][n][l], mt=128 bt=8192 rt=64 nt=64 "
+                              "rt_l=120, U[-1,1) seed 5",
+    "contraction_ref_big": "contract5d Out[m][b][r]=sum_nl G[r][n][m][l] In[b][n][l], mt=128 bt=16384 rt=64 nt=1024 "
+                           "rt_l=128 (G 2 GiB), U[-1,1) seed 5",
     "copy": "copy 256 MiB fp32 device-to-device (counter scaling reference), zeros",
     "mfma_ceiling": "MFMA ceiling probe: the 8192x8192x8192 persistent tile kernel's MFMA stream and C stores with "
                     "register-resident operands (no loads, LDS or barriers), U[-1,1) seed 1",
     "read_ceiling": "HBM read ceiling probe: one pass over 1 GiB with 16-byte loads into registers, zeros",
     "read_ceiling_lds": "HBM read ceiling probe: one pass over 1 GiB with direct-to-LDS 16-byte loads, zeros",
+}
+
+
+# (mt, bt, rt, nt, rt_l) of the reference-layout contraction workloads (mmmTensor.cpp:20-24)
+REFERENCE_DIMS = {
+    "contraction_ref": (128, 8192, 64, 64, 128),
+    "contraction_ref_rtl120": (128, 8192, 64, 64, 120),
+    "contraction_ref_big": (128, 16384, 64, 1024, 128),
 }
 
 
@@ -122,7 +139,8 @@ def make_workload(name, torch, mmm):
         return {"launch": lambda: mmm.probe_mfma_ceiling(A, B, Cd), "witness": None, "host_inputs": None,
                 "clocked": clocked, "M": M, "N": N, "K": K}
     if kind == "contraction_ref":
-        mt, bt, rt, nt, rt_l = 128, 8192, 64, 64, 128
+        mt, bt, rt, nt, rt_l = REFERENCE_DIMS[name]
+        assert (mt * rt, bt, nt * rt_l) == (M, N, K)
         G = torch.empty((rt, nt, mt, rt_l), dtype=torch.float16, device=dev)
         In = torch.empty((bt, nt, rt_l), dtype=torch.float16, device=dev)
         fill(G, seed, 0)
