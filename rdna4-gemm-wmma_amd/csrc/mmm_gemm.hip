@@ -1295,6 +1295,65 @@ __device__ __forceinline__ int64_t fold_off(int i, int lo, int64_t s_hi, int64_t
   return (int64_t)(i / lo) * s_hi + (int64_t)(i % lo) * s_lo;
 }
 
+// X at the 8 consecutive fold indices i .. i+7 past base (index j at base + fold_off(j, ...)),
+// with one division for i and the rest stepped (the low sub-index carrying into the high one);
+// indices at or past `end` read as zero and are not dereferenced.
+__device__ __forceinline__ half8 gather8(const _Float16* X, int64_t base, int i, int end, int lo, int64_t s_hi,
+                                         int64_t s_lo) {
+  half8 v = {};
+  int l = i % lo;
+  int64_t off = base + (int64_t)(i / lo) * s_hi + (int64_t)l * s_lo;
+  const int64_t carry = s_hi - (int64_t)lo * s_lo;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (i + e < end) v[e] = X[off];
+    off += s_lo;
+    if (++l == lo) l = 0, off += carry;
+  }
+  return v;
+}
+
+// gather8 for a contiguous low sub-index (s_lo == 1) whose extent, high stride and row bases are
+// multiples of G, with X + base 2G-byte aligned: groups of G elements never cross a block, so each
+// is one 2G-byte load (end is then a multiple of G too: a group is wholly in or out).
+template <int G>
+__device__ __forceinline__ half8 gather8_vec(const _Float16* X, int64_t base, int i, int end, int lo, int64_t s_hi) {
+  typedef _Float16 halfG __attribute__((ext_vector_type(G)));
+  half8 v = {};
+  int l = i % lo;
+  int64_t off = base + (int64_t)(i / lo) * s_hi + l;
+#pragma unroll
+  for (int j = 0; j < 8 / G; ++j) {
+    if (i + j * G < end) {
+      const halfG g = *(const halfG*)(X + off);
+#pragma unroll
+      for (int e = 0; e < G; ++e) v[j * G + e] = g[e];
+    }
+    off += G, l += G;
+    if (l == lo) l = 0, off += s_hi - lo;
+  }
+  return v;
+}
+
+// Widest group (8, 4, 2 or 1 elements) gather8_vec may use for an operand whose fold index
+// (low extent lo, strides s_hi / s_lo) is contiguous, given every row base's strides r0, r1.
+__device__ __forceinline__ int gather_width(const void* X, int lo, int64_t s_hi, int64_t s_lo, int64_t r0, int64_t r1) {
+  if (s_lo != 1) return 1;
+#pragma unroll
+  for (int g = 8; g > 1; g /= 2)
+    if (lo % g == 0 && s_hi % g == 0 && r0 % g == 0 && r1 % g == 0 && (uintptr_t)X % (2 * g) == 0) return g;
+  return 1;
+}
+
+// gather8 at the widest group width gw (uniform: the branch is scalar).
+__device__ __forceinline__ half8 gather8_w(int gw, const _Float16* X, int64_t base, int i, int end, int lo, int64_t s_hi,
+                                           int64_t s_lo) {
+  if (gw == 8) return gather8_vec<8>(X, base, i, end, lo, s_hi);
+  if (gw == 4) return gather8_vec<4>(X, base, i, end, lo, s_hi);
+  if (gw == 2) return gather8_vec<2>(X, base, i, end, lo, s_hi);
+  return gather8(X, base, i, end, lo, s_hi, s_lo);
+}
+
 template <class T, bool BKM>
 __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int tiles_m, int tiles_n) {
   static_assert(T::MF == 32, "the folded kernels use 32x32 fragments");
@@ -1367,6 +1426,11 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
 
   const _Float16* A = (const _Float16*)p.A;
   const _Float16* B = (const _Float16*)p.B;
+  // group widths of the gathers: A along k (row bases from the m strides); B along k (K-major,
+  // column bases from the n strides) or along n (row bases from the k strides)
+  const int a_gw = gather_width(A, p.k_lo, p.ak[0], p.ak[1], p.am[0], p.am[1]);
+  const int b_gw = BKM ? gather_width(B, p.k_lo, p.bk[0], p.bk[1], p.bn[0], p.bn[1])
+                       : gather_width(B, p.n_lo, p.bn[0], p.bn[1], p.bk[0], p.bk[1]);
   u32x4 ra[T::RA], rb[RBK];
   auto load = [&](int t) {
     const int k0 = t * T::BK;
@@ -1374,11 +1438,7 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
     for (int r = 0; r < T::RA; ++r) {
       const int k = k0 + a_kc[r];
       half8 v = {};
-      if (m0 + a_row[r] < M) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (k + e < K) v[e] = A[a_base[r] + fold_off(k + e, p.k_lo, p.ak[0], p.ak[1])];
-      }
+      if (m0 + a_row[r] < M) v = gather8_w(a_gw, A, a_base[r], k, K, p.k_lo, p.ak[0], p.ak[1]);
       ra[r] = __builtin_bit_cast(u32x4, v);
     }
 #pragma unroll
@@ -1386,19 +1446,10 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
       half8 v = {};
       if constexpr (BKM) {
         const int k = k0 + b_c[r];
-        if (n0 + b_row[r] < N) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (k + e < K) v[e] = B[b_base[r] + fold_off(k + e, p.k_lo, p.bk[0], p.bk[1])];
-        }
+        if (n0 + b_row[r] < N) v = gather8_w(b_gw, B, b_base[r], k, K, p.k_lo, p.bk[0], p.bk[1]);
       } else {
         const int k = k0 + b_row[r], n = n0 + b_c[r];
-        if (k < K) {
-          const int64_t kb = fold_off(k, p.k_lo, p.bk[0], p.bk[1]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (n + e < N) v[e] = B[kb + fold_off(n + e, p.n_lo, p.bn[0], p.bn[1])];
-        }
+        if (k < K) v = gather8_w(b_gw, B, fold_off(k, p.k_lo, p.bk[0], p.bk[1]), n, N, p.n_lo, p.bn[0], p.bn[1]);
       }
       rb[r] = __builtin_bit_cast(u32x4, v);
     }

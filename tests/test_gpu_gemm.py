@@ -806,6 +806,30 @@ def test_contraction_reference_layout_lane_k_exact(mm, cuda, orc, dims):
     assert np.array_equal(Out.cpu().numpy(), truth.astype(np.float32))
 
 
+# Folds off the direct-to-LDS path, on the register-staged kernel's grouped gathers: rt_l = 100,
+# 50 and 25 give groups of 4, 2 and 1 elements; G or Input placed 4 or 2 elements into its buffer
+# narrows the group by its alignment (G 8-byte aligned: groups of 4 for A, 8 for Input)
+@pytest.mark.parametrize("dims,g_off,in_off", [((8, 300, 64, 3, 100), 0, 0), ((8, 301, 64, 3, 50), 0, 0),
+                                               ((4, 258, 32, 3, 25), 0, 0), ((8, 300, 64, 3, 128), 4, 0),
+                                               ((8, 300, 64, 3, 100), 0, 2), ((32, 8448, 64, 2, 100), 0, 0)],
+                         ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else str(v))
+def test_contraction_reference_layout_gathers_exact(mm, cuda, orc, dims, g_off, in_off):
+    """Reference layout on the register-staged fold kernel (grouped gathers): bit-exact."""
+    mt, bt, rt, nt, rt_l = dims
+    rng = np.random.default_rng(sum(dims) + 3 + g_off + in_off)
+    G = rng.integers(-4, 5, size=(rt, nt, mt, rt_l)).astype(np.float16)
+    In = rng.integers(-4, 5, size=(bt, nt, rt_l)).astype(np.float16)
+    hA = orc.pack_reference_G(G).astype(np.float64)
+    truth = (hA @ In.reshape(bt, nt * rt_l).astype(np.float64).T).reshape(mt, rt, bt).transpose(0, 2, 1)
+    Gbuf = to_dev(cuda, np.concatenate([np.zeros(g_off, np.float16), G.ravel()]))
+    Ibuf = to_dev(cuda, np.concatenate([np.zeros(in_off, np.float16), In.ravel()]))
+    Gd = Gbuf[g_off:].view(rt, nt, mt, rt_l)
+    Id = Ibuf[in_off:].view(bt, nt, rt_l)
+    Out = cuda.full((mt, bt, rt), float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(mm.contract_desc_reference(mt, bt, rt, nt, rt_l), Gd, Id, Out)
+    assert np.array_equal(Out.cpu().numpy(), truth.astype(np.float32))
+
+
 def test_contraction_reference_layout_dma_unaligned_out(mm, cuda, orc):
     """Out 4-byte but not 16-byte aligned."""
     mt, bt, rt, nt, rt_l = 8, 300, 64, 3, 128
