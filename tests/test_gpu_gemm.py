@@ -981,6 +981,26 @@ def _fold_case(rng, ext, order_a, order_b, order_c):
     return d, A, B, Cz.shape, truth.astype(np.float32)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_contraction_random_folds_lane_k_exact(mm, cuda, seed):
+    """Random 2-level folds with the K sub-index innermost in both operands and a k_lo that is a
+    multiple of 8 (so every stride is too): the direct-to-LDS fold kernel, mostly with K tiles
+    crossing k blocks and K ending inside a tile; the other sub-indices in random memory orders.
+    Integer inputs, bit-exact against an int64 einsum."""
+    rng = np.random.default_rng(2000 + seed)
+    kl = int(rng.choice([8, 16, 24, 40, 56, 72, 96, 120, 128]))
+    ext = {"mh": int(rng.integers(2, 6)), "ml": int(rng.integers(3, 70)), "nh": int(rng.integers(2, 6)),
+           "nl": int(rng.integers(3, 70)), "kh": int(rng.integers(1, 6)), "kl": kl}
+    order_a = list(rng.permutation(["mh", "ml", "kh"])) + ["kl"]
+    order_b = list(rng.permutation(["kh", "nh", "nl"])) + ["kl"]
+    order_c = list(rng.permutation(["mh", "ml", "nh", "nl"]))
+    d, A, B, cshape, truth = _fold_case(rng, ext, order_a, order_b, order_c)
+    Cd = cuda.full(cshape, float("nan"), dtype=cuda.float32, device="cuda")
+    mm.contract(d, to_dev(cuda, A), to_dev(cuda, B), Cd)
+    got = Cd.cpu().numpy()
+    assert np.array_equal(got, truth), f"{ext} {order_a} {order_b} {order_c}: {int((got != truth).sum())} mismatches"
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_contraction_random_folds_exact(mm, cuda, seed):
     """Random 2-level folds: every operand's four sub-indices in a random memory order (the generic
