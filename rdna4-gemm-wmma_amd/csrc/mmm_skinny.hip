@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <cmath>
 
 #include "mmm.h"
 #include "mmm_kernels.h"
@@ -578,9 +580,26 @@ static StreamShape stream_shape(const GemmProblem& p) {
     return {mr, strips, 0};
   const int nst_all = (p.K + 63) / 64;  // 64-deep K steps
   int splits = 256 / strips;
+  if (strips > 256) {
+    // More strips than CUs: every workgroup streams its strip piece at about the same rate
+    // (one strip's whole K, 256 bytes a row, at ~24 GB/s per CU), so s splits take
+    // ceil(strips * s / 256) rounds of 1/s of that, plus the partials' round trip and the
+    // reduction launch.  The smallest s within 3% of the best (up to 16, four K steps each,
+    // partials within the workspace): 33001 columns (258 strips) run 16 rounds of 15 splits
+    // instead of 2 rounds of whole strips, one of them nearly empty.
+    const int ws_units = (int)(kMaxWorkspaceBytes / ((size_t)16 * mr * 128 * 4));
+    const int smax = std::max(1, std::min({kMaxSplits, nst_all / 4, ws_units / strips}));
+    const double t_strip = (double)p.K * 256.0 / 24e9;
+    double best = 1e300;
+    for (int sp = 1; sp <= smax; ++sp) {
+      const double partials = sp > 1 ? (double)strips * sp * 16 * mr * 128 * 4 * 2 / 4e12 + 4e-6 : 0.0;
+      const double t = std::ceil((double)strips * sp / 256.0) / sp * t_strip + partials;
+      if (t < best * 0.97) best = t, splits = sp;
+    }
+  }
   splits = splits < kMaxSplits ? splits : kMaxSplits;
   splits = splits < nst_all / 4 ? splits : nst_all / 4;
-  if (splits > kWsTiles / strips) splits = kWsTiles / strips;
+  if (strips <= 256 && splits > kWsTiles / strips) splits = kWsTiles / strips;
   if (splits < 1) splits = 1;
   if (splits == 1 && strips < 128 && mr == 1) return {mr, strips, 0};
   return {mr, strips, splits};
@@ -603,7 +622,9 @@ bool skinny_ok(const GemmProblem& p) {
   if (p.M > kStreamMaxRows || p.M < 1) return false;
   if ((a & 1) || (b & 1)) return false;
   if ((int64_t)16 * stream_mr(p.M) * p.lda * 2 >= (int64_t)kOobOffset) return false;
-  // B offsets are taken from the strip base: the whole operand must fit a 32-bit offset
+  // B offsets are taken from the strip base: the whole operand must fit a 32-bit offset (a
+  // larger B goes to the tile kernels, whose descriptors are rebased per K tile; with per-slot
+  // descriptors here, 16 x 33001 x 66000 ran 1005 us against 915 on 64 x 64 tiles)
   if (((int64_t)p.K * p.ldb + 128) * 2 >= (int64_t)kOobOffset) return false;
   return true;
 }

@@ -1185,3 +1185,26 @@ def test_large_reference_contraction_exact(mm, cuda, case):
     finally:
         del G, In
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("shape", [(16, 33001, 8192), (16, 40000, 8192), (32, 33001, 4096), (16, 49152, 8192),
+                                   (64, 50257, 4096)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("ws", [None, False], ids=["workspace", "no_workspace"])
+def test_stream_many_strips_exact(mm, cuda, shape, ws):
+    """M <= 64 with more 128-column strips than CUs: the streaming kernel's K splits balance the
+    rounds (several rounds of split strips, then the reduction), or run unsplit without a
+    workspace.  Integer inputs, bit-exact against a device fp64 product, confined to C's view."""
+    torch = cuda
+    M, N, K = shape
+    plan = mm.gemm_plan(M, N, K)
+    assert plan["kernel"] == "stream" and plan["stream_workgroups"] > 256, plan
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(sum(shape))
+    A = _dev_ints(torch, gen, (M, K))
+    B = _dev_ints(torch, gen, (K, N))
+    Cbuf = torch.full((M, N + 8), -1.0, dtype=torch.float32, device="cuda")
+    Cv = Cbuf[:, 4:4 + N]
+    mm.gemm(A, B, Cv, workspace=ws)
+    torch.cuda.synchronize()
+    assert bool((Cbuf[:, :4] == -1.0).all()) and bool((Cbuf[:, 4 + N:] == -1.0).all()), "wrote outside the C view"
+    _assert_exact_rows(torch, A, B, Cv, f"{shape} workspace {ws is None}")
