@@ -225,7 +225,8 @@ struct GemmPlan {
 static GemmPlan plan_gemm(const GemmProblem& p) {
   if (p.M == 0 || p.N == 0) return {MMM_KERNEL_NONE, -1, 0};
   if (p.K == 0) return {MMM_KERNEL_ZERO, -1, 0};
-  if (skinny_ok(p)) return {MMM_KERNEL_STREAM, -1, 0};  // M <= 64: HBM-bound streaming kernel
+  // M <= 64: HBM-bound streaming kernel, unless its strips run better as tiles
+  if (skinny_ok(p) && !skinny_prefers_tiles(p)) return {MMM_KERNEL_STREAM, -1, 0};
   // A few rows past a whole number of 256-row tiles (4097 = 16*256 + 1) would cost a full
   // extra round of tiles; those rows go to the streaming kernel instead when that saves a round.
   const int rem = p.M % 256;
@@ -240,7 +241,8 @@ static GemmPlan plan_gemm(const GemmProblem& p) {
     pr.C = p.C + (int64_t)Mm * p.ldc;
     GemmProblem pm = p;
     pm.M = Mm;
-    if (rounds_main < rounds_full && skinny_ok(pr)) return {MMM_KERNEL_TILE_STREAM, pick_tile(pm), Mm};
+    if (rounds_main < rounds_full && skinny_ok(pr) && !skinny_prefers_tiles(pr))
+      return {MMM_KERNEL_TILE_STREAM, pick_tile(pm), Mm};
   }
   return {MMM_KERNEL_TILE, pick_tile(p), p.M};
 }

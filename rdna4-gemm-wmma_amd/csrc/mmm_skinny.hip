@@ -18,9 +18,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <algorithm>
-#include <cmath>
-
 #include "mmm.h"
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
@@ -580,32 +577,32 @@ static StreamShape stream_shape(const GemmProblem& p) {
     return {mr, strips, 0};
   const int nst_all = (p.K + 63) / 64;  // 64-deep K steps
   int splits = 256 / strips;
-  if (strips > 256) {
-    // More strips than CUs: every workgroup streams its strip piece at about the same rate
-    // (one strip's whole K, 256 bytes a row, at ~24 GB/s per CU), so s splits take
-    // ceil(strips * s / 256) rounds of 1/s of that, plus the partials' round trip and the
-    // reduction launch.  The smallest s within 3% of the best (up to 16, four K steps each,
-    // partials within the workspace): 33001 columns (258 strips) run 16 rounds of 15 splits
-    // instead of 2 rounds of whole strips, one of them nearly empty.
-    const int ws_units = (int)(kMaxWorkspaceBytes / ((size_t)16 * mr * 128 * 4));
-    const int smax = std::max(1, std::min({kMaxSplits, nst_all / 4, ws_units / strips}));
-    const double t_strip = (double)p.K * 256.0 / 24e9;
-    double best = 1e300;
-    for (int sp = 1; sp <= smax; ++sp) {
-      const double partials = sp > 1 ? (double)strips * sp * 16 * mr * 128 * 4 * 2 / 4e12 + 4e-6 : 0.0;
-      const double t = std::ceil((double)strips * sp / 256.0) / sp * t_strip + partials;
-      if (t < best * 0.97) best = t, splits = sp;
-    }
-  }
   splits = splits < kMaxSplits ? splits : kMaxSplits;
   splits = splits < nst_all / 4 ? splits : nst_all / 4;
-  if (strips <= 256 && splits > kWsTiles / strips) splits = kWsTiles / strips;
+  if (splits > kWsTiles / strips) splits = kWsTiles / strips;
   if (splits < 1) splits = 1;
   if (splits == 1 && strips < 128 && mr == 1) return {mr, strips, 0};
   return {mr, strips, splits};
 }
 
 int skinny_splits(const GemmProblem& p) { return stream_shape(p).splits; }
+
+// More 128-column strips than CUs, on B rows that are not 16-byte aligned or with rounds less than
+// 2/3 filled on average: the tile kernels run the problem faster.  Measured (B rotating through
+// HBM, auto-picked tiles against the streaming kernel): unaligned 16 x 33001 x 8192 129 us against
+// 207.6, 16 x 50257 x 4096 92.0 against 140.7, 64 x 50257 x 4096 100.3 against 155.9; aligned
+// 16 x 33000 x 8192 (258 strips) 118.1 against 140.1, 16 x 40000 x 8192 (313) 121.8 against 128.2.
+// Fuller rounds stream faster: 16 x 49152 x 8192 (384 strips) 150.4 against 172.1, 32 x 81920 x
+// 4096 (640) 134.9 against 151.0, 16 x 151936 x 4096 (1187) 204.2 against 233.3, 16 x 65536 x
+// 8192 174.4 against 186.7 (16 x 100000 x 4096, 782 strips: 184.9 streamed, 163.0 on tiles).
+bool skinny_prefers_tiles(const GemmProblem& p) {
+  const StreamShape sh = stream_shape(p);
+  if (sh.splits == 0) return false;  // the wave-split kernel
+  const int wgs = sh.strips * sh.splits;
+  if (wgs <= 256) return false;
+  const bool b_unaligned = ((uintptr_t)p.B & 15) || p.ldb % 8;
+  return b_unaligned || (double)((wgs + 255) / 256) * 256.0 / wgs > 1.5;
+}
 
 size_t skinny_workspace_bytes(const GemmProblem& p) {
   const StreamShape sh = stream_shape(p);

@@ -1187,17 +1187,18 @@ def test_large_reference_contraction_exact(mm, cuda, case):
         torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("shape", [(16, 33001, 8192), (16, 40000, 8192), (32, 33001, 4096), (16, 49152, 8192),
-                                   (64, 50257, 4096)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape,kernel", [((16, 33001, 8192), "tile"), ((16, 40000, 8192), "tile"),
+                                          ((64, 50257, 4096), "tile"), ((16, 49152, 8192), "stream"),
+                                          ((32, 81920, 4096), "stream")], ids=lambda v: "x".join(map(str, v)) if isinstance(v, tuple) else v)
 @pytest.mark.parametrize("ws", [None, False], ids=["workspace", "no_workspace"])
-def test_stream_many_strips_exact(mm, cuda, shape, ws):
-    """M <= 64 with more 128-column strips than CUs: the streaming kernel's K splits balance the
-    rounds (several rounds of split strips, then the reduction), or run unsplit without a
-    workspace.  Integer inputs, bit-exact against a device fp64 product, confined to C's view."""
+def test_skinny_many_strips_exact(mm, cuda, shape, kernel, ws):
+    """M <= 64 with more 128-column strips than CUs: unaligned B rows and thinly filled rounds on
+    the tile kernels (K splits where the planner takes them), fuller rounds streamed over several
+    rounds.  Integer inputs, bit-exact against a device fp64 product, confined to C's view."""
     torch = cuda
     M, N, K = shape
     plan = mm.gemm_plan(M, N, K)
-    assert plan["kernel"] == "stream" and plan["stream_workgroups"] > 256, plan
+    assert plan["kernel"] == kernel, plan
     gen = torch.Generator(device="cuda")
     gen.manual_seed(sum(shape))
     A = _dev_ints(torch, gen, (M, K))

@@ -262,22 +262,15 @@ def test_gemm_plan(mm):
     p = mm.gemm_plan(32, 28672, 8192)  # 224 strips fill the chip unsplit
     assert p["stream_splits"] == 1 and p["stream_workgroups"] == 224
     assert mm.gemm_plan(65, 8192, 8192)["kernel"] == "tile"
-    # more strips than CUs: K splits fill the last round (258 strips: 6 splits, 1548 workgroups,
-    # 6 rounds of 1/6 of a strip each instead of 2 whole-strip rounds, one of them nearly empty);
-    # a whole number of rounds (512 strips) stays unsplit.  Every choice keeps four K steps per
-    # split and its partials within the largest workspace.
-    p = mm.gemm_plan(16, 33001, 8192)
-    assert (p["stream_splits"], p["stream_workgroups"]) == (6, 258 * 6)
-    assert mm.gemm_plan(16, 65536, 8192)["stream_splits"] == 1
-    for M, N, K in [(16, 33001, 66000), (16, 50257, 4096), (64, 50257, 4096), (32, 151936, 4096), (16, 40000, 256),
-                    (64, 262144, 8192), (1, 33001, 1024)]:
+    # more 128-column strips than CUs: B rows that are not 16-byte aligned, or rounds less than 2/3
+    # filled on average, run on the tile kernels; fuller rounds stream unsplit
+    for (M, N, K), kernel in [((16, 33001, 8192), "tile"), ((64, 50257, 4096), "tile"), ((16, 33000, 8192), "tile"),
+                              ((16, 40000, 8192), "tile"), ((16, 49152, 8192), "stream"), ((32, 81920, 4096), "stream"),
+                              ((16, 151936, 4096), "stream"), ((16, 65536, 4096), "stream")]:
         p = mm.gemm_plan(M, N, K)
-        if p["kernel"] != "stream" or p["stream_splits"] <= 1:
-            continue
-        strips = (N + 127) // 128
-        assert p["stream_workgroups"] == strips * p["stream_splits"] and p["stream_splits"] <= 16, (M, N, K)
-        assert (K + 63) // 64 >= 4 * p["stream_splits"], (M, N, K)
-        assert 0 < p["workspace_bytes"] <= mm.MAX_WORKSPACE_BYTES, (M, N, K)
+        assert p["kernel"] == kernel, (M, N, K, p["kernel"])
+        if kernel == "stream":
+            assert p["stream_splits"] == 1 and p["stream_workgroups"] == (N + 127) // 128
     # grids too small for 128x128 tiles to fill the chip take 64x64 tiles (1024^3: 256 of them)
     p = mm.gemm_plan(1024, 1024, 1024)
     assert (p["block_m"], p["block_n"], p["wave_m"], p["wave_n"], p["tile_workgroups"]) == (64, 64, 1, 1, 256)
