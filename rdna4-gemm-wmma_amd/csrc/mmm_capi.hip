@@ -125,10 +125,7 @@ hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------- tile selection
-#ifndef MMM_PARTIAL_ROUND_BOOST
-#define MMM_PARTIAL_ROUND_BOOST 0.6
-#endif
-constexpr double kPartialRoundBoost = MMM_PARTIAL_ROUND_BOOST;
+constexpr double kPartialRoundBoost = 0.6;
 
 // Estimated time of a tile launch, in seconds: rounds of 256 concurrent workgroups (one per
 // CU) times the MFMA time of one tile's K range at the tile's relative efficiency (measured
@@ -141,31 +138,18 @@ constexpr double kPartialRoundBoost = MMM_PARTIAL_ROUND_BOOST;
 // from 1536^3) plus a fixed per-round cost (prologue, epilogue).
 // With a K split (gemm_nn_split) the split tiles' round runs K / splits, and the reduction's
 // traffic and launch are added.
-#ifndef MMM_T0_EFF
-#define MMM_T0_EFF 0.45
-#endif
-#ifndef MMM_T1_EFF
-#define MMM_T1_EFF 0.76
-#endif
-#ifndef MMM_T2_EFF
-#define MMM_T2_EFF 0.82
-#endif
-#ifndef MMM_T3_EFF
-#define MMM_T3_EFF 0.91
-#endif
+constexpr double kEff64 = 0.45, kEff128 = 0.76, kEffNarrow = 0.82, kEff192 = 0.91;
 // The 128x128 tile in an unsplit launch of one round runs its 3-stage ring (DeepTile128), faster
 // per CU than the 2-stage multi-round version the 0.76 was measured on: priced at 0.80, which
 // picks it at 512 x 8192 x 8192 (867-919 TFLOP/s against 842-876 for a 4-way K split of 64
 // 256x256 tiles, the estimate that tied at 0.76).
-#ifndef MMM_T1_DEEP_EFF
-#define MMM_T1_DEEP_EFF 0.80
-#endif
+constexpr double kEff128Deep = 0.80;
 static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
-  static const double eff_of[kTileCount] = {1.0, MMM_T2_EFF, MMM_T2_EFF, MMM_T1_EFF, MMM_T0_EFF, MMM_T3_EFF};
+  static const double eff_of[kTileCount] = {1.0, kEffNarrow, kEffNarrow, kEff128, kEff64, kEff192};
   const int bm = tile_bm(tile), bn = tile_bn(tile);
   const TileSplit sp = gemm_nn_split(p, tile);
   const double tiles = (double)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
-  const double tile_eff = tile == kTile128x128 && sp.splits <= 1 && tiles <= 256.0 ? MMM_T1_DEEP_EFF : eff_of[tile];
+  const double tile_eff = tile == kTile128x128 && sp.splits <= 1 && tiles <= 256.0 ? kEff128Deep : eff_of[tile];
   const double per_cu_flops = 4.8e12;  // sustained MFMA rate of one CU under load (256x256 at 8192^3)
   // A round with `active` of its 256 slots busy runs each CU faster: the chip is then below its
   // power cap and keeps a higher clock.  Fitted to the forced-tile times of the 23-shape sweep

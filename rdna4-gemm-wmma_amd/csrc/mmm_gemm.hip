@@ -37,50 +37,11 @@
 #include <type_traits>
 
 #include "mmm.h"
+#include "mmm_dma.h"
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
 
-#ifndef MMM_XINTERLEAVE
-#define MMM_XINTERLEAVE 1  // interleave the steady-state refill loads with the last K-step's MFMAs
-#endif
-// Count a round as 256 x (the tile's workgroups per CU) when deciding a K split (measured:
-// 3072^3 -5.5%, 1536^2 x 12288 -5%, 2304^2 x 8192 -2% against 256 per round).
-#ifndef MMM_SPLIT_OCC
-#define MMM_SPLIT_OCC 0
-#endif
-// MFMAs between two refill loads in the steady-state step; 0 spreads the loads evenly over
-// the step's MFMAs (stride = MFMAs / loads, at least 1).  All eight waves refill in the same
-// K-step, and every load is a 1 KB request to the address unit, so a burst of loads fills its
-// queue and stalls each wave's MFMAs behind its next load.  Measured on the 256x256 tile
-// (32 MFMAs, 8 loads): stride 1 1258 TFLOP/s at 8192^3, stride 2 within 1%, 3 +1%, 4 +4.4%.
-#ifndef MMM_DMA_STRIDE
-#define MMM_DMA_STRIDE 0
-#endif
-#ifndef MMM_SPREAD_BODY
-#define MMM_SPREAD_BODY 1  // spread each K-step's next-step fragment reads over its MFMAs
-#endif
-#ifndef MMM_SPREAD_READS
-#define MMM_SPREAD_READS 1  // spread the next tile's first fragment reads over the last K-step's MFMAs
-#endif
-#ifndef MMM_PIN_BODY
-#define MMM_PIN_BODY 1  // keep a tile's body MFMAs ahead of the next tile's load wait and barrier
-#endif
-
 namespace mmm {
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-#define LDS_AS __attribute__((address_space(3)))
-
-// Buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format, no swizzle).
-constexpr int kRsrcWord3 = 0x00020000;
-// Byte offset used for masked-off chunks; every descriptor's range is clipped below it.
-constexpr uint32_t kOobOffset = 0x7ffffff0u;
 
 // Block tile BM x BN, K step BK (32 or 64), WGM x WGN waves, STAGES-deep LDS ring, OCC
 // workgroups per CU targeted by the launch bounds (OCC > 1 caps registers accordingly), MFMA
@@ -169,52 +130,6 @@ __device__ __forceinline__ half8 lds_read_b_tr(const char LDS_AS* p_lo, const ch
   return __builtin_shufflevector(l4, h4, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor (base, num_records bytes, word 3) built from uniform values.
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t num_records) {
-  const uint64_t b = (uint64_t)(uintptr_t)base;
-  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)b), __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
-               __builtin_amdgcn_readfirstlane((int)num_records), kRsrcWord3};
-}
-
-// 16 bytes per lane from the buffer at byte offset voff straight into LDS at
-// lds_addr + 16 * lane (buffer_load_dwordx4 ... lds; m0 holds the wave's LDS base).
-// Issued as inline asm so the compiler does not treat every later LDS read as dependent on
-// it: completion is awaited explicitly (vmcnt(0)) before the barrier that publishes the
-// stage.  Out-of-range offsets (>= num_records) write zeros.  DS instructions on gfx9-family
-// targets do not read m0, so overwriting it here is safe.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma_b128(uint32_t lds_addr, i32x4 rsrc, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-
-// The same 16 bytes per lane from a 64-bit global address (global_load_lds_dwordx4, gfx950),
-// for operands whose per-lane offsets do not fit a buffer's 32 bits.  No range check: the
-// caller passes addresses inside the operand.
-__device__ __forceinline__ void dma_b128_flat(uint32_t lds_addr, const void* src) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :
-               : "s"(lds_addr), "v"(src)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// Wait until at most N of this wave's vector-memory operations are outstanding (they
-// complete in issue order), i.e. all but the N most recent DMA loads have landed in LDS.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt range");
-#if defined(__HIP_DEVICE_COMPILE__)  // the host pass checks "I" against its own (narrower) range
-  asm volatile("s_waitcnt vmcnt(%0)" ::"I"(N) : "memory");
-#endif
-}
-__device__ __forceinline__ void wait_dma() { wait_vmcnt<0>(); }
-
 // Wait until at most n tiles of LPT loads each are still in flight (0 <= n <= NMAX; n is
 // wave-uniform, the branch is scalar).
 template <int LPT, int NMAX>
@@ -228,14 +143,6 @@ __device__ __forceinline__ void wait_tiles(int n) {
     else
       wait_tiles<LPT, NMAX - 1>(n);
   }
-}
-
-__device__ __forceinline__ uint32_t lds_addr_of(const char LDS_AS* p) { return (uint32_t)(uintptr_t)p; }
-
-// A buffer descriptor's record count for `bytes` readable bytes: 0 if none, at most kOobOffset.
-__device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
-  if (bytes <= 0) return 0u;
-  return bytes > (int64_t)kOobOffset ? kOobOffset : (uint32_t)bytes;
 }
 
 // One pass over an LDS stage: KSTEPS K-steps of FM x FN MFMAs.  `after_first_reads` runs
@@ -292,29 +199,20 @@ __device__ __forceinline__ void mfma_one(const half8& b, const half8& a, AccT<T>
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(b, a, acc, 0, 0, 0);
 }
 
-// Issue order of a K-step's FM x FN MFMAs: MFMA i updates accumulator (ord_mb(i), ord_nb(i)).
-// Each accumulator still sees its K-steps in order, so the order does not change any result.
-// MMM_MFMA_ORDER 0: row-major (A fragment held over FN MFMAs); 1: column-major (B fragment held
-// over FM MFMAs); 2 / 3: the same, snaking, so consecutive rows (columns) share the fragment at
-// the turn as well.  Under sustained load the MI355X runs at its power cap, and fewer operand
-// changes between consecutive MFMAs cost less power: at 8192^3 (interleaved runs, bit-identical
-// results) order 2 ran 1363 TFLOP/s against 1354 for orders 0 and 1 and 1359 for order 3.
-#ifndef MMM_MFMA_ORDER
-#define MMM_MFMA_ORDER 2
-#endif
+// Issue order of a K-step's FM x FN MFMAs: MFMA i updates accumulator (ord_mb(i), ord_nb(i)),
+// row by row with the column order reversed on every other row (a snake), so consecutive MFMAs
+// share an operand at the turns too.  Each accumulator still sees its K-steps in order, so the
+// order does not change any result.  Under sustained load the MI355X runs at its power cap, and
+// fewer operand changes between consecutive MFMAs cost less power: at 8192^3 (interleaved runs,
+// bit-identical results) the snake ran 1363 TFLOP/s against 1354 for plain row-major or
+// column-major order and 1359 for a column snake.
 template <class T>
 __host__ __device__ constexpr int ord_mb(int i) {
-  if constexpr (MMM_MFMA_ORDER == 0) return i / T::FN;
-  else if constexpr (MMM_MFMA_ORDER == 1) return i % T::FM;
-  else if constexpr (MMM_MFMA_ORDER == 2) return i / T::FN;
-  else return ((i / T::FM) & 1) ? T::FM - 1 - i % T::FM : i % T::FM;
+  return i / T::FN;
 }
 template <class T>
 __host__ __device__ constexpr int ord_nb(int i) {
-  if constexpr (MMM_MFMA_ORDER == 0) return i % T::FN;
-  else if constexpr (MMM_MFMA_ORDER == 1) return i / T::FM;
-  else if constexpr (MMM_MFMA_ORDER == 2) return ((i / T::FN) & 1) ? T::FN - 1 - i % T::FN : i % T::FN;
-  else return i / T::FM;
+  return ((i / T::FN) & 1) ? T::FN - 1 - i % T::FN : i % T::FN;
 }
 
 template <class T>
@@ -349,15 +247,12 @@ __device__ __forceinline__ void block_sync() { __syncthreads(); }
 // (rows r and r + 8) trade their block-(nb+1) values (one DPP move per register), after which
 // one store writes rows 0-7 and the next rows 8-15, each row 32 columns: one 128-byte line (the
 // 192x192 tile's odd third block of a row stays half lines).  gemm_nn_kernel stores its interior
-// tiles this way with every store policy; the persistent kernels with non-temporal stores only
-// (MMM_C_LINES 2; 1: with plain stores too, 0: nowhere).  Measured on MI355X (interleaved runs,
+// tiles this way with every store policy; the persistent kernels with non-temporal stores only.
+// Measured on MI355X (interleaved runs,
 // same box, exact results), against half lines: 8192^3 +0.6-0.9%, 12288^2 x 4096 +1.4%,
 // 16384^2 x 4096 +1.0%, 8192 x 2048 x 2048 +1.4%, 4096^3 +0.8%, 6144^3 +0.4%; with plain
 // (L2-allocating) stores the persistent grids lost up to 2% at short K (8192^2 x 2048 -1.6%,
 // 16384 x 8192 x 1024 -2.0%).
-#ifndef MMM_C_LINES
-#define MMM_C_LINES 2
-#endif
 enum CStore { kStorePlain = 0, kStoreNonTemporal = 1, kStoreWriteThrough = 2 };
 
 // System-scope write-through 16-byte store (sc0 sc1), as inline asm.  The compiler does not see
@@ -398,7 +293,7 @@ __device__ __forceinline__ int lane_id_fresh() {
 
 template <class T>
 constexpr bool c_lines_ok() {
-  return MMM_C_LINES != 0 && T::MF == 16 && T::FN >= 2;
+  return T::MF == 16 && T::FN >= 2;
 }
 // every store of the tile a whole line (an even number of blocks per row)
 template <class T>
@@ -407,7 +302,7 @@ constexpr bool c_lines_all() {
 }
 template <class T, int POLICY>
 constexpr bool use_c_lines() {
-  return c_lines_ok<T>() && (MMM_C_LINES == 1 || POLICY != kStorePlain);
+  return c_lines_ok<T>() && POLICY != kStorePlain;
 }
 
 // The wave's whole TM x TN accumulator tile to C at `c` (the wave tile's first element; rows
@@ -464,11 +359,6 @@ template <class T, bool BKM, int NST = 0, class Prep, class DmaOne, class IssueT
 __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool tail_regs, const uint32_t (&a_off)[4],
                                             const uint32_t (&b_off)[4], AccT<T> (&acc)[T::FM][T::FN], Prep&& prep,
                                             DmaOne&& dma_one, IssueTile&& issue_tile, int pre = 0) {
-  auto issue = [&](int t, int stage) {
-    const auto d = prep(t, stage);
-#pragma unroll
-    for (int j = 0; j < T::LPT; ++j) dma_one(d, j);
-  };
   // Ring of S slots, tile u in slot u % S.  Cross-stage pipeline: during the last K-step of
   // tile t, this wave waits for its own loads of tile t+1, then the barrier (a) publishes
   // tile t+1 -- every wave's loads of it have landed -- and (b) retires slot t % S: every
@@ -498,27 +388,19 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
     const char LDS_AS* st = lds_base + cur * T::STAGE;
 #pragma unroll
     for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
-      if constexpr (MMM_SPREAD_BODY) {
-        // MFMA i of this step carries fragment read i of the next
+      // MFMA i of this step carries fragment read i of the next
 #pragma unroll
-        for (int i = 0; i < T::FM * T::FN; ++i) {
-          mfma_one<T>(f[kk & 1].b[ord_nb<T>(i)], f[kk & 1].a[ord_mb<T>(i)], acc[ord_mb<T>(i)][ord_nb<T>(i)]);
-          if (i < T::FM + T::FN) load_frag_unit<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, i, f[(kk + 1) & 1]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      } else {
-        load_frags<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, f[(kk + 1) & 1]);
-        mfma_frags<T>(f[kk & 1], acc);
-        // keep the next step's LDS reads ahead of this step's MFMAs
-        __builtin_amdgcn_sched_group_barrier(0x100, T::FM + 2 * T::FN, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, T::FM * T::FN, 0);
+      for (int i = 0; i < T::FM * T::FN; ++i) {
+        mfma_one<T>(f[kk & 1].b[ord_nb<T>(i)], f[kk & 1].a[ord_mb<T>(i)], acc[ord_mb<T>(i)][ord_nb<T>(i)]);
+        if (i < T::FM + T::FN) load_frag_unit<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, i, f[(kk + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
   // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
   // retired slot (`refill` loads tile t+S into slot `cur`), then the MFMAs.
   auto tile_next = [&](int t, auto&& refill) {
-    if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
+    __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
     const int issued = t + S < KT ? t + S : KT;  // tiles 0 .. issued-1 are issued
     int ahead = issued - (t + 2);                // of those, after t+1 (may stay in flight)
     if (tail_regs && issued == KT && ahead > 0) --ahead;
@@ -534,19 +416,22 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
   // Steady state: after the barrier the next tile's first fragment reads and the refill's
   // loads are interleaved with the last K-step's MFMAs (scheduling fences keep the order), so
   // neither a burst of LDS reads nor a burst of load issue leaves the matrix pipe idle.
-  // MFMA i carries fragment read i (i < FM + FN) when MMM_SPREAD_READS is set, and the DMA
-  // loads go on the MFMAs after the reads when there are enough of them.
+  // MFMA i carries fragment read i (i < FM + FN), and the DMA loads go on the MFMAs after the
+  // reads when there are enough of them, spread evenly: all waves refill in the same K-step and
+  // every load is a 1 KB request to the address unit, so a burst of them fills its queue and
+  // stalls each wave's MFMAs behind its next load.  Measured on the 256x256 tile (32 MFMAs, 8
+  // loads) at 8192^3: one load every MFMA 1258 TFLOP/s, every 2 within 1%, every 3 +1%, every 4
+  // (the even spread) +4.4%.
   auto tile_next_interleaved = [&](int t) {
-    if constexpr (MMM_PIN_BODY) __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
+    __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
     wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(S - 2);  // steady state: S-2 tiles after t+1 in flight
     block_sync();
     const int nslot = cur + 1 == S ? 0 : cur + 1;
     const char LDS_AS* ns = lds_base + nslot * T::STAGE;
-    constexpr int NM = T::FM * T::FN, NU = MMM_SPREAD_READS ? T::FM + T::FN : 0;
+    constexpr int NM = T::FM * T::FN, NU = T::FM + T::FN;
     constexpr int NL = T::LPT;
-    constexpr int DS = MMM_DMA_STRIDE > 0 ? MMM_DMA_STRIDE : (NM / NL > 1 ? NM / NL : 1);  // MFMAs between loads
+    constexpr int DS = NM / NL > 1 ? NM / NL : 1;  // MFMAs between loads
     constexpr int D0 = NM - DS * NL >= NU ? NU : (NM > DS * NL ? NM - DS * NL : 0);
-    if constexpr (!MMM_SPREAD_READS) load_frags<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
     const auto d = prep(t + S, cur);
     int issued = 0;
 #pragma unroll
@@ -567,10 +452,7 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
   int t = 0;
   for (; t + S < KT - 1; ++t) {
     tile_body();
-    if constexpr (MMM_XINTERLEAVE)
-      tile_next_interleaved(t);
-    else
-      tile_next(t, [&] { issue(t + S, cur); });
+    tile_next_interleaved(t);
   }
   if (t + S == KT - 1) {
     tile_body();
@@ -1797,25 +1679,12 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
 // at 8192^3 (median TFLOP/s): 64 x 2 stages with 2 x 4 waves (two waves per SIMD, so one
 // wave's MFMAs cover the other's barrier and LDS waits) 1126; the same with 2 x 2 waves
 // 1077; 32 x 4 or 32 x 5 stages 1055-1106 -- deeper prefetch does not pay, latency of the
-// operand fetch is not the limiter.
-#ifndef MMM_DMA_BK
-#define MMM_DMA_BK 64
-#endif
-#ifndef MMM_DMA_STAGES
-#define MMM_DMA_STAGES 2
-#endif
-#ifndef MMM_DMA_WGM
-#define MMM_DMA_WGM 2
-#endif
-#ifndef MMM_DMA_WGN
-#define MMM_DMA_WGN 4
-#endif
-// MFMA shape of the 256x256 tile (measured at 8192^3 under sustained load: 16x16x32 runs at a
-// 16% higher power-limited clock than 32x32x16 -- a quarter of the accumulator traffic per
-// instruction -- and is 2-9% faster across 4096^3 .. 16384^2 x 4096)
-#ifndef MMM_DMA_MF
-#define MMM_DMA_MF 16
-#endif
+// operand fetch is not the limiter.  MFMA shape of the 256x256 tile: 16x16x32 (measured at
+// 8192^3 under sustained load, it runs at a 16% higher power-limited clock than 32x32x16 -- a
+// quarter of the accumulator traffic per instruction -- and is 2-9% faster across 4096^3 ..
+// 16384^2 x 4096).
+constexpr int kDmaBK = 64;
+using Tile256 = Tile<256, 256, 2, 4, kDmaBK, 2, 1, 16>;
 // The 128-wide tiles run eight 16x16x32 waves (two per SIMD) like the 256x256 tile.  Measured on
 // MI355X against the four-wave 32x32x16 versions they replace (interleaved runs, same box):
 //   128x256 (2 x 4 waves of 64x64, 3 x 48 KB ring): 2048 x 4096 x 4096 858 -> 939 TFLOP/s,
@@ -1837,12 +1706,9 @@ struct DmaCfg {  // 128x128
 // TFLOP/s, 512^3 23.8 -> 30.4, 768^3 67 -> 96, 1024^2 x 2048 207 -> 297; it loses where 128x128
 // tiles fill a round or split well (1536^3 333 vs 365, 2048^3 515 vs 640).  8 stages (K = 512
 // in flight at once) ran 3-7% slower than 3 or 4; two workgroups per CU at 2 stages, slower still.
-#ifndef MMM_T0_STAGES
-#define MMM_T0_STAGES 3
-#endif
 template <>
 struct DmaCfg<64, 64> {
-  using T = Tile<64, 64, 2, 2, 64, MMM_T0_STAGES, 1, 16>;
+  using T = Tile<64, 64, 2, 2, 64, 3, 1, 16>;
 };
 // 192x192: 16 x 16 tiles fill one round exactly at 3072 x 3072, where 256x256 tiles leave 112
 // of the 256 CUs idle, and whole multiples of 256 tiles run as the persistent grid (6144^2 x
@@ -1858,7 +1724,7 @@ struct DmaCfg<192, 192> {
 };
 template <>
 struct DmaCfg<256, 256> {
-  using T = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1, MMM_DMA_MF>;
+  using T = Tile256;
 };
 template <>
 struct DmaCfg<256, 128> {
@@ -1878,10 +1744,7 @@ using DmaTile = typename DmaCfg<BM, BN>::T;
 // 4096 760 -> 822, 1024^2 x 8192 538 -> 564, 512 x 8192 x 8192 783 -> 852.
 using DeepTile128 = Tile<128, 128, 2, 4, 64, 3, 1, 16>;
 // The folded direct-to-LDS kernel: the 256x256 tile's waves and ring.
-#ifndef MMM_FOLD_MF
-#define MMM_FOLD_MF 16
-#endif
-using FoldDmaTile = Tile<256, 256, MMM_DMA_WGM, MMM_DMA_WGN, MMM_DMA_BK, MMM_DMA_STAGES, 1, MMM_FOLD_MF>;
+using FoldDmaTile = Tile256;
 // Register-staged path: 64-deep stages, double-buffered.
 template <int BM, int BN>
 using RegTile = Tile<BM, BN, 2, 2, 64, 2>;
@@ -1897,7 +1760,7 @@ static bool dma_ok(const GemmProblem& p, int bm) {
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   if ((a & 1) || (b & 1)) return false;
   if ((int64_t)bm * p.lda * 2 >= (int64_t)kOobOffset) return false;
-  if ((int64_t)MMM_DMA_BK * p.ldb * 2 >= (int64_t)kOobOffset) return false;
+  if ((int64_t)kDmaBK * p.ldb * 2 >= (int64_t)kOobOffset) return false;
   return true;
 }
 
@@ -1922,9 +1785,9 @@ TileSplit gemm_nn_split(const GemmProblem& p, int tile_id) {
   if (!gemm_nn_direct_to_lds(p, tile_id)) return {1, 0};
   const int bm = tile_bm(tile_id), bn = tile_bn(tile_id);
   const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
-  // workgroups one round holds: one per CU, times the tile's workgroups per CU when counted
-  const int occ = MMM_SPLIT_OCC ? (tile_id == kTile128x128 ? 2 : 1) : 1;
-  const int64_t slots = 256 * occ;
+  // A round counts one workgroup per CU for every tile (counting the 128x128 tile's two per CU
+  // measured 3072^3 -5.5%, 1536^2 x 12288 -5%, 2304^2 x 8192 -2%).
+  const int64_t slots = 256;
   const int64_t last = tiles - (tiles - 1) / slots * slots;  // tiles in the last round (1 .. slots)
   if (last * 2 >= slots) return {1, 0};
   const int kt = (p.K + 63) / 64;  // 64-deep K tiles (the 32-deep tiles have twice as many)
@@ -1958,12 +1821,6 @@ size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id) {
 // split) over more than one round of 256 workgroups, aligned operands (no gathered K tile),
 // 4-byte-aligned C, and at least S + 1 K tiles.  Measured against one workgroup per tile (same
 // box): 8192^3 +1%, 8192^2 x 2048 +3.7%, 16384 x 8192 x 1024 +3.8%; 192x192 at 6144^2 x 2048 +4%.
-#ifndef MMM_PERSIST
-#define MMM_PERSIST 1
-#endif
-#ifndef MMM_PERSIST_192
-#define MMM_PERSIST_192 1
-#endif
 template <class TP = DmaTile<256, 256>>
 static bool persistent_ok(const GemmProblem& p) {
   if (!dma_ok(p, TP::BM) || p.tail_regs || !p.c_vec4) return false;
@@ -1979,12 +1836,12 @@ static int64_t launch_blocks(const GemmProblem& p, int bm, int bn) {
 }
 
 bool gemm_nn_persistent(const GemmProblem& p0, int tile_id) {
-  if (!MMM_PERSIST || (tile_id != kTile256x256 && tile_id != kTile192x192)) return false;
+  if (tile_id != kTile256x256 && tile_id != kTile192x192) return false;
   GemmProblem p = p0;
   p.c_vec4 = (uintptr_t)p.C % 4 == 0;
   p.tail_regs = !tail_aligned(p);
   p.k_splits = gemm_nn_split(p, tile_id).splits;
-  if (tile_id == kTile192x192) return MMM_PERSIST_192 && p.k_splits <= 1 && persistent_ok<DmaTile<192, 192>>(p);
+  if (tile_id == kTile192x192) return p.k_splits <= 1 && persistent_ok<DmaTile<192, 192>>(p);
   return persistent_ok(p);
 }
 
@@ -2001,7 +1858,7 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
     p.k_splits = sp.splits, p.split_tiles = sp.tiles, p.partials = p.ws;  // else unsplit
   switch (tile_id) {
     case kTile256x256:
-      if (MMM_PERSIST && persistent_ok(p)) {
+      if (persistent_ok(p)) {
         using TP = DmaTile<256, 256>;
         // Non-temporal C stores: the persistent grid stores a tile's C while its next tile's
         // operand loads run, and L2-allocating stores would evict the operand panels other
@@ -2053,7 +1910,7 @@ hipError_t launch_gemm_nn(const GemmProblem& p0, int tile_id, hipStream_t stream
     case kTile64x64:
       return dma_ok(p, 64) ? launch_nn<DmaTile<64, 64>, false>(p, stream) : launch_nn<RegTile<64, 64>, true>(p, stream);
     case kTile192x192:
-      if (MMM_PERSIST && MMM_PERSIST_192 && p.k_splits <= 1 && persistent_ok<DmaTile<192, 192>>(p)) {
+      if (p.k_splits <= 1 && persistent_ok<DmaTile<192, 192>>(p)) {
         using TP = DmaTile<192, 192>;
         const int tiles_m = p.M / TP::BM, tiles_n = p.N / TP::BN;
         // non-temporal C as for the 256x256 tile; this tile's third block of a row is stored as

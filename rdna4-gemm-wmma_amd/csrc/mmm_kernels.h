@@ -52,10 +52,7 @@ constexpr int tile_bn(int tile) {
 // with C written by the reduction), as the tile planner prices it.  The partials of an
 // under-filled round (tens of MB) are read back from the 256 MB Infinity Cache: fitted to the
 // measured times of split launches on MI355X (2304^2 x 8192 on 256x256 tiles: 90 us measured).
-#ifndef MMM_SPLIT_TRAFFIC_BPS
-#define MMM_SPLIT_TRAFFIC_BPS 10e12
-#endif
-constexpr double kSplitTrafficBps = MMM_SPLIT_TRAFFIC_BPS;
+constexpr double kSplitTrafficBps = 10e12;
 
 hipError_t launch_gemm_nn(const GemmProblem& p, int tile_id, hipStream_t stream);
 bool gemm_nn_direct_to_lds(const GemmProblem& p, int tile_id);  // else the register-staged path
@@ -75,10 +72,7 @@ size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id);
 constexpr size_t kMaxWorkspaceBytes = (size_t)64 << 20;
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
 // Rows of C up to which the streaming kernels take a GEMM (the kernels handle up to 64).
-#ifndef MMM_STREAM_MAX_ROWS
-#define MMM_STREAM_MAX_ROWS 64
-#endif
-constexpr int kStreamMaxRows = MMM_STREAM_MAX_ROWS;
+constexpr int kStreamMaxRows = 64;
 static_assert(kStreamMaxRows >= 16 && kStreamMaxRows <= 64, "streaming kernels take 16 to 64 rows");
 bool skinny_ok(const GemmProblem& p);  // M <= kStreamMaxRows and operands within 32-bit offsets
 hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "mmm.h"
+#include "mmm_dma.h"
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
 
@@ -13,10 +14,6 @@ namespace mmm {
 
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 // One wave reads the shader-clock counter (s_memtime, one count per shader clock) and the
 // constant-rate real-time counter (s_memrealtime, 100 MHz), spins until `ticks` real-time
@@ -137,25 +134,18 @@ __global__ __launch_bounds__(256) void read_lds_ceiling_kernel(const void* src, 
   __shared__ __attribute__((aligned(1024))) char ring[4 * 8 * 1024];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-  const uint64_t b = (uint64_t)(uintptr_t)src;
-  const i32x4 rsrc = {__builtin_amdgcn_readfirstlane((int)(uint32_t)b), __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
-                      __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+  const i32x4 rsrc = make_rsrc(src, bytes);
   const uint32_t waves = gridDim.x * 4, wid = blockIdx.x * 4 + w;
   const uint32_t pieces = bytes / 1024;
   const uint32_t ring_base = (uint32_t)(uintptr_t)(ring + w * 8 * 1024);
   int slot = 0;
   for (uint32_t piece = wid; piece < pieces; piece += waves) {
     const uint32_t voff = piece * 1024 + lane * 16;
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds\n\ts_waitcnt vmcnt(7)"
-                 :
-                 : "s"(ring_base + slot * 1024), "v"(voff), "s"(rsrc)
-                 : "memory", "m0");
-#pragma clang diagnostic pop
+    dma_b128_nt(ring_base + slot * 1024, rsrc, voff);
+    wait_vmcnt<7>();
     slot = (slot + 1) & 7;
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  wait_vmcnt<0>();
   __syncthreads();
   if (threadIdx.x == 0) out[blockIdx.x] = *(volatile uint32_t*)ring;
 }

@@ -19,6 +19,7 @@
 #include <stdint.h>
 
 #include "mmm.h"
+#include "mmm_dma.h"
 #include "mmm_kernels.h"
 #include "mmm_tile_map.h"
 
@@ -26,26 +27,9 @@ namespace mmm {
 
 namespace {
 
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef __fp16 fp16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-#define LDS_AS __attribute__((address_space(3)))
-
-#ifndef MMM_SKINNY_NS
-#define MMM_SKINNY_NS 32
-#endif
-#ifndef MMM_SKINNY_KS
-#define MMM_SKINNY_KS 64
-#endif
-#ifndef MMM_SKINNY_SLOTS
-#define MMM_SKINNY_SLOTS 6
-#endif
-constexpr int kNS = MMM_SKINNY_NS;        // columns per workgroup
-constexpr int kKS = MMM_SKINNY_KS;        // K rows per ring slot
-constexpr int kSlots = MMM_SKINNY_SLOTS;  // ring slots per wave
+constexpr int kNS = 32;     // columns per workgroup
+constexpr int kKS = 64;     // K rows per ring slot
+constexpr int kSlots = 6;   // ring slots per wave
 constexpr int kWaves = 4;
 constexpr int kABytes = 16 * kKS * 2;   // A [16][KS]
 constexpr int kBBytes = kKS * kNS * 2;  // B [KS][NS]
@@ -55,47 +39,7 @@ constexpr int kNT = kNS / 16;           // 16-column MFMA tiles per strip
 constexpr int kCPR = kNS / 8;           // 16-byte chunks per B row
 static_assert(kKS == 32 || kKS == 64, "K rows per slot");
 static_assert(kNS == 32 || kNS == 64, "strip width");
-constexpr int kRsrcWord3 = 0x00020000;
-constexpr uint32_t kOobOffset = 0x7ffffff0u;
 static_assert(kWaves * kSlots * kSlot <= 160 * 1024, "rings must fit the LDS");
-
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t num_records) {
-  const uint64_t b = (uint64_t)(uintptr_t)base;
-  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)b), __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
-               __builtin_amdgcn_readfirstlane((int)num_records), kRsrcWord3};
-}
-
-__device__ __forceinline__ uint32_t clip_records(int64_t bytes) {
-  if (bytes <= 0) return 0u;
-  return bytes > (int64_t)kOobOffset ? kOobOffset : (uint32_t)bytes;
-}
-
-// buffer_load_dwordx4 ... lds: 16 bytes per lane into LDS at lds_addr + 16*lane.  Issued as
-// inline asm so the compiler does not serialise later LDS reads behind it; completion is
-// awaited explicitly.  DS instructions on gfx9-family targets do not read m0.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma_b128(uint32_t lds_addr, i32x4 rsrc, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-// The same load with the non-temporal policy, for a B operand streamed once from HBM: its lines
-// are not kept in the caches for reuse, so the stream does not evict what the next lines need.
-__device__ __forceinline__ void dma_b128_nt(uint32_t lds_addr, i32x4 rsrc, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"I"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // A-slot swizzle: 16 rows at one logical chunk land in 16 distinct 16-byte bank groups.
 // Rows of 128 B (KS = 64): chunk ^ ((row >> 1) & 7).  Rows of 64 B (KS = 32): four rows
