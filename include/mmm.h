@@ -14,7 +14,10 @@
  * Conventions (all entry points):
  *  - fp16 tensors are passed as pointers to IEEE binary16 bit patterns (mmm_half).
  *  - Pointers are device pointers owned by the caller.  No entry point synchronises the host,
- *    exits the process or allocates memory.  Launches that would leave most of the chip idle
+ *    exits the process or allocates memory at call time.  Loading the library does reserve
+ *    memory: a 64 MiB device array (the K-split partials of mmm_gemm_f16f32_noalloc) on every
+ *    GPU the process uses the library on, held until the process ends, whether or not that
+ *    entry point is ever called.  Launches that would leave most of the chip idle
  *    split K across workgroups and sum the partials in a fixed order; the partials go to a
  *    workspace the caller passes to the _ws entry points (size from mmm_gemm_workspace_f16f32
  *    or mmm_contract5d_workspace_f16f32, at most 64 MiB).  Without one (the entry points
@@ -27,9 +30,11 @@
  *    M == 0 or N == 0 is a no-op; K == 0 writes zeros to C.
  *  - Work is enqueued on `stream` (0 = the null stream, as the reference) and is
  *    asynchronous, as the reference's launches are (the caller synchronises, mmm.cpp:1491).
- *  - Thread safety: the library has no mutable global state.  A workspace serves one call at
- *    a time: calls on one stream may share one (they are ordered); concurrent calls on
- *    different streams need their own.
+ *  - Thread safety: the only mutable global state is mmm_gemm_f16f32_noalloc's: its 64 MiB
+ *    device array (shared by every call of that entry point on one GPU) and a mutex-guarded
+ *    table of the array's device address per GPU, filled on the first call on each GPU.  A
+ *    workspace serves one call at a time: calls on one stream may share one (they are
+ *    ordered); concurrent calls on different streams need their own.
  */
 #ifndef MMM_H
 #define MMM_H
@@ -89,7 +94,9 @@ hipError_t mmm_gemm_f16f32_clocked(const mmm_half* A, const mmm_half* B, float* 
  * Results equal mmm_gemm_f16f32_ws's with a workspace of at least mmm_gemm_workspace_f16f32
  * bytes.  Returns hipErrorInvalidValue where mmm_gemm_f16f32_ws would, and when a planned split
  * needs more than the array holds (not reached by the planner's 64 MiB limit).  Every call on one
- * GPU shares its array: calls that overlap on one GPU (different streams) race on it.
+ * GPU shares its array: calls that overlap on one GPU (different streams) race on it.  The
+ * looked-up address is kept for the life of the process: after hipDeviceReset (which frees the
+ * device's copy of the array) this entry point must not be called on that device again.
  */
 hipError_t mmm_gemm_f16f32_noalloc(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
                                    int64_t lda, int64_t ldb, int64_t ldc, hipStream_t stream);

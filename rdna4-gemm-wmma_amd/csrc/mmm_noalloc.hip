@@ -8,7 +8,8 @@
 // array's own name to a kernel.  Every call on one GPU shares that GPU's array: the split kernels
 // overwrite every partial the reduction reads, so nothing needs clearing between calls, but calls
 // that overlap on one GPU (different streams, or graph replays concurrent with eager calls) race
-// on it.
+// on it.  The kept address is not looked up again: hipDeviceReset frees the device's copy, and
+// calls on that device afterwards would hand the kernels a stale address.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
