@@ -151,6 +151,62 @@ def test_refkernel_blocking_differs_from_naive(orc):
     assert not np.array_equal(orc.gemm_naive_f32(A, B), orc.gemm_refkernel_f32(A, B))
 
 
+def _np_naive_f32(A, B):
+    """GEMM_Naive's order (mmm.cpp:57-58) in numpy float32: one running sum per output, k
+    ascending, every addition rounded to fp32 (the fp16 x fp16 products are exact in fp32)."""
+    a, b = A.astype(np.float32), B.astype(np.float32)
+    acc = np.zeros((A.shape[0], B.shape[1]), dtype=np.float32)
+    for k in range(A.shape[1]):
+        acc = acc + np.outer(a[:, k], b[k]).astype(np.float32)
+    return acc
+
+
+def _np_refkernel_f32(A, B, tile=32, step=16):
+    """WMMA_Swizzled_Full's order (mmm.cpp:1309-1356) in numpy float32: K walked in 32-deep
+    LDS tiles of two 16-deep WMMA steps; each step's 16 products are summed in ascending k
+    from zero, then added to the accumulator; past K the operands are zero (mmmTensor.cpp:137-175)."""
+    M, K = A.shape
+    N = B.shape[1]
+    kp = -(-K // tile) * tile
+    a = np.zeros((M, kp), dtype=np.float32)
+    b = np.zeros((kp, N), dtype=np.float32)
+    a[:, :K], b[:K] = A, B
+    acc = np.zeros((M, N), dtype=np.float32)
+    for k0 in range(0, kp, step):
+        s = np.zeros((M, N), dtype=np.float32)
+        for k in range(k0, k0 + step):
+            s = s + np.outer(a[:, k], b[k]).astype(np.float32)
+        acc = acc + s
+    return acc
+
+
+def test_fp32_orders_match_numpy_restatements(orc):
+    """Both fp32 restatements reproduce, bit for bit on non-integer inputs (where the order of
+    the additions decides the rounding), an independent float32 restatement of their order:
+    the naive running sum and the reference kernel's 16-deep steps (K 203, so the last 32-deep
+    tile is partly past K)."""
+    A = orc.uniform_f16((9, 203), 11, 0)
+    B = orc.uniform_f16((203, 7), 11, 1)
+    assert np.array_equal(orc.gemm_naive_f32(A, B).view(np.uint32), _np_naive_f32(A, B).view(np.uint32))
+    assert np.array_equal(orc.gemm_refkernel_f32(A, B).view(np.uint32), _np_refkernel_f32(A, B).view(np.uint32))
+    # the TN layout of the reference's tensor kernel walks K the same way
+    Bt = np.ascontiguousarray(B.T)
+    assert np.array_equal(orc.gemm_refkernel_f32(A, Bt, b_layout="nk").view(np.uint32),
+                          _np_refkernel_f32(A, B).view(np.uint32))
+
+
+def test_fp32_order_checks_catch_wrong_orders(orc):
+    """The numpy restatements tell plausible mistakes apart: K blocked by 8 instead of 16,
+    and a running sum without the 16-deep steps, both give other bits on these inputs."""
+    A = orc.uniform_f16((9, 203), 11, 0)
+    B = orc.uniform_f16((203, 7), 11, 1)
+    ref = orc.gemm_refkernel_f32(A, B).view(np.uint32)
+    assert not np.array_equal(ref, _np_refkernel_f32(A, B, step=8).view(np.uint32))
+    assert not np.array_equal(ref, _np_naive_f32(A, B).view(np.uint32))
+    desc = _np_naive_f32(A[:, ::-1], B[::-1])  # k descending
+    assert not np.array_equal(orc.gemm_naive_f32(A, B).view(np.uint32), desc.view(np.uint32))
+
+
 def test_refkernel_zero_fills_k_tail(orc):
     """K not a multiple of 32: elements past K contribute nothing (mmmTensor.cpp:137-175)."""
     rng = np.random.default_rng(8)
