@@ -19,6 +19,10 @@
 
 #include "mmm.h"
 
+#if defined(__FLT16_MANT_DIG__)
+#include <type_traits>
+#endif
+
 namespace mmm {
 
 // Row-major C[DIM_I][DIM_J] (fp32) = A[DIM_I][DIM_K] * B[DIM_K][DIM_J] (fp16), dense rows.
@@ -54,6 +58,36 @@ inline hipError_t WMMA_Tensor(const mmm_half* G, const mmm_half* Input, float* O
   if (e != hipSuccess) return e;
   return mmm_contract5d_f16f32(&d, G, Input, Out, stream);
 }
+
+#if defined(__FLT16_MANT_DIG__)
+// The reference's own pointer types: its call sites hold the operands as _Float16* (mmm.cpp:1446-1447,
+// 1488, 1496; mmmTensor.cpp:44-45, 364, 369), so with a compiler that has _Float16 (hipcc, clang)
+// those call sites compile unchanged.  Templates on the pointee, so that a literal nullptr still
+// selects the mmm_half forms above without ambiguity.
+template <class H>
+using if_f16 = typename std::enable_if<std::is_same<typename std::remove_cv<H>::type, _Float16>::value, int>::type;
+static_assert(sizeof(_Float16) == sizeof(mmm_half), "_Float16 is the binary16 bit pattern mmm_half holds");
+
+template <int WAVE_M, int WAVE_N, int WAVES_I, int WAVES_J, class HA, class HB, if_f16<HA> = 0, if_f16<HB> = 0>
+inline hipError_t WMMA_Swizzled_Full(HA* A, HB* B, float* C, int DIM_I, int DIM_J, int DIM_K,
+                                     hipStream_t stream = nullptr) {
+  return WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>((const mmm_half*)A, (const mmm_half*)B, C, DIM_I,
+                                                              DIM_J, DIM_K, stream);
+}
+
+template <class HA, class HB, if_f16<HA> = 0, if_f16<HB> = 0>
+inline hipError_t WMMA_Auto(HA* A, HB* B, float* C, int M, int N, int K, int64_t lda, int64_t ldb, int64_t ldc,
+                            hipStream_t stream = nullptr, void* workspace = nullptr, size_t workspace_bytes = 0) {
+  return WMMA_Auto((const mmm_half*)A, (const mmm_half*)B, C, M, N, K, lda, ldb, ldc, stream, workspace,
+                   workspace_bytes);
+}
+
+template <class HA, class HB, if_f16<HA> = 0, if_f16<HB> = 0>
+inline hipError_t WMMA_Tensor(HA* G, HB* Input, float* Out, int mt, int bt, int rt, int nt, int rt_l,
+                              hipStream_t stream = nullptr) {
+  return WMMA_Tensor((const mmm_half*)G, (const mmm_half*)Input, Out, mt, bt, rt, nt, rt_l, stream);
+}
+#endif
 
 }  // namespace mmm
 

@@ -203,6 +203,39 @@ int main() {
     assert r.returncode == 0 and r.stdout.strip() == "0", r.stdout + r.stderr
 
 
+def test_cpp_header_float16_call_sites(mm, tmp_path):
+    """With a compiler that has _Float16 (clang, as hipcc uses), include/mmm.hpp takes the
+    reference's own operand types at its call sites -- _Float16* (mmm.cpp:1446-1447, 1496) and
+    const _Float16* (mmmTensor.cpp:44-45) -- while a literal nullptr still resolves to the
+    mmm_half forms; null pointers report hipErrorInvalidValue (no GPU needed)."""
+    src = tmp_path / "use_f16.cpp"
+    src.write_text("""
+#include <cstdio>
+#include "mmm.hpp"
+int main() {
+  _Float16* dA = nullptr;
+  const _Float16* cG = nullptr;
+  float* dC = nullptr;
+  int bad = 0;
+  bad += mmm::WMMA_Swizzled_Full<2, 2, 4, 4>(dA, dA, dC, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_Swizzled_Full<2, 2, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_Auto(dA, cG, dC, 8, 8, 8, 8, 8, 8) != hipErrorInvalidValue;
+  bad += mmm::WMMA_Tensor(cG, cG, dC, 2, 3, 4, 5, 6) != hipErrorInvalidValue;
+  std::printf("%d\\n", bad);
+  return bad;
+}
+""")
+    exe = tmp_path / "use_f16"
+    libdir = os.path.dirname(mm.LIB_PATH)
+    r = subprocess.run(["/opt/rocm/llvm/bin/clang++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I",
+                        os.path.join(REPO, "include"), "-I", "/opt/rocm/include", str(src), "-o", str(exe),
+                        f"-L{libdir}", "-lmmm", f"-Wl,-rpath,{libdir}", "-L/opt/rocm/lib", "-lamdhip64"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip() == "0", r.stdout + r.stderr
+
+
 def test_isa_report(tmp_path):
     """Every gfx950 kernel: wave64, no VGPR spill or scratch, LDS within one CU's 160 KiB; the
     main tiles issue matrix-core ops and direct-to-LDS loads; the committed report lists them."""
