@@ -16,7 +16,14 @@ Extra objects on the line:
                   WRITE_SIZE (read from profiles/, null when not measured for the workload).
   cpu_baseline -- the oracle's multithreaded CPU FP16->FP32 GEMM on a bounded sample of the
                   same workload, on this host's cores (reported only).
-  hipblaslt    -- hipBLASLt on the same inputs and problem (FP16 in, FP32 out).
+  hipblaslt    -- hipBLASLt on the same inputs and problem (FP16 in, FP32 out): the fastest of
+                  its heuristic's (up to 16) candidates, each timed on these inputs first.
+  validation   -- one step's output checked in full on the device against the fp64 truth:
+                  |C - T| <= 1e-3 * sum_k |a*b| for every element (violations must be 0).
+
+Order of a run: the validation and hipBLASLt's candidate search come first (`before_timing_s`
+is how long they kept the GPU busy), then the W untimed and K timed steps, then hipBLASLt's W
+and K, the MFMA-ceiling probe and the CPU baseline.
 
 Other workloads (parity configs, reported with --workload or --report, never the default):
 gemm256, ragged, contraction, skinny (and skinny_nows, the same problem without a workspace),
@@ -147,8 +154,16 @@ def make_workload(name, torch, mmm):
         fill(In, seed, 1)
         Out = torch.empty((mt, bt, rt), dtype=torch.float32, device=dev)
         desc = mmm.contract_desc_reference(mt, bt, rt, nt, rt_l)
-        return {"launch": mmm.bind_contract(desc, G, In, Out), "witness": None, "host_inputs": None,
-                "M": M, "N": N, "K": K}
+        launch = mmm.bind_contract(desc, G, In, Out)
+
+        def truth():
+            T = torch.empty(Out.shape, dtype=torch.float64, device=dev)
+            S = torch.empty_like(T)
+            mmm.contract_truth(desc, G, In, T, S)
+            return T, S
+
+        return {"launch": launch, "witness": None, "host_inputs": None, "M": M, "N": N, "K": K,
+                "validate": lambda: validate_step(torch, launch, Out, truth)}
     if kind == "contraction":
         b, i, k, l, j = 8, 1024, 32, 64, 2048
         A = torch.empty((b, i, k, l), dtype=torch.float16, device=dev)
@@ -158,8 +173,10 @@ def make_workload(name, torch, mmm):
         Cd = torch.empty((b, i, j), dtype=torch.float32, device=dev)
         desc = mmm.contract_desc_baseline(b, i, k, l, j)
         A2, B2, C2 = A.view(M, K), B.view(K, N), Cd.view(M, N)
+        launch = mmm.bind_contract(desc, A, B, Cd)
         return {
-            "launch": mmm.bind_contract(desc, A, B, Cd),
+            "launch": launch,
+            "validate": lambda: validate_step(torch, launch, C2, lambda: mmm.gemm_truth(A2, B2)),
             "witness": lambda: mmm.bind_witness_hipblaslt(A2, B2, C2),
             "clocked": lambda clock: mmm.bind_gemm_clocked(A2, B2, C2, clock),
             "host_inputs": lambda: (A2.cpu().numpy(), B2.cpu().numpy()),
@@ -192,13 +209,32 @@ def make_workload(name, torch, mmm):
             wb[wstate["i"] % nb]()
             wstate["i"] += 1
 
+        run.tuning = wb[0].tuning
         return run
 
     # the tile kernels record their clock (the M <= 64 streaming kernels do not)
     clocked = (lambda clock: mmm.bind_gemm_clocked(A, Bs[0], Cd, clock, workspace=ws)) if M > 64 else None
     return {"launch": launch, "witness": witness, "clocked": clocked,
+            "validate": lambda: validate_step(torch, bound[0], Cd, lambda: mmm.gemm_truth(A, Bs[0])),
             "host_inputs": lambda: (A.cpu().numpy(), Bs[0].cpu().numpy()),
             "M": M, "N": N, "K": K}
+
+
+def validate_step(torch, launch, C_out, truth, tol: float = 1e-3):
+    """One step, then every output checked on the device against the fp64 truth T and scale
+    S = sum_k |a*b| of the on-device cross-check kernel: |C - T| <= tol * S (NaN fails)."""
+    C_out.fill_(float("nan"))
+    launch()
+    T, S = truth()
+    torch.cuda.synchronize()
+    d = (C_out.double() - T).abs()
+    ok = d <= tol * S
+    worst = (d / S.clamp_min(1e-300)).nan_to_num(nan=float("inf")).max().item()
+    out = {"outputs": int(C_out.numel()), "violations": int((~ok).sum().item()), "worst_err_over_S": worst,
+           "tolerance": f"|C - T| <= {tol:g} * sum_k |a*b|, T and S the fp64 truth on the device"}
+    del T, S, d, ok
+    torch.cuda.empty_cache()
+    return out
 
 
 def time_launches(torch, fn, steps: int, warmup: int):
@@ -322,16 +358,30 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_ceiling=False):
+def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_ceiling=False, with_validate=True):
+    """One workload's measurements.  Order: the step's output is validated in full (fp64 truth on
+    the device) and the hipBLASLt comparison is planned and tuned (every heuristic candidate timed,
+    the fastest bound) before anything is timed; then the library's W + K launches, its clocked
+    launches, hipBLASLt's W + K launches, the MFMA-ceiling probe and the CPU baseline."""
     W = make_workload(name, torch, mmm)
     M, N, K = W["M"], W["N"], W["K"]
     flops = 2.0 * M * N * K
     algo_bytes = W.get("bytes", 2.0 * M * K + 2.0 * K * N + 4.0 * M * N)
+    t_pre = time.perf_counter()
+    validation = W["validate"]() if with_validate and W.get("validate") else None
+    with_witness = with_witness and W.get("witness") is not None
+    witness, witness_err = None, None
+    if with_witness:
+        try:
+            witness = W["witness"]()
+        except Exception as e:  # the comparison point must not hide the measurement
+            witness_err = str(e)
+    torch.cuda.synchronize()
+    pre_s = time.perf_counter() - t_pre
     ms, per, wall = time_launches(torch, W["launch"], steps, warmup)
     clk = clocked_pass(torch, mmm, W, steps) if W.get("clocked") else None
     avg_launch = statistics.fmean(per)
     hbm = name in ("skinny", "skinny_nows", "copy", "read_ceiling", "read_ceiling_lds")
-    with_witness = with_witness and W["witness"] is not None
     with_cpu = with_cpu and W["host_inputs"] is not None
     res = {
         "workload": name,
@@ -341,6 +391,7 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_c
         "launch_ms": {"avg": avg_launch, "min": min(per), "median": statistics.median(per),
                       "first": per[0], "last": per[-1]},
         "wall_s": wall,
+        "before_timing_s": pre_s,
     }
     if hbm:
         achieved = algo_bytes / (avg_launch * 1e-3) / 1e9
@@ -361,12 +412,19 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_c
                          "tflops and pct_peak_at_clock are those launches' own")
         res["clock"] = clk
     res["smi"] = smi_snapshot()
+    if validation is not None:
+        res["validation"] = validation
     if with_witness:
         try:
-            wms, wper, _ = time_launches(torch, W["witness"](), steps, warmup)
+            if witness is None:
+                raise RuntimeError(witness_err)
+            wms, wper, _ = time_launches(torch, witness, steps, warmup)
             res["hipblaslt"] = {"ms_per_step": wms, "tflops": flops / (wms * 1e-3) / 1e12,
                                 "gbs": algo_bytes / (wms * 1e-3) / 1e9,
-                                "launch_ms_median": statistics.median(wper)}
+                                "launch_ms_median": statistics.median(wper),
+                                "algos": witness.tuning["algos"], "best_index": witness.tuning["best_index"],
+                                "algo_choice": "fastest of the heuristic's candidates, each timed on these "
+                                               "inputs (median of 5 after 1)"}
         except Exception as e:  # the comparison point must not hide the measurement
             res["hipblaslt"] = {"error": str(e)}
     if with_ceiling:
@@ -459,8 +517,8 @@ def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool
     """Every instantiated tile and the library's own choice on each problem of `shapes`
     (SWEEP_SHAPES by default); median per-launch TFLOP/s, written as a markdown table to path."""
     tiles = list(mmm.TILES)
-    lines = ["| M x N x K | library pick | pick TFLOP/s | " + " | ".join(tiles) + " | best | pick / best | hipBLASLt |",
-             "|" + "---|" * (len(tiles) + 6)]
+    lines = ["| M x N x K | library pick | pick TFLOP/s | " + " | ".join(tiles) + " | best | pick / best | hipBLASLt | hipBLASLt candidate |",
+             "|" + "---|" * (len(tiles) + 7)]
     for (M, N, K) in (shapes or SWEEP_SHAPES):
         A = torch.empty((M, K), dtype=torch.float16, device="cuda")
         B = torch.empty((K, N), dtype=torch.float16, device="cuda")
@@ -504,8 +562,10 @@ def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool
         per_tile = {t: med[t] for t in tiles}
         best = max(per_tile, key=per_tile.get)
         wit = med.get("hipblaslt", float("nan"))
+        wpick = launchers["hipblaslt"].tuning if "hipblaslt" in launchers else None
         row = (f"| {M} x {N} x {K} | {pick} | {auto:.1f} | " + " | ".join(f"{per_tile[t]:.1f}" for t in tiles) +
-               f" | {best} | {auto / per_tile[best]:.2f} | {wit:.1f} |")
+               f" | {best} | {auto / per_tile[best]:.2f} | {wit:.1f} | "
+               + (f"#{wpick['best_index']} of {wpick['algos']}" if wpick else "") + " |")
         lines.append(row)
         _log("[sweep] " + row)
         del A, B, Cm, launchers
@@ -524,6 +584,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-witness", action="store_true", help="skip the hipBLASLt comparison")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the live MFMA-ceiling probe (gemm8192 only)")
+    ap.add_argument("--no-validate", action="store_true",
+                    help="skip the full-output fp64 validation of the step that precedes the timing")
     ap.add_argument("--steady", type=float, metavar="SECONDS", default=0.0,
                     help="also run the workload back to back for SECONDS and add its steady-state throughput, "
                          "SMU clock/power and in-kernel clock to the line (object `steady`)")
@@ -559,7 +621,7 @@ def main() -> int:
         for name in ["gemm8192", "contraction", "ragged", "skinny", "skinny_nows", "gemm256", "contraction_ref"]:
             _log(f"[bench] {name}")
             r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=False,
-                             with_witness=not args.no_witness)
+                             with_witness=not args.no_witness, with_validate=not args.no_validate)
             _log(f"[bench] {name}: {r['tflops']:.1f} TFLOP/s ({r['gbs']:.0f} GB/s); "
                  f"hipBLASLt {r.get('hipblaslt', {}).get('tflops', float('nan')):.1f} TFLOP/s")
             report.append(r)
@@ -569,7 +631,8 @@ def main() -> int:
 
     name = args.workload
     r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=not args.no_cpu,
-                     with_witness=not args.no_witness, with_ceiling=name == "gemm8192" and not args.no_ceiling)
+                     with_witness=not args.no_witness, with_ceiling=name == "gemm8192" and not args.no_ceiling,
+                     with_validate=not args.no_validate)
     M, N, K = WORKLOADS[name][:3]
     skinny = name in ("skinny", "skinny_nows", "copy", "read_ceiling", "read_ceiling_lds")
     line = {
@@ -589,7 +652,10 @@ def main() -> int:
         "pct_peak": round(100.0 * r["tflops"] / PEAK_TFLOPS, 2),
         "launch_ms": {k: round(v, 5) for k, v in r["launch_ms"].items()},
         "roofline": r["roofline"],
+        "before_timing_s": round(r["before_timing_s"], 3),
     }
+    if "validation" in r:
+        line["validation"] = r["validation"]
     if "clock" in r:
         line["clock"] = r["clock"]
     if "ceiling" in r:

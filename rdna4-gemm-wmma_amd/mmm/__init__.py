@@ -525,6 +525,11 @@ def _witness_lib():
         W.mmm_witness_hipblaslt_run.argtypes = [p, p, p, p, p, sz, p]
         W.mmm_witness_hipblaslt_destroy.restype = None
         W.mmm_witness_hipblaslt_destroy.argtypes = [p]
+        fp = C.POINTER(C.c_float)
+        W.mmm_witness_hipblaslt_tune.restype = i
+        W.mmm_witness_hipblaslt_tune.argtypes = [p, p, p, p, p, sz, p, i, C.POINTER(i), fp, fp]
+        W.mmm_witness_hipblaslt_info.restype = i
+        W.mmm_witness_hipblaslt_info.argtypes = [p, C.POINTER(i), C.POINTER(i)]
         _witness = W
     return _witness
 
@@ -557,7 +562,8 @@ def witness_hipblaslt(A, B, C_out=None, stream=None):
 
 
 class _WitnessPlan:
-    """A hipBLASLt plan (descriptors, layouts, heuristic result) built once for one shape."""
+    """A hipBLASLt plan (descriptors, layouts, up to 16 heuristic candidates) built once for one
+    shape; its runs use the heuristic's first candidate until tune() binds the fastest."""
 
     def __init__(self, W, M, N, K, lda, ldb, ldc, ws_bytes):
         self._W = W
@@ -566,15 +572,35 @@ class _WitnessPlan:
         if rc != 0:
             raise MMMError("mmm_witness_hipblaslt_create", rc)
 
+    def info(self):
+        n, chosen = C.c_int(), C.c_int()
+        self._W.mmm_witness_hipblaslt_info(self.ptr, C.byref(n), C.byref(chosen))
+        return n.value, chosen.value
+
+    def tune(self, A, B, C_out, ws, stream=None, reps: int = 5):
+        """Time every candidate on these operands (median of `reps` matmuls after one untimed)
+        and bind the fastest; returns {"algos": n, "best_index": i, "ms": [...per candidate]}."""
+        n, _ = self.info()
+        each = (C.c_float * max(n, 1))()
+        best, best_ms = C.c_int(), C.c_float()
+        rc = self._W.mmm_witness_hipblaslt_tune(self.ptr, _ptr(A), _ptr(B), _ptr(C_out), _ptr(ws), ws.numel(),
+                                                _stream(stream), reps, C.byref(best), C.byref(best_ms), each)
+        if rc != 0:
+            raise MMMError("mmm_witness_hipblaslt_tune", rc)
+        return {"algos": n, "best_index": best.value, "ms": [round(each[i], 5) for i in range(n)]}
+
     def __del__(self):
         if getattr(self, "ptr", None) and self.ptr.value:
             self._W.mmm_witness_hipblaslt_destroy(self.ptr)
 
 
-def bind_witness_hipblaslt(A, B, C_out, stream=None):
+def bind_witness_hipblaslt(A, B, C_out, stream=None, tune: bool = True):
     """A zero-argument launcher of hipBLASLt's C = A @ B on fixed tensors and stream: the
-    descriptors, layouts and algorithm heuristic are built once here, and each call is one
-    hipblasLtMatmul -- the same footing as bind_gemm's launchers."""
+    descriptors, layouts and up to 16 algorithm candidates are built once here, and each call is
+    one hipblasLtMatmul -- the same footing as bind_gemm's launchers.  With tune (the default)
+    every candidate is timed on these operands first and the fastest is bound (launch.tuning
+    records the candidate count, the winner's index in the heuristic's order and each median);
+    without it the heuristic's first candidate runs."""
     W = _witness_lib()
     ws = _witness_workspace(A.device)
     M, K = A.shape
@@ -583,4 +609,5 @@ def bind_witness_hipblaslt(A, B, C_out, stream=None):
     args = (plan.ptr, _ptr(A), _ptr(B), _ptr(C_out), _ptr(ws), ws.numel(), _stream(stream))
     launch = _bound(W.mmm_witness_hipblaslt_run, "mmm_witness_hipblaslt_run", args, (A, B, C_out, ws))
     launch.plan = plan  # keeps the plan alive as long as the launcher
+    launch.tuning = plan.tune(A, B, C_out, ws, stream) if tune else {"algos": plan.info()[0], "best_index": 0}
     return launch
