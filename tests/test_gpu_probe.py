@@ -64,6 +64,26 @@ def test_probe_read_runs(mm, cuda, lds):
         assert folded == 0x5A5A5A5A
 
 
+def test_probe_read_lds_pieces(mm, cuda):
+    """The direct-to-LDS read probe loads the pieces it claims: each 1 KB piece p starts with the
+    word p + 1, and workgroup b reports the first word of wave 0's ring slot 0, which is the last
+    piece that wave put there.  Wave 4b (2048 workgroups x 4 waves) takes pieces 4b + 8192 j and
+    ring slot j % 8; with 131072 pieces (128 MiB) that is j = 8, piece 4b + 65536."""
+    pieces = 1 << 17
+    src = cuda.zeros(pieces * 1024, dtype=cuda.uint8, device="cuda")
+    src.view(cuda.int32)[::256] = cuda.arange(1, pieces + 1, dtype=cuda.int32, device="cuda")
+    out = cuda.full((2048,), -1, dtype=cuda.int32, device="cuda")
+    mm.probe_read(src, out, direct_to_lds=True)
+    cuda.cuda.synchronize()
+    waves = 2048 * 4
+    expect = []
+    for b in range(2048):
+        wid = 4 * b
+        j_last = max(j for j in range(0, pieces // waves + 1, 8) if wid + j * waves < pieces)
+        expect.append(wid + j_last * waves + 1)
+    assert np.array_equal(out.cpu().numpy(), np.array(expect, dtype=np.int32))
+
+
 @pytest.mark.parametrize("shape", [(256, 256, 256), (1000, 777, 320), (16, 4096, 4096)])
 def test_bound_hipblaslt_matches_library(orc, mm, cuda, shape):
     """The bound hipBLASLt launcher (descriptors and heuristic planned once) computes the same

@@ -52,6 +52,46 @@ def test_noalloc_matches_workspace_entry(mm, cuda):
             assert torch.equal(out, ref), f"{M}x{N}x{K} rep {rep}"
 
 
+@pytest.mark.parametrize("shape", [(2304, 2304, 8192), (16, 4096, 4096)], ids=lambda s: "x".join(map(str, s)))
+def test_noalloc_graph_capture(mm, cuda, shape):
+    """The documented order for callers under graph capture: one eager call (looks the array's
+    address up), then a captured call, replayed.  Both shapes split K into the array (a tile
+    split with its reduction launch; the streaming kernel's split).  Every replay, with eager
+    work and synchronisation in between, equals mmm_gemm_f16f32_ws's result bit for bit."""
+    torch = cuda
+    M, N, K = shape
+    assert mm.gemm_plan(M, N, K)["workspace_bytes"] > 0
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    A = torch.empty((M, K), dtype=torch.float16, device="cuda")
+    B = torch.empty((K, N), dtype=torch.float16, device="cuda")
+    mm.fill_uniform(A, 41, 0)
+    mm.fill_uniform(B, 41, 1)
+    ref = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    _call_ws(mm, torch, A, B, ref, ws)
+    out = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    assert _call_noalloc(mm, torch, A, B, out) == 0  # eager first
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = _call_noalloc(mm, torch, A, B, out)
+    assert rc == 0
+    other = torch.empty((300, 264), dtype=torch.float32, device="cuda")
+    for i in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {i}"
+        # eager calls that reuse the array between the replays
+        a2 = torch.empty((300, 200), dtype=torch.float16, device="cuda")
+        b2 = torch.empty((200, 264), dtype=torch.float16, device="cuda")
+        mm.fill_uniform(a2, 42 + i, 0)
+        mm.fill_uniform(b2, 42 + i, 1)
+        assert _call_noalloc(mm, torch, A, B, other.new_empty((M, N))) == 0
+        assert _call_noalloc(mm, torch, a2, b2, other) == 0
+        torch.cuda.synchronize()
+
+
 def test_noalloc_argument_checks(mm, cuda):
     L = mm.lib()
     null = C.c_void_p(0)
