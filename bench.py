@@ -112,8 +112,13 @@ def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_workload(name, torch, mmm):
-    """Device inputs and a launch closure for one step of the named workload."""
+# the GEMM given by --shape (and --tile): U[-1,1) inputs from seed 7, as in the tile sweep
+SHAPE_SEED = 7
+
+
+def make_workload(name, torch, mmm, tile=None):
+    """Device inputs and a launch closure for one step of the named workload (`tile`: a block tile
+    forced on a GEMM workload instead of the library's pick)."""
     M, N, K, kind, seed, dist = WORKLOADS[name]
     dev = "cuda"
     fill = mmm.fill_uniform if dist == "uniform" else (lambda t, s, i: mmm.fill_normal(t, s, i, 0.1))
@@ -194,7 +199,7 @@ def make_workload(name, torch, mmm):
     Cd = torch.empty((M, N), dtype=torch.float32, device=dev)
     state = {"i": 0}
     # launchers bound once (checks and argument marshalling outside the timed loop)
-    bound = [mmm.bind_gemm(A, Bt, Cd, workspace=ws) for Bt in Bs]
+    bound = [mmm.bind_gemm(A, Bt, Cd, workspace=ws, tile=tile) for Bt in Bs]
 
     def launch():
         bound[state["i"] % nb]()
@@ -213,7 +218,7 @@ def make_workload(name, torch, mmm):
         return run
 
     # the tile kernels record their clock (the M <= 64 streaming kernels do not)
-    clocked = (lambda clock: mmm.bind_gemm_clocked(A, Bs[0], Cd, clock, workspace=ws)) if M > 64 else None
+    clocked = (lambda clock: mmm.bind_gemm_clocked(A, Bs[0], Cd, clock, workspace=ws)) if M > 64 and not tile else None
     return {"launch": launch, "witness": witness, "clocked": clocked,
             "validate": lambda: validate_step(torch, bound[0], Cd, lambda: mmm.gemm_truth(A, Bs[0])),
             "host_inputs": lambda: (A.cpu().numpy(), Bs[0].cpu().numpy()),
@@ -358,12 +363,13 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_ceiling=False, with_validate=True):
+def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_ceiling=False, with_validate=True,
+                 tile=None):
     """One workload's measurements.  Order: the step's output is validated in full (fp64 truth on
     the device) and the hipBLASLt comparison is planned and tuned (every heuristic candidate timed,
     the fastest bound) before anything is timed; then the library's W + K launches, its clocked
     launches, hipBLASLt's W + K launches, the MFMA-ceiling probe and the CPU baseline."""
-    W = make_workload(name, torch, mmm)
+    W = make_workload(name, torch, mmm, tile=tile)
     M, N, K = W["M"], W["N"], W["K"]
     flops = 2.0 * M * N * K
     algo_bytes = W.get("bytes", 2.0 * M * K + 2.0 * K * N + 4.0 * M * N)
@@ -592,6 +598,9 @@ def main() -> int:
     ap.add_argument("--report", metavar="PATH", help="measure every workload and write a JSON report to PATH")
     ap.add_argument("--sweep", metavar="PATH", help="time every tile against the library's pick over a shape "
                                                      "grid and write a markdown table to PATH")
+    ap.add_argument("--shape", metavar="MxNxK", help="measure this GEMM (U[-1,1) inputs, seed 7) instead of --workload")
+    ap.add_argument("--tile", metavar="BMxBN", help="with --shape: force this block tile (one of the library's six; "
+                                                    "default: the library's own pick)")
     ap.add_argument("--shapes", metavar="MxNxK,...", help="the problems --sweep runs: a list, or `llm` for the "
                                                           "transformer-layer set (default: the built-in list)")
     args = ap.parse_args()
@@ -630,9 +639,17 @@ def main() -> int:
             json.dump({"device": torch.cuda.get_device_name(0), "results": report}, f, indent=1)
 
     name = args.workload
+    if args.shape:
+        (sM, sN, sK), = parse_shapes(args.shape)
+        name = "shape"
+        WORKLOADS[name] = (sM, sN, sK, "gemm", SHAPE_SEED, "uniform")
+        DESCRIPTIONS[name] = (f"gemm_nn {sM}x{sN}x{sK} fp16 row-major, " + (f"tile {args.tile} forced, " if args.tile else "")
+                              + f"U[-1,1) seed {SHAPE_SEED}")
+    if args.tile and (not args.shape or args.tile not in mmm.TILES):
+        ap.error(f"--tile needs --shape and one of {', '.join(mmm.TILES)}")
     r = run_workload(name, torch, mmm, args.steps, args.warmup, with_cpu=not args.no_cpu,
                      with_witness=not args.no_witness, with_ceiling=name == "gemm8192" and not args.no_ceiling,
-                     with_validate=not args.no_validate)
+                     with_validate=not args.no_validate, tile=args.tile)
     M, N, K = WORKLOADS[name][:3]
     skinny = name in ("skinny", "skinny_nows", "copy", "read_ceiling", "read_ceiling_lds")
     line = {

@@ -128,9 +128,16 @@ hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream) {
 constexpr double kPartialRoundBoost = 0.6;
 
 // Estimated time of a tile launch, in seconds: rounds of 256 concurrent workgroups (one per
-// CU) times the MFMA time of one tile's K range at the tile's relative efficiency (measured
-// at 8192^3, each tile forced: 256x256 1.0, 128x256 0.82, 256x128 0.84, 128x128 0.75; 192x192
-// 0.82 and 64x64 0.38 there, priced at 0.91 and 0.45, which pick the faster tile on the shapes
+// CU) times the MFMA time of one tile's K range at the tile's relative efficiency -- its MFMA
+// rate against the 256x256 tile's.  Measured at 8192^3 with each tile forced, as throughput
+// (128x256 0.82, 256x128 0.84, 128x128 0.75, 192x192 0.82, 64x64 0.38) and as the matrix cores'
+// busy share under rocprofv3 (SQ_VALU_MFMA_BUSY_CYCLES: 256x256 0.732; 128x256 0.600, 256x128
+// 0.598 -> 0.82; 128x128 0.575 -> 0.79; 192x192 0.608 -> 0.83; 64x64 0.291 -> 0.40).  What lowers
+// the smaller tiles' rate is operand loads per flop ((BM + BN) / (BM * BN): 1.5x for the narrow
+// tiles, 2x for 128x128, 4x for 64x64), which saturate the address unit (TA busy 0.48 for
+// 256x256, 0.59-0.65 narrow, 0.83 for 128x128, 0.89 for 64x64); no tile has LDS bank conflicts.
+// The narrow tiles are priced at 0.82 and 128x128 at 0.76; 192x192 and 64x64 at 0.91 and 0.45,
+// the values that pick the faster tile on the shapes
 // measured for them: 192x192 on 3072^3, 3072^2 x 8192, 4357 x 4095 x 4111 and the 4-way K split
 // of 1536^2 x 12288 (937 TFLOP/s against 864 for a 7-way split of 256x256 tiles; at 0.90 the
 // estimates were 2.6% apart and the larger tile kept it), 256x256 on 2304^2 x 8192, 4608^2 x

@@ -43,6 +43,9 @@
 
 namespace mmm {
 
+// Fragment offsets a wave keeps per K-step (A) or per B fragment: at most kMaxOff of each.
+constexpr int kMaxOff = 8;
+
 // Block tile BM x BN, K step BK (32 or 64), WGM x WGN waves, STAGES-deep LDS ring, OCC
 // workgroups per CU targeted by the launch bounds (OCC > 1 caps registers accordingly), MFMA
 // shape MF: 32 = v_mfma_f32_32x32x16_f16, 16 = v_mfma_f32_16x16x32_f16 (same MACs per LDS byte;
@@ -105,13 +108,14 @@ struct Tile {
   static_assert(BK == 32 || BK == 64, "K step must be 32 or 64");
   static_assert(TM % 32 == 0 && (TN % 32 == 0 || (MF == 16 && TN % 16 == 0)),
                 "wave tile must be a multiple of 32x32 (32 x 16 with 16x16 fragments)");
-  static_assert(FN <= 4 && KSTEPS * APAR <= 4, "at most 4 B fragments and 4 A offsets per wave");
+  static_assert(FN <= kMaxOff && KSTEPS * APAR <= kMaxOff, "fragment offsets per wave");
   static_assert(CB == 8 || CB == 24 || CB >= 16, "B swizzle: rows of 8 or 24 chunks or at least 16");
   // B staging: chunk slot s = r*NT + w*64 + lane of a stage's [BK][CB] chunk grid is row s / CB.
-  // When CB divides 64, a wave's slots are whole rows, rows advance by NT / CB per r and the
-  // logical chunk is the same for every r (one base offset plus a uniform step per r);
-  // otherwise (BN = 192) each r has its own row and chunk.
-  static constexpr bool B_UNIFORM = 64 % CB == 0;
+  // When CB divides 64, a wave's slots are whole rows and rows advance by NT / CB per r; if that
+  // step is also a multiple of the rows the B swizzle depends on, the logical chunk is the same
+  // for every r (one base offset plus a uniform step per r).  Otherwise (BN = 192; four waves
+  // over 32-chunk rows, 8 rows per round against a 16-row swizzle) each r has its own row and chunk.
+  static constexpr bool B_UNIFORM = 64 % CB == 0 && (NT / CB) % SWZ_B_ROWS == 0;
   static_assert((BM * CA) % NT == 0 && (BK * CB) % NT == 0, "chunks must divide evenly over threads");
   static_assert(STAGES >= 2 && OCC * STAGES * STAGE <= 160 * 1024, "LDS rings must fit the 160 KB LDS");
 };
@@ -168,7 +172,7 @@ using AccT = typename std::conditional<T::MF == 32, f32x16, f32x4>::type;
 // B) or b_off[kk * APAR + phase] (K-major B, laid out and swizzled like A).
 template <class T, bool BKM>
 __device__ __forceinline__ void load_frag_unit(const char LDS_AS* a_st, const char LDS_AS* b_st,
-                                               const uint32_t (&a_off)[4], const uint32_t (&b_off)[4], int kk, int u,
+                                               const uint32_t (&a_off)[kMaxOff], const uint32_t (&b_off)[kMaxOff], int kk, int u,
                                                Frags<T>& f) {
   if (u < T::FM) {
     f.a[u] = lds_read_a(a_st + a_off[kk * T::APAR + u % T::APAR] + (u / T::APAR) * T::AROWS * T::BK * 2);
@@ -184,8 +188,8 @@ __device__ __forceinline__ void load_frag_unit(const char LDS_AS* a_st, const ch
 
 // All fragment reads of K-step kk from an LDS stage.
 template <class T, bool BKM>
-__device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char LDS_AS* b_st, const uint32_t (&a_off)[4],
-                                           const uint32_t (&b_off)[4], int kk, Frags<T>& f) {
+__device__ __forceinline__ void load_frags(const char LDS_AS* a_st, const char LDS_AS* b_st, const uint32_t (&a_off)[kMaxOff],
+                                           const uint32_t (&b_off)[kMaxOff], int kk, Frags<T>& f) {
 #pragma unroll
   for (int u = 0; u < T::FM + T::FN; ++u) load_frag_unit<T, BKM>(a_st, b_st, a_off, b_off, kk, u, f);
 }
@@ -225,7 +229,7 @@ __device__ __forceinline__ void mfma_frags(const Frags<T>& f, AccT<T> (&acc)[T::
 
 template <class T, bool BKM, class Hook>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* a_st, const char LDS_AS* b_st,
-                                              const uint32_t (&a_off)[4], const uint32_t (&b_off)[4],
+                                              const uint32_t (&a_off)[kMaxOff], const uint32_t (&b_off)[kMaxOff],
                                               AccT<T> (&acc)[T::FM][T::FN], Hook&& after_first_reads) {
   using Frags = mmm::Frags<T>;
   auto load = [&](int kk, Frags& f) { load_frags<T, BKM>(a_st, b_st, a_off, b_off, kk, f); };
@@ -356,8 +360,8 @@ __device__ __forceinline__ void record_clock(uint64_t* clk, int at) {
 // previous tile's C stores) were issued after them; the first wait lets those stay
 // outstanding (vmcnt retires in issue order).
 template <class T, bool BKM, int NST = 0, class Prep, class DmaOne, class IssueTile>
-__device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool tail_regs, const uint32_t (&a_off)[4],
-                                            const uint32_t (&b_off)[4], AccT<T> (&acc)[T::FM][T::FN], Prep&& prep,
+__device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool tail_regs, const uint32_t (&a_off)[kMaxOff],
+                                            const uint32_t (&b_off)[kMaxOff], AccT<T> (&acc)[T::FM][T::FN], Prep&& prep,
                                             DmaOne&& dma_one, IssueTile&& issue_tile, int pre = 0) {
   // Ring of S slots, tile u in slot u % S.  Cross-stage pipeline: during the last K-step of
   // tile t, this wave waits for its own loads of tile t+1, then the barrier (a) publishes
@@ -542,7 +546,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
   // 16*((l/16)%2) + 4*(l%4) of each 32-column fragment.  MF = 16: row l % 16 of A, k chunk
   // l / 16 of each 32-deep step; B rows 8*(l/16) + (l/4)%4 (+4), columns 4*(l%4) of each
   // 16-column fragment.
-  uint32_t a_off[4] = {0, 0, 0, 0};
+  uint32_t a_off[kMaxOff] = {};
 #pragma unroll
   for (int kk = 0; kk < T::KSTEPS; ++kk)
 #pragma unroll
@@ -551,7 +555,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       const int chunk = (T::KK / 8) * kk + lane / T::MF;
       a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
     }
-  uint32_t b_off[4] = {0, 0, 0, 0};
+  uint32_t b_off[kMaxOff] = {};
   {
     const int k = 8 * (lane / T::MF) + ((lane >> 2) & 3);
 #pragma unroll
@@ -834,11 +838,11 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_kernel(GemmP
   // Fragment offsets (as gemm_nn_kernel), rebuilt at every tile from a freshly read lane index:
   // kept from the kernel's start they would be live through the epilogue, whose line stores
   // need the registers.
-  uint32_t a_off[4], b_off[4];
+  uint32_t a_off[kMaxOff], b_off[kMaxOff];
   auto frag_offsets = [&]() {
     const int ln = lane_id_fresh();
 #pragma unroll
-    for (int q = 0; q < 4; ++q) a_off[q] = b_off[q] = 0;
+    for (int q = 0; q < kMaxOff; ++q) a_off[q] = b_off[q] = 0;
 #pragma unroll
     for (int kk = 0; kk < T::KSTEPS; ++kk)
 #pragma unroll
@@ -1009,7 +1013,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_split_kernel
   const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
   const int b_row0 = w * (64 / T::CB) + lane / T::CB;
   const int b_nc = 8 * ((lane % T::CB) ^ T::swz_bk(b_row0));
-  uint32_t a_off[4] = {0, 0, 0, 0};
+  uint32_t a_off[kMaxOff] = {};
 #pragma unroll
   for (int kk = 0; kk < T::KSTEPS; ++kk)
 #pragma unroll
@@ -1018,7 +1022,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_persistent_split_kernel
       const int chunk = (T::KK / 8) * kk + lane / T::MF;
       a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
     }
-  uint32_t b_off[4] = {0, 0, 0, 0};
+  uint32_t b_off[kMaxOff] = {};
   {
     const int k = 8 * (lane / T::MF) + ((lane >> 2) & 3);
 #pragma unroll
@@ -1280,13 +1284,13 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
     }
   }
 
-  uint32_t a_off[4] = {0, 0, 0, 0};
+  uint32_t a_off[kMaxOff] = {};
   {
     const int m = wm * T::TM + (lane & 31);
 #pragma unroll
     for (int kk = 0; kk < T::KSTEPS; ++kk) a_off[kk] = m * T::BK * 2 + ((2 * kk + (lane >> 5)) ^ T::swz_a(m)) * 16;
   }
-  uint32_t b_off[4] = {0, 0, 0, 0};
+  uint32_t b_off[kMaxOff] = {};
   if constexpr (BKM) {
     const int n = wn * T::TN + (lane & 31);
 #pragma unroll
@@ -1446,7 +1450,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_fold_dma_kernel(FoldProble
 
   // fragment read offsets: A rows and K-major B columns share the layout (lane l reads row
   // l % MF, k chunk l / MF of each K-step)
-  uint32_t a_off[4] = {0, 0, 0, 0}, b_off[4] = {0, 0, 0, 0};
+  uint32_t a_off[kMaxOff] = {}, b_off[kMaxOff] = {};
 #pragma unroll
   for (int kk = 0; kk < T::KSTEPS; ++kk)
 #pragma unroll
