@@ -154,7 +154,11 @@ typedef struct mmm_gemm_plan {
     int tile_persistent;                   /* 1: 256 workgroups each loop over tiles (whole
                                               interior tiles over several rounds) */
     int64_t workspace_bytes;               /* workspace the splits need (mmm_gemm_f16f32_ws);
-                                              the split counts above assume it is given */
+                                              the split counts above assume it is given, and so
+                                              does the kernel choice for M <= 64: without a
+                                              workspace, aligned problems whose 128-column strips
+                                              fill rounds of 256 workgroups less than 1/1.8 run
+                                              on the streaming kernel, not on tiles */
 } mmm_gemm_plan;
 
 /*

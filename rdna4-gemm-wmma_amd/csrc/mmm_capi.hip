@@ -381,6 +381,7 @@ hipError_t mmm_gemm_f16f32_clocked(const mmm_half* A, const mmm_half* B, float* 
   GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
   p.ws = (float*)workspace;
   p.ws_bytes = workspace ? workspace_bytes : 0;
+  p.ws_absent = workspace == nullptr;
   p.clk = clock;
   const GemmPlan pl = plan_gemm(p);
   switch (pl.kind) {
@@ -468,6 +469,7 @@ hipError_t mmm_gemm_f16f32_tiled(const mmm_half* A, const mmm_half* B, float* C,
   GemmProblem p{A, B, C, M, N, K, lda, ldb, ldc, false, false};
   p.ws = (float*)workspace;
   p.ws_bytes = workspace ? workspace_bytes : 0;
+  p.ws_absent = workspace == nullptr;
   return launch_gemm_nn(p, tile, stream);
 }
 

@@ -24,6 +24,8 @@ struct GemmProblem {
   size_t ws_bytes; // its size
   uint64_t* clk;   // null, or 4 counters workgroup 0 of a tile kernel writes: shader clock and
                    // real-time counter at its start, then at its end (measurement only)
+  bool ws_absent;  // the call has no workspace at all (not set by the plan query, which assumes
+                   // one): the tile kernels' K split is unavailable when choosing kernels
 };
 
 // Folded problem (the 5-D contraction descriptor, see mmm.h), with int32 extents.

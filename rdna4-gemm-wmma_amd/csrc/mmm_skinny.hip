@@ -539,13 +539,19 @@ int skinny_splits(const GemmProblem& p) { return stream_shape(p).splits; }
 // Fuller rounds stream faster: 16 x 49152 x 8192 (384 strips) 150.4 against 172.1, 32 x 81920 x
 // 4096 (640) 134.9 against 151.0, 16 x 151936 x 4096 (1187) 204.2 against 233.3, 16 x 65536 x
 // 8192 174.4 against 186.7 (16 x 100000 x 4096, 782 strips: 184.9 streamed, 163.0 on tiles).
+// Without a workspace the tiles run their last round unsplit, and on aligned rows the
+// threshold rises to 1.8 (measured: 16 x 33000 x 8192, 1.98, tiles 130.2 against 165.5 streamed;
+// 16 x 40000 x 8192, 1.64, tiles 129.4 against 123.3-125.2 streamed); unaligned rows still go to
+// tiles (16 x 33001 x 8192 147.2 against 201.6; 16 x 50257 x 4096 96.0 against 126.9-130.2;
+// 64 x 50257 x 4096 97.2 against 152.0).
 bool skinny_prefers_tiles(const GemmProblem& p) {
   const StreamShape sh = stream_shape(p);
   if (sh.splits == 0) return false;  // the wave-split kernel
   const int wgs = sh.strips * sh.splits;
   if (wgs <= 256) return false;
   const bool b_unaligned = ((uintptr_t)p.B & 15) || p.ldb % 8;
-  return b_unaligned || (double)((wgs + 255) / 256) * 256.0 / wgs > 1.5;
+  const double fill = (double)((wgs + 255) / 256) * 256.0 / wgs;  // rounds' slots per workgroup
+  return b_unaligned || fill > (p.ws_absent ? 1.8 : 1.5);
 }
 
 size_t skinny_workspace_bytes(const GemmProblem& p) {
