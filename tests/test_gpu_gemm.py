@@ -309,6 +309,42 @@ def test_exact_skinny_no_workspace(mm, cuda, shape):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
+@pytest.mark.parametrize("case", [
+    (4095, 4111, 4095, 0, 0), (4096, 5120, 4096, 0, 0), (4096, 5121, 4096, 0, 0), (17, 1, 17, 0, 0),
+    (9, 129, 9, 0, 0), (8, 8, 8, 0, 0), (7, 300, 8, 0, 0), (3, 50, 3, 0, 0), (4801, 2000, 4801, 1, 1),
+    (4095, 4111, 4103, 1, 0), (16 * 300 + 5, 127, 16 * 300 + 8, 0, 1), (60000, 4096, 60000, 0, 0)],
+    ids=lambda c: "N{}-K{}-ldb{}-A{}-B{}".format(*c))
+@pytest.mark.parametrize("ws", [None, False], ids=["workspace", "no_workspace"])
+def test_exact_one_row(mm, cuda, case, ws):
+    """M = 1 (decode-shaped GEMV, the ragged configuration's remainder row) on the streaming
+    kernels: N and K tails (odd K: A's last element shares a dword with the byte after A), B rows
+    padded with NaN (ldb > N), A and B starting one element past a 16-byte boundary, N below one
+    strip, several rounds of strips, with and without a workspace, C confined to its view.
+    Integer inputs, bit-exact against the int64 product."""
+    torch = cuda
+    N, K, ldb, a_off, b_off = case
+    rng = np.random.default_rng(N + 3 * K + ldb)
+    A = rng.integers(-4, 5, size=(1, K)).astype(np.float16)
+    B = rng.integers(-4, 5, size=(K, N)).astype(np.float16)
+    truth = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32)
+    Abuf = torch.zeros(K + a_off, dtype=torch.float16, device="cuda")
+    Abuf[a_off:] = to_dev(torch, A)[0]
+    Ad = Abuf[a_off:].view(1, K)
+    Bbuf = torch.full((K * ldb + b_off,), float("nan"), dtype=torch.float16, device="cuda")
+    Bd = Bbuf[b_off:].view(K, ldb)[:, :N]
+    Bd.copy_(to_dev(torch, B))
+    Cbuf = torch.full((N + 8,), -1.0, dtype=torch.float32, device="cuda")
+    Cv = Cbuf[4:4 + N].view(1, N)
+    print(f"[one_row] N={N} K={K} ldb={ldb} A+{a_off} B+{b_off} ws={ws is None} plan {mm.gemm_plan(1, N, K, ldb=ldb)}",
+          flush=True)
+    mm.gemm(Ad, Bd, Cv, workspace=ws)
+    torch.cuda.synchronize()
+    Cb = Cbuf.cpu().numpy()
+    assert np.all(Cb[:4] == -1.0) and np.all(Cb[4 + N:] == -1.0), "wrote outside the C view"
+    C = Cb[4:4 + N].reshape(1, N)
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
+
+
 @pytest.mark.parametrize("shape", [(16 * 256 + 1, 4096, 264), (16 * 256 + 40, 4096, 264), (16 * 256 + 64, 4096, 1000),
                                    (16 * 256 + 17, 4095, 523)],
                          ids=lambda s: "x".join(map(str, s)))
