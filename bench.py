@@ -70,6 +70,10 @@ WORKLOADS = {
     # measured ceilings (library probes): the 8192^3 tile kernel's MFMA stream with register-
     # resident operands, and streaming reads of 1 GiB (plain loads / direct to LDS)
     "mfma_ceiling": (8192, 8192, 8192, "mfma_ceiling", 1, "uniform"),
+    # the same kernel's fragment reads and MFMAs on operands already in LDS (no operand loads or C
+    # stores), with and without its one workgroup barrier per K tile
+    "lds_mfma": (8192, 8192, 8192, "lds_mfma", 1, "uniform"),
+    "lds_mfma_nobarrier": (8192, 8192, 8192, "lds_mfma_nobarrier", 1, "uniform"),
     "read_ceiling": (1 << 30, 1, 1, "read", 0, "uniform"),
     "read_ceiling_lds": (1 << 30, 1, 1, "read_lds", 0, "uniform"),
 }
@@ -89,6 +93,11 @@ DESCRIPTIONS = {
     "copy": "copy 256 MiB fp32 device-to-device (counter scaling reference), zeros",
     "mfma_ceiling": "MFMA ceiling probe: the 8192x8192x8192 persistent tile kernel's MFMA stream and C stores with "
                     "register-resident operands (no loads, LDS or barriers), U[-1,1) seed 1",
+    "lds_mfma": "operand-path probe: the 8192x8192x8192 persistent tile kernel's fragment reads and MFMAs on "
+                "operands staged in LDS once, with its per-K-tile barrier (no operand loads, no C stores), "
+                "U[-1,1) seed 1",
+    "lds_mfma_nobarrier": "operand-path probe: the 8192x8192x8192 persistent tile kernel's fragment reads and MFMAs "
+                          "on operands staged in LDS once, no barrier (no operand loads, no C stores), U[-1,1) seed 1",
     "read_ceiling": "HBM read ceiling probe: one pass over 1 GiB with 16-byte loads into registers, zeros",
     "read_ceiling_lds": "HBM read ceiling probe: one pass over 1 GiB with direct-to-LDS 16-byte loads, zeros",
 }
@@ -150,6 +159,25 @@ def make_workload(name, torch, mmm, tile=None):
 
         return {"launch": lambda: mmm.probe_mfma_ceiling(A, B, Cd), "witness": None, "host_inputs": None,
                 "clocked": clocked, "M": M, "N": N, "K": K}
+    if kind in ("lds_mfma", "lds_mfma_nobarrier"):
+        A = torch.empty((M, K), dtype=torch.float16, device=dev)
+        B = torch.empty((K, N), dtype=torch.float16, device=dev)
+        fill(A, seed, 0)
+        fill(B, seed, 1)
+        out = torch.empty(256 * 512, dtype=torch.float32, device=dev)
+        barrier = kind == "lds_mfma"
+
+        def clocked(clock):
+            st = {"i": 0}
+
+            def run():
+                mmm.probe_lds_mfma(A, B, out, barrier=barrier, clock=clock[st["i"] % clock.shape[0]])
+                st["i"] += 1
+
+            return run
+
+        return {"launch": lambda: mmm.probe_lds_mfma(A, B, out, barrier=barrier), "witness": None,
+                "host_inputs": None, "clocked": clocked, "M": M, "N": N, "K": K}
     if kind == "contraction_ref":
         mt, bt, rt, nt, rt_l = REFERENCE_DIMS[name]
         assert (mt * rt, bt, nt * rt_l) == (M, N, K)
@@ -412,7 +440,8 @@ def run_workload(name, torch, mmm, steps, warmup, with_cpu, with_witness, with_c
         tf = flops / (clk["ms_per_launch"] * 1e-3) / 1e12
         clk["tflops"] = round(tf, 1)
         clk["pct_peak_at_clock"] = round(100.0 * tf / (256 * 4096 * clk["sclk_mhz"] * 1e6 / 1e12), 2)
-        entry = {"mfma_ceiling": "mmm_probe_mfma_ceiling"}.get(name, "mmm_gemm_f16f32_clocked")
+        entry = {"mfma_ceiling": "mmm_probe_mfma_ceiling", "lds_mfma": "mmm_probe_lds_mfma",
+                 "lds_mfma_nobarrier": "mmm_probe_lds_mfma"}.get(name, "mmm_gemm_f16f32_clocked")
         clk["method"] = (f"in-kernel: workgroup 0's s_memtime / s_memrealtime at its start and end ({entry}), "
                          "over `launches` launches right after the timed region; "
                          "tflops and pct_peak_at_clock are those launches' own")
@@ -484,6 +513,78 @@ def steady_state(name, torch, mmm, seconds: float):
     if W.get("clocked"):
         out["clock"] = clocked_pass(torch, mmm, W, 20)
     return out
+
+
+# the 8192^3 kernel and the probes that take its parts away, in the order of the table
+DECOMPOSE = [
+    ("gemm8192", "the library's kernel (mmm_gemm_f16f32)", "operand loads (HBM/L2 -> LDS), barrier, LDS fragment "
+     "reads, MFMAs, C stores"),
+    ("lds_mfma", "mmm_probe_lds_mfma, barrier = 1", "barrier, LDS fragment reads, MFMAs"),
+    ("lds_mfma_nobarrier", "mmm_probe_lds_mfma, barrier = 0", "LDS fragment reads, MFMAs"),
+    ("mfma_ceiling", "mmm_probe_mfma_ceiling", "MFMAs on register operands, C stores"),
+]
+
+
+def run_decompose(path, torch, mmm, seconds: float, rounds: int = 2):
+    """Steady-state throughput, clock and power of the 8192^3 kernel and of the probes that leave
+    out its operand loads, its barrier and its LDS reads in turn (DECOMPOSE), `rounds` rounds in
+    rotated order, each variant run back to back for `seconds` (steady_state); writes a markdown
+    table to `path`."""
+    rows = {name: [] for name, _, _ in DECOMPOSE}
+    for r in range(rounds):
+        order = DECOMPOSE[r % len(DECOMPOSE):] + DECOMPOSE[:r % len(DECOMPOSE)]
+        for name, _, _ in order:
+            res = steady_state(name, torch, mmm, seconds)
+            _log(f"[decompose] round {r} {name}: {res['tflops']} TFLOP/s, clock {res.get('clock')}, smi {res['smi']}")
+            rows[name].append(res)
+            torch.cuda.empty_cache()
+    flop_per_clk = 256 * 4096  # dense FP16 MFMA: 256 CU x 4096 flop per clock
+
+    def span(vals, fmt):
+        vals = [v for v in vals if isinstance(v, (int, float))]
+        if not vals:
+            return "-"
+        lo, hi = min(vals), max(vals)
+        return fmt.format(lo) if fmt.format(lo) == fmt.format(hi) else fmt.format(lo) + "-" + fmt.format(hi)
+
+    lines = [
+        "| variant | runs | what is left of the kernel | TFLOP/s | in-kernel clock (MHz) | SMU gfxclk (MHz) | "
+        "socket power (W) | MFMA busy at the in-kernel clock |",
+        "|---|---|---|---|---|---|---|---|",
+    ]
+    for name, runs, left in DECOMPOSE:
+        rs = rows[name]
+        tf = [x["tflops"] for x in rs]
+        clk = [x["clock"]["sclk_mhz"] for x in rs if x.get("clock")]
+        smi_clk = [x["smi"].get("gfxclk_mhz") for x in rs]
+        pw = [x["smi"].get("socket_power_w") for x in rs]
+        busy = [x["tflops"] * 1e12 / (flop_per_clk * x["clock"]["sclk_mhz"] * 1e6) for x in rs if x.get("clock")]
+        lines.append(f"| `{name}` | {runs} | {left} | {span(tf, '{:.0f}')} | {span(clk, '{:.0f}')} | "
+                     f"{span(smi_clk, '{:.0f}')} | {span(pw, '{:.0f}')} | {span(busy, '{:.3f}')} |")
+    head = [
+        "# Where the 8192^3 kernel's time goes: the kernel against probes that leave out its parts",
+        "",
+        "Command (repository root on the GPU box):",
+        "",
+        "```",
+        "python3 bench.py " + " ".join(sys.argv[1:]),
+        "```",
+        "",
+        f"Device: {torch.cuda.get_device_name(0)}.  Each variant runs M = N = K = 8192 (2.2e12 flop per launch) "
+        f"back to back for {seconds:g} s per round, {rounds} rounds in rotated order: throughput over the last 40% "
+        "of each run (HIP events), then the SMU's gfx clock and socket power (amdsmi, about one reading a "
+        "second), then the in-kernel shader clock of 20 clock-recording launches (workgroup 0's s_memtime / "
+        "s_memrealtime).  Cells give the range over the rounds.  MFMA busy = TFLOP/s / (256 CU x 4096 flop "
+        "per clock x in-kernel clock).  The probes (include/mmm.h) run the kernel's own code for what they "
+        "keep: `mmm_probe_lds_mfma` its per-K-tile fragment reads and MFMAs at its LDS addresses on two "
+        "K tiles staged once, `mmm_probe_mfma_ceiling` its MFMA stream on register operands.",
+        "",
+    ]
+    text = "\n".join(head + lines) + "\n"
+    with open(path, "w") as f:
+        f.write(text)
+    print(text, file=sys.stderr, flush=True)
+    return rows
 
 
 # shapes of the tile sweep (--sweep): squares, the configs, and tall / wide / deep / shallow cases
@@ -598,6 +699,11 @@ def main() -> int:
     ap.add_argument("--report", metavar="PATH", help="measure every workload and write a JSON report to PATH")
     ap.add_argument("--sweep", metavar="PATH", help="time every tile against the library's pick over a shape "
                                                      "grid and write a markdown table to PATH")
+    ap.add_argument("--decompose", metavar="PATH", help="run the 8192^3 kernel and the probes that leave out its "
+                                                         "operand loads, barrier and LDS reads in the steady state "
+                                                         "and write a markdown table to PATH")
+    ap.add_argument("--decompose-seconds", type=float, default=4.0, metavar="SECONDS",
+                    help="with --decompose: seconds each variant runs back to back per round (two rounds)")
     ap.add_argument("--shape", metavar="MxNxK", help="measure this GEMM (U[-1,1) inputs, seed 7) instead of --workload")
     ap.add_argument("--tile", metavar="BMxBN", help="with --shape: force this block tile (one of the library's six; "
                                                     "default: the library's own pick)")
@@ -624,6 +730,9 @@ def main() -> int:
     if args.sweep:
         run_sweep(args.sweep, torch, mmm, args.steps, args.warmup, with_witness=not args.no_witness,
                   shapes=parse_shapes(args.shapes) if args.shapes else None)
+
+    if args.decompose:
+        run_decompose(args.decompose, torch, mmm, args.decompose_seconds)
 
     if args.report:
         report = []

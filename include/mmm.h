@@ -281,6 +281,17 @@ hipError_t mmm_tile_of_block(int block, int tiles_m, int tiles_n, int* tm, int* 
  *   kernel does, store_tiles == 0 writes one float per thread into C's first 256 * 512 floats.
  *   The values written are not A*B.  M, N multiples of 256, K of 64.  clock (NULL allowed)
  *   receives workgroup 0's start and end counters as mmm_gemm_f16f32_clocked writes them.
+ * mmm_probe_lds_mfma: the same kernel's K loop on operands already in LDS.  Each of
+ *   min(M/256 * N/256, 256) workgroups stages K tiles 0 and 1 of its first 256x256 tile of A
+ *   [M][K] and B [K][N] (contiguous row-major, 16-byte aligned) into the kernel's two LDS ring
+ *   slots once, then runs the kernel's fragment reads and MFMAs for every K tile of its share of
+ *   the tiles (2*M*N*K flops in all), alternating the two slots, without operand loads or C
+ *   stores; barrier != 0 keeps the kernel's one workgroup barrier per K tile.  out (out_floats
+ *   floats, at least min(M/256 * N/256, 256) * 512) receives one float per thread: thread t of
+ *   workgroup g writes out[g * 512 + t], the
+ *   sum of its accumulators; a workgroup's outputs sum to (tiles * K / 128) * (1^T A0)(B0 1),
+ *   tiles its number of output tiles, A0 and B0 its first tile's rows of A and columns of B
+ *   over K 0 .. 127.  M, N multiples of 256, K of 128.  clock as for mmm_probe_mfma_ceiling.
  * mmm_probe_read: streams `bytes` (a multiple of 1024, 16-byte-aligned src) once: with plain
  *   16-byte loads into registers (direct_to_lds == 0; out receives 2048 * 256 words), or with
  *   the tile kernels' direct-to-LDS loads (direct_to_lds != 0, bytes < 2^31; out receives 2048
@@ -289,6 +300,8 @@ hipError_t mmm_tile_of_block(int block, int tiles_m, int tiles_n, int* tm, int* 
 hipError_t mmm_probe_clock(uint64_t* out, int64_t ticks, hipStream_t stream);
 hipError_t mmm_probe_mfma_ceiling(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,
                                   int store_tiles, uint64_t* clock, hipStream_t stream);
+hipError_t mmm_probe_lds_mfma(const mmm_half* A, const mmm_half* B, float* out, int64_t out_floats, int M, int N,
+                              int K, int barrier, uint64_t* clock, hipStream_t stream);
 hipError_t mmm_probe_read(const void* src, int64_t bytes, int direct_to_lds, uint32_t* out, int64_t out_words,
                           hipStream_t stream);
 

@@ -348,6 +348,53 @@ __device__ __forceinline__ void record_clock(uint64_t* clk, int at) {
   }
 }
 
+// K-steps 0 .. KSTEPS-2 of the K tile in LDS stage `st`: each step's MFMAs (fragments f[kk & 1])
+// run while the next step's fragments are read into f[(kk + 1) & 1]; MFMA i carries fragment
+// read i, and scheduling fences keep that order.
+template <class T, bool BKM>
+__device__ __forceinline__ void ktile_body(const char LDS_AS* st, const uint32_t (&a_off)[kMaxOff],
+                                           const uint32_t (&b_off)[kMaxOff], Frags<T> (&f)[2],
+                                           AccT<T> (&acc)[T::FM][T::FN]) {
+#pragma unroll
+  for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
+#pragma unroll
+    for (int i = 0; i < T::FM * T::FN; ++i) {
+      mfma_one<T>(f[kk & 1].b[ord_nb<T>(i)], f[kk & 1].a[ord_mb<T>(i)], acc[ord_mb<T>(i)][ord_nb<T>(i)]);
+      if (i < T::FM + T::FN) load_frag_unit<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, i, f[(kk + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
+// The last K-step of a K tile, after the barrier that publishes the next one in stage `ns`: its
+// MFMAs (fragments f[1]) carry the next stage's first fragment reads (into f[0], MFMA i carrying
+// read i) and the LPT refill loads dma_one(d, 0 .. LPT-1), spread evenly over the MFMAs after the
+// reads when there are enough of them (every load is a 1 KB request to the address unit, and all
+// waves refill in the same K-step, so a burst of them fills its queue and stalls each wave's
+// MFMAs behind its next load).  Measured on the 256x256 tile (32 MFMAs, 8 loads) at 8192^3: one
+// load every MFMA 1258 TFLOP/s, every 2 within 1%, every 3 +1%, every 4 (the even spread) +4.4%.
+template <class T, bool BKM, class D, class DmaOne>
+__device__ __forceinline__ void ktile_last_step(const char LDS_AS* ns, const uint32_t (&a_off)[kMaxOff],
+                                                const uint32_t (&b_off)[kMaxOff], Frags<T> (&f)[2],
+                                                AccT<T> (&acc)[T::FM][T::FN], const D& d, DmaOne&& dma_one) {
+  constexpr int NM = T::FM * T::FN, NU = T::FM + T::FN;
+  constexpr int NL = T::LPT;
+  constexpr int DS = NM / NL > 1 ? NM / NL : 1;  // MFMAs between loads
+  constexpr int D0 = NM - DS * NL >= NU ? NU : (NM > DS * NL ? NM - DS * NL : 0);
+  int issued = 0;
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    const int mb = ord_mb<T>(i), nb = ord_nb<T>(i);
+    mfma_one<T>(f[1].b[nb], f[1].a[mb], acc[mb][nb]);
+    if (i < NU) load_frag_unit<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, i, f[0]);
+    if (i >= D0 && (i - D0) % DS == 0 && issued < NL) dma_one(d, issued++);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int j = 0; j < NL; ++j)
+    if (j >= issued) dma_one(d, j);
+}
+
 // Cross-stage K loop over KT K tiles (the direct-to-LDS kernels).  The caller supplies the
 // loads: prep(t, slot) builds the per-tile load state of K tile t for ring slot `slot` (and
 // advances any running state: tiles are prepared in order), dma_one(d, j) issues load j of
@@ -388,19 +435,7 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
   int cur = 0;
   // K-steps 0 .. KSTEPS-2 of the tile in slot `cur` (each step's MFMAs run while the next
   // step's fragments are read).
-  auto tile_body = [&] {
-    const char LDS_AS* st = lds_base + cur * T::STAGE;
-#pragma unroll
-    for (int kk = 0; kk + 1 < T::KSTEPS; ++kk) {
-      // MFMA i of this step carries fragment read i of the next
-#pragma unroll
-      for (int i = 0; i < T::FM * T::FN; ++i) {
-        mfma_one<T>(f[kk & 1].b[ord_nb<T>(i)], f[kk & 1].a[ord_mb<T>(i)], acc[ord_mb<T>(i)][ord_nb<T>(i)]);
-        if (i < T::FM + T::FN) load_frag_unit<T, BKM>(st, st + T::A_BYTES, a_off, b_off, kk + 1, i, f[(kk + 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  };
+  auto tile_body = [&] { ktile_body<T, BKM>(lds_base + cur * T::STAGE, a_off, b_off, f, acc); };
   // Last K-step of tile t < KT-1: publish tile t+1, read its first fragments, refill the
   // retired slot (`refill` loads tile t+S into slot `cur`), then the MFMAs.
   auto tile_next = [&](int t, auto&& refill) {
@@ -418,37 +453,14 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
     cur = nslot;
   };
   // Steady state: after the barrier the next tile's first fragment reads and the refill's
-  // loads are interleaved with the last K-step's MFMAs (scheduling fences keep the order), so
-  // neither a burst of LDS reads nor a burst of load issue leaves the matrix pipe idle.
-  // MFMA i carries fragment read i (i < FM + FN), and the DMA loads go on the MFMAs after the
-  // reads when there are enough of them, spread evenly: all waves refill in the same K-step and
-  // every load is a 1 KB request to the address unit, so a burst of them fills its queue and
-  // stalls each wave's MFMAs behind its next load.  Measured on the 256x256 tile (32 MFMAs, 8
-  // loads) at 8192^3: one load every MFMA 1258 TFLOP/s, every 2 within 1%, every 3 +1%, every 4
-  // (the even spread) +4.4%.
+  // loads are interleaved with the last K-step's MFMAs (ktile_last_step), so neither a burst of
+  // LDS reads nor a burst of load issue leaves the matrix pipe idle.
   auto tile_next_interleaved = [&](int t) {
     __builtin_amdgcn_sched_barrier(0);  // the body's MFMAs stay ahead of the waits
     wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(S - 2);  // steady state: S-2 tiles after t+1 in flight
     block_sync();
     const int nslot = cur + 1 == S ? 0 : cur + 1;
-    const char LDS_AS* ns = lds_base + nslot * T::STAGE;
-    constexpr int NM = T::FM * T::FN, NU = T::FM + T::FN;
-    constexpr int NL = T::LPT;
-    constexpr int DS = NM / NL > 1 ? NM / NL : 1;  // MFMAs between loads
-    constexpr int D0 = NM - DS * NL >= NU ? NU : (NM > DS * NL ? NM - DS * NL : 0);
-    const auto d = prep(t + S, cur);
-    int issued = 0;
-#pragma unroll
-    for (int i = 0; i < NM; ++i) {
-      const int mb = ord_mb<T>(i), nb = ord_nb<T>(i);
-      mfma_one<T>(f[1].b[nb], f[1].a[mb], acc[mb][nb]);
-      if (i < NU) load_frag_unit<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, i, f[0]);
-      if (i >= D0 && (i - D0) % DS == 0 && issued < NL) dma_one(d, issued++);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int j = 0; j < NL; ++j)
-      if (j >= issued) dma_one(d, j);
+    ktile_last_step<T, BKM>(lds_base + nslot * T::STAGE, a_off, b_off, f, acc, prep(t + S, cur), dma_one);
     cur = nslot;
   };
   // steady state refills by DMA only; the refill of the last tile (possibly gathered
@@ -1837,6 +1849,123 @@ static bool persistent_ok(const GemmProblem& p) {
 static int64_t launch_blocks(const GemmProblem& p, int bm, int bn) {
   const int64_t tiles = (int64_t)((p.M + bm - 1) / bm) * ((p.N + bn - 1) / bn);
   return p.k_splits > 1 ? tiles - p.split_tiles + (int64_t)p.split_tiles * p.k_splits : tiles;
+}
+
+// ------------------------------------------------------------------------------------
+// Operand-path probe (measurement only; entry point mmm_probe_lds_mfma).  The persistent 256x256
+// kernel's K loop on operands that are already in LDS: each workgroup stages K tiles 0 and 1 of
+// its first output tile into the two ring slots once (the kernels' staging map), then runs the
+// kernel's own per-K-tile code -- ktile_body and ktile_last_step: the same MFMAs and fragment
+// reads, at the same LDS addresses, in the same order -- over as many K tiles as its share of the
+// M x N x K problem holds, alternating the slots as the ring does.  Left out: the refill loads (the
+// last step's load hook is empty), their waits and the C stores.  With BARRIER the workgroup
+// barrier stays where the kernel publishes the next K tile; without it the waves run
+// unsynchronised (nothing writes the LDS after the staging, so nothing races).  Each thread
+// writes the sum of its accumulators at the end.  A workgroup's accumulators see slot 0 (K 0..63
+// of its first tile) and slot 1 (K 64..127) total/2 = tiles * K / 128 times each, so the sum of
+// its threads' outputs is (total / 2) * (1^T A0)(B0 1), A0 = A[m0 .. m0+255][0 .. 127],
+// B0 = B[0 .. 127][n0 .. n0+255] (exact for small integer inputs).
+// ------------------------------------------------------------------------------------
+template <class T, bool BARRIER>
+__global__ __launch_bounds__(T::NT, T::OCC) void lds_mfma_probe_kernel(GemmProblem p, int tiles_m, int tiles_n,
+                                                                       float* out) {
+  __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
+  static_assert(T::STAGES == 2 && T::B_UNIFORM, "two ring slots, the uniform staging map");
+  record_clock(p.clk, 0);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w / T::WGN, wn = w % T::WGN;
+  const int K = p.K;
+  const int64_t lda = p.lda, ldb = p.ldb;
+  char LDS_AS* lds_base = (char LDS_AS*)lds;
+
+  // staging of K tiles 0 and 1 of the first output tile, as the kernels stage them (thread
+  // (w, lane) moves chunk slot r * NT + w * 64 + lane of each operand's rounds r)
+  constexpr int RPA = T::NT / T::CA, RPB = T::NT / T::CB;
+  int tm, tn;
+  tile_of_block(blockIdx.x, tiles_m, tiles_n, 4, &tm, &tn);
+  const int m0 = __builtin_amdgcn_readfirstlane(tm * T::BM), n0 = __builtin_amdgcn_readfirstlane(tn * T::BN);
+  {
+    const int a_row0 = w * (64 / T::CA) + lane / T::CA;
+    const int a_kc = 8 * ((lane % T::CA) ^ T::swz_a(a_row0));
+    const int b_row0 = w * (64 / T::CB) + lane / T::CB;
+    const int b_nc = 8 * ((lane % T::CB) ^ T::swz_bk(b_row0));
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const i32x4 ra = make_rsrc(p.A + (int64_t)m0 * lda + s * T::BK,
+                                 clip_records(((int64_t)(p.M - 1 - m0) * lda + K - s * T::BK) * 2));
+      const i32x4 rb = make_rsrc(p.B + (int64_t)s * T::BK * ldb + n0,
+                                 clip_records(((int64_t)(K - 1 - s * T::BK) * ldb + p.N - n0) * 2));
+      const uint32_t a_dst = lds_addr_of(lds_base) + s * T::STAGE + w * 64 * 16, b_dst = a_dst + T::A_BYTES;
+#pragma unroll
+      for (int r = 0; r < T::RA; ++r)
+        dma_b128(a_dst + r * T::NT * 16, ra, (uint32_t)(((a_row0 + r * RPA) * lda + a_kc) * 2));
+#pragma unroll
+      for (int r = 0; r < T::RB; ++r)
+        dma_b128(b_dst + r * T::NT * 16, rb, (uint32_t)(((b_row0 + r * RPB) * ldb + b_nc) * 2));
+    }
+    wait_vmcnt<0>();
+  }
+  block_sync();
+
+  // fragment read offsets (as gemm_nn_kernel)
+  uint32_t a_off[kMaxOff] = {};
+#pragma unroll
+  for (int kk = 0; kk < T::KSTEPS; ++kk)
+#pragma unroll
+    for (int ph = 0; ph < T::APAR; ++ph) {
+      const int m = wm * T::TM + ph * T::MF + (lane % T::MF);
+      const int chunk = (T::KK / 8) * kk + lane / T::MF;
+      a_off[kk * T::APAR + ph] = m * T::BK * 2 + (chunk ^ T::swz_a(m)) * 16;
+    }
+  uint32_t b_off[kMaxOff] = {};
+  {
+    const int k = 8 * (lane / T::MF) + ((lane >> 2) & 3);
+#pragma unroll
+    for (int nb = 0; nb < T::FN; ++nb) {
+      const int n = wn * T::TN + 16 * nb + 4 * (lane & 3);
+      b_off[nb] = k * T::BN * 2 + (((n >> 3) ^ T::swz_bk(k)) * 16) + (n & 7) * 2;
+    }
+  }
+  static_assert(T::MF == 16, "the 16x16x32 tile's fragment map");
+
+  // this workgroup's K tiles: its output tiles b, b + grid, ... times K / BK each
+  const int mine = (tiles_m * tiles_n - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int total = __builtin_amdgcn_readfirstlane(mine * (K / T::BK));
+  AccT<T> acc[T::FM][T::FN];
+#pragma unroll
+  for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) acc[i][j] = AccT<T>{};
+  Frags<T> f[2];
+  load_frags<T, false>(lds_base, lds_base + T::A_BYTES, a_off, b_off, 0, f[0]);
+  int cur = 0;
+  for (int t = 0; t < total; ++t) {
+    ktile_body<T, false>(lds_base + cur * T::STAGE, a_off, b_off, f, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (BARRIER) block_sync();
+    cur ^= 1;
+    ktile_last_step<T, false>(lds_base + cur * T::STAGE, a_off, b_off, f, acc, 0, [](int, int) {});
+  }
+  float keep = 0.0f;
+#pragma unroll
+  for (int i = 0; i < T::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < T::FN; ++j) keep += acc[i][j][0] + acc[i][j][1] + acc[i][j][2] + acc[i][j][3];
+  out[(int64_t)blockIdx.x * T::NT + tid] = keep;
+  record_clock(p.clk, 2);
+}
+
+hipError_t launch_lds_mfma_probe(const GemmProblem& p, bool barrier, float* out, hipStream_t stream) {
+  using T = Tile256;
+  const int tiles_m = p.M / T::BM, tiles_n = p.N / T::BN;
+  const int64_t tiles = (int64_t)tiles_m * tiles_n;
+  const int grid = (int)(tiles < 256 ? tiles : 256);
+  if (barrier)
+    hipLaunchKernelGGL((lds_mfma_probe_kernel<T, true>), dim3(grid), dim3(T::NT), 0, stream, p, tiles_m, tiles_n, out);
+  else
+    hipLaunchKernelGGL((lds_mfma_probe_kernel<T, false>), dim3(grid), dim3(T::NT), 0, stream, p, tiles_m, tiles_n, out);
+  return hipGetLastError();
 }
 
 bool gemm_nn_persistent(const GemmProblem& p0, int tile_id) {

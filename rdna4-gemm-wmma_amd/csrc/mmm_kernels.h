@@ -73,6 +73,9 @@ bool gemm_nn_persistent(const GemmProblem& p, int tile_id);  // launch as the pe
 size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id);
 constexpr size_t kMaxWorkspaceBytes = (size_t)64 << 20;
 hipError_t launch_gemm_fold(const FoldProblem& p, hipStream_t stream);
+// The operand-path probe (lds_mfma_probe_kernel): M, N multiples of 256, K of 128, row-major A
+// and B 16-byte aligned (lda = K, ldb = N); out holds min(M/256 * N/256, 256) * 512 floats.
+hipError_t launch_lds_mfma_probe(const GemmProblem& p, bool barrier, float* out, hipStream_t stream);
 // Rows of C up to which the streaming kernels take a GEMM (the kernels handle up to 64).
 constexpr int kStreamMaxRows = 64;
 static_assert(kStreamMaxRows >= 16 && kStreamMaxRows <= 64, "streaming kernels take 16 to 64 rows");

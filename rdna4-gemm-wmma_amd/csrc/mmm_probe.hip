@@ -1,5 +1,7 @@
 // Measurement probes: the shader clock, and what the MI355X sustains under its power limit
-// with the tile kernel's MFMA stream alone (no operand traffic) and with pure HBM streaming.
+// with the tile kernel's MFMA stream alone (no operand traffic), with its MFMAs and LDS fragment
+// reads on operands already in LDS (lds_mfma_probe_kernel, beside the tile kernels), and with
+// pure HBM streaming.
 // They give the GEMM's roofline fractions a measured denominator next to the spec peaks.  No
 // counterpart in the reference, which reports only ms and GFLOPS (mmm.cpp:1503-1504).
 #include <hip/hip_runtime.h>
@@ -176,6 +178,24 @@ hipError_t mmm_probe_mfma_ceiling(const mmm_half* A, const mmm_half* B, float* C
   hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(grid), dim3(512), 0, stream, A, B, C, M, N, K, store_tiles ? 1 : 0,
                      clock);
   return hipGetLastError();
+}
+
+hipError_t mmm_probe_lds_mfma(const mmm_half* A, const mmm_half* B, float* out, int64_t out_floats, int M, int N,
+                              int K, int barrier, uint64_t* clock, hipStream_t stream) {
+  if (!A || !B || !out || M <= 0 || N <= 0 || K <= 0 || ((uintptr_t)clock & 7)) return hipErrorInvalidValue;
+  if (M % 256 || N % 256 || K % 128 || ((uintptr_t)A & 15) || ((uintptr_t)B & 15)) return hipErrorInvalidValue;
+  // the staging reads rows m0 .. m0+255 of A and rows 0 .. 127 of B through 32-bit buffer offsets
+  if ((int64_t)255 * K + 128 >= (int64_t)kOobOffset / 2 || (int64_t)127 * N + 256 >= (int64_t)kOobOffset / 2 ||
+      (int64_t)(M / 256) * (N / 256) > 0x7fffffff)
+    return hipErrorInvalidValue;
+  const int64_t tiles = (int64_t)(M / 256) * (N / 256);
+  if (out_floats < (tiles < 256 ? tiles : 256) * 512) return hipErrorInvalidValue;
+  GemmProblem p{};
+  p.A = A, p.B = B, p.C = nullptr;
+  p.M = M, p.N = N, p.K = K;
+  p.lda = K, p.ldb = N, p.ldc = N;
+  p.clk = clock;
+  return launch_lds_mfma_probe(p, barrier != 0, out, stream);
 }
 
 hipError_t mmm_probe_read(const void* src, int64_t bytes, int direct_to_lds, uint32_t* out, int64_t out_words,

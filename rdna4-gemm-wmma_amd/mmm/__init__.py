@@ -129,13 +129,14 @@ def lib() -> C.CDLL:
     L.mmm_gemm_plan_f16f32.argtypes = [p, p, p, i, i, i, i64, i64, i64, C.POINTER(GemmPlan)]
     L.mmm_probe_clock.argtypes = [p, i64, s]
     L.mmm_probe_mfma_ceiling.argtypes = [p, p, p, i, i, i, i, p, s]
+    L.mmm_probe_lds_mfma.argtypes = [p, p, p, i64, i, i, i, i, p, s]
     L.mmm_probe_read.argtypes = [p, i64, i, p, i64, s]
     for name in ("mmm_gemm_f16f32", "mmm_gemm_f16f32_ws", "mmm_gemm_f16f32_clocked", "mmm_gemm_f16f32_noalloc", "mmm_gemm_workspace_f16f32", "mmm_gemm_f16f32_tiled",
                  "mmm_contract_desc_baseline", "mmm_contract_desc_reference", "mmm_contract5d_f16f32",
                  "mmm_contract5d_f16f32_ws", "mmm_contract5d_workspace_f16f32", "mmm_fill_uniform_f16",
                  "mmm_fill_normal_f16", "mmm_tile_of_block", "mmm_gemm_naive_f16f32", "mmm_gemm_truth_f64",
                  "mmm_contract5d_truth_f64", "mmm_gemm_plan_f16f32", "mmm_probe_clock", "mmm_probe_mfma_ceiling",
-                 "mmm_probe_read"):
+                 "mmm_probe_lds_mfma", "mmm_probe_read"):
         getattr(L, name).restype = C.c_int
     L.mmm_version.restype = C.c_char_p
     L.mmm_version.argtypes = []
@@ -495,6 +496,29 @@ def probe_mfma_ceiling(A, B, C_out, store_tiles: bool = True, stream=None, clock
     _check("mmm_probe_mfma_ceiling", lib().mmm_probe_mfma_ceiling(_ptr(A), _ptr(B), _ptr(C_out), M, N, K,
                                                                   1 if store_tiles else 0, ck, _stream(stream)))
     return C_out
+
+
+def probe_lds_mfma(A, B, out=None, barrier: bool = True, stream=None, clock=None):
+    """The persistent 256x256 tile kernel's fragment reads and MFMAs on operands already in LDS
+    (see include/mmm.h); 2*M*N*K flops per call, no operand loads or C stores.  Returns the
+    per-thread outputs (float32, min(M/256 * N/256, 256) * 512 of them).  ``clock``: None, or a
+    CUDA int64 tensor of 4 elements receiving workgroup 0's start and end counters."""
+    import torch
+
+    _check_f16("A", A)
+    _check_f16("B", B)
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[0] or not (A.is_contiguous() and B.is_contiguous()):
+        raise ValueError("A must be a contiguous [M,K] and B a contiguous [K,N] tensor")
+    M, K = A.shape
+    N = B.shape[1]
+    if out is None:
+        out = torch.empty(min((M // 256) * (N // 256), 256) * 512, dtype=torch.float32, device=A.device)
+    if out.dtype != torch.float32 or not out.is_cuda or not out.is_contiguous():
+        raise TypeError("out must be a contiguous CUDA float32 tensor")
+    ck = C.c_void_p(clock.data_ptr()) if clock is not None else None
+    _check("mmm_probe_lds_mfma", lib().mmm_probe_lds_mfma(_ptr(A), _ptr(B), _ptr(out), out.numel(), M, N, K,
+                                                          1 if barrier else 0, ck, _stream(stream)))
+    return out
 
 
 def probe_read(src, out, direct_to_lds: bool = False, stream=None):

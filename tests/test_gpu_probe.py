@@ -47,6 +47,59 @@ def test_probe_mfma_ceiling_runs(mm, cuda):
         mm.probe_mfma_ceiling(A[:, :96], B[:96], C)  # K % 64 != 0
 
 
+@pytest.mark.parametrize("shape", [(256, 256, 128), (512, 768, 512), (8192, 8192, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_probe_lds_mfma_closed_form(mm, cuda, shape):
+    """The operand-path probe streams every K tile of its workgroups' shares through the tile
+    kernel's fragment reads and MFMAs: on inputs in {-1, 0, 1} each workgroup's outputs sum
+    exactly to (tiles * K / 128) * (1^T A0)(B0 1), A0 / B0 its first tile's rows of A and columns
+    of B over K 0 .. 127 (the two staged K tiles), with and without the per-K-tile barrier, and
+    the barrier changes no bit of any output."""
+    torch = cuda
+    M, N, K = shape
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(M + N + K)
+    A = torch.randint(-1, 2, (M, K), generator=gen, device="cuda", dtype=torch.int8).to(torch.float16)
+    B = torch.randint(-1, 2, (K, N), generator=gen, device="cuda", dtype=torch.int8).to(torch.float16)
+    tiles_m, tiles_n = M // 256, N // 256
+    tiles = tiles_m * tiles_n
+    grid = min(tiles, 256)
+    print(f"[probe_lds_mfma] {M}x{N}x{K} grid {grid}", flush=True)
+    outs = {}
+    for barrier in (True, False):
+        out = torch.full((grid * 512 + 64,), float("nan"), dtype=torch.float32, device="cuda")
+        mm.probe_lds_mfma(A, B, out, barrier=barrier)
+        torch.cuda.synchronize()
+        assert torch.isnan(out[grid * 512:]).all(), "wrote past its outputs"
+        outs[barrier] = out[: grid * 512].cpu().numpy().astype(np.float64).reshape(grid, 512)
+    assert np.array_equal(outs[True], outs[False])
+    Ah = A.float().cpu().numpy().astype(np.int64)
+    Bh = B.float().cpu().numpy().astype(np.int64)
+    for g in range(grid):
+        tm, tn = mm.tile_of_block(g, tiles_m, tiles_n)
+        mine = (tiles - g + grid - 1) // grid
+        a_rows = Ah[tm * 256:(tm + 1) * 256, :128].sum(axis=0)
+        b_cols = Bh[:128, tn * 256:(tn + 1) * 256].sum(axis=1)
+        want = mine * K // 128 * int(a_rows @ b_cols)
+        assert outs[True][g].sum() == want, f"workgroup {g} (tile {tm},{tn}): {outs[True][g].sum()} != {want}"
+
+
+def test_probe_lds_mfma_rejects(mm, cuda):
+    """Shapes outside the probe's grid (K not a multiple of 128, M not of 256) and an output
+    buffer shorter than one float per thread are refused before any launch."""
+    A = cuda.zeros((512, 256), dtype=cuda.float16, device="cuda")
+    B = cuda.zeros((256, 512), dtype=cuda.float16, device="cuda")
+    with pytest.raises(mm.MMMError):
+        mm.probe_lds_mfma(A[:, :192].contiguous(), B[:192].contiguous())  # K % 128 != 0
+    with pytest.raises(mm.MMMError):
+        mm.probe_lds_mfma(A[:300].contiguous(), B)  # M % 256 != 0
+    short = cuda.empty(4 * 512 - 1, dtype=cuda.float32, device="cuda")
+    with pytest.raises(mm.MMMError):
+        mm.probe_lds_mfma(A, B, short)
+    with pytest.raises(ValueError):
+        mm.probe_lds_mfma(A[:, :128], B[:128])  # not contiguous
+
+
 @pytest.mark.parametrize("lds", [False, True])
 def test_probe_read_runs(mm, cuda, lds):
     """The streaming-read probe reads every byte: an all-zero buffer XOR-folds to zeros, and a
