@@ -1122,6 +1122,49 @@ def _dev_ints(torch, gen, shape):
     return torch.randint(-4, 5, shape, generator=gen, device="cuda", dtype=torch.int8).to(torch.float16)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_exact_random_large(mm, cuda, seed):
+    """Random problems of 200 .. 6000 rows and columns and 1 .. 3000 deep, where the planner picks
+    among persistent grids, K-split last rounds, the six tiles and the tile+stream split (the plan
+    is printed), on views with random row pitches and one-element base offsets, with the
+    wrapper's workspace or none: bit-exact against a device fp64 product, confined to C."""
+    torch = cuda
+    rng = np.random.default_rng(9000 + seed)
+    M, N = (int(x) for x in rng.integers(200, 6001, size=2))
+    K = int(rng.integers(1, 3001))
+    pa, pb, pc = (int(x) for x in rng.integers(0, 9, size=3))
+    oa, ob, oc = (int(x) for x in rng.integers(0, 2, size=3))
+    if seed % 4 in (0, 2):  # aligned views (16-byte rows and bases)
+        pa, pb, pc = (8 * int(x) for x in rng.integers(0, 2, size=3))
+        oa = ob = oc = 0
+    if seed % 4 == 0:  # a few rows past whole 256-row tiles: the tile+stream split
+        M = 256 * int(rng.integers(12, 24)) + int(rng.integers(1, 65))
+        N = 256 * int(rng.integers(12, 24))
+        K = 64 * int(rng.integers(16, 48))
+    elif seed % 4 == 2:  # whole 256 x 256 tiles over more than one round: the persistent grids
+        M, N = (256 * int(x) for x in rng.integers(17, 24, size=2))
+        K = 64 * int(rng.integers(4, 48))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    Abig = _dev_ints(torch, gen, (M, K + pa + oa))
+    Bbig = _dev_ints(torch, gen, (K, N + pb + ob))
+    Ad, Bd = Abig[:, oa:oa + K], Bbig[:, ob:ob + N]
+    Cbig = torch.full((M, N + pc + oc), -1.0, dtype=torch.float32, device="cuda")
+    Cv = Cbig[:, oc:oc + N]
+    ws = None if seed % 2 == 0 else False
+    plan = mm.gemm_plan(M, N, K, lda=Ad.stride(0), ldb=Bd.stride(0), ldc=Cv.stride(0), A=Ad, B=Bd, C_out=Cv)
+    where = f"{M}x{N}x{K} pitches +{pa},+{pb},+{pc} offsets {oa},{ob},{oc} workspace {ws is None}"
+    print(f"[random_large] {where} plan {plan['kernel']} tile {plan['block_m']}x{plan['block_n']} "
+          f"splits {plan['tile_splits']} persistent {plan['tile_persistent']} stream rows {plan['stream_rows']}",
+          flush=True)
+    mm.gemm(Ad, Bd, Cv, workspace=ws)
+    torch.cuda.synchronize()
+    assert bool((Cbig[:, :oc] == -1.0).all()) and bool((Cbig[:, oc + N:] == -1.0).all()), "wrote outside C: " + where
+    _assert_exact_rows(torch, Ad, Bd, Cv, where)
+    del Abig, Bbig, Cbig
+    torch.cuda.empty_cache()
+
+
 def _assert_exact_rows(torch, A, B, C, label, chunk=8192):
     """C (a device view) equals the fp64 product A.B exactly, compared on the device in row chunks
     (integer inputs: every value is an integer below 2^24, exact in fp32 and fp64)."""
