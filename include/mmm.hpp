@@ -2,6 +2,8 @@
 //
 // The reference launches
 //     WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J><<<grid, dim3(32, WAVES_I*WAVES_J)>>>(A, B, C)
+// (and names the same GEMM WMMA_Templated_Base, WMMA_LDS_Padded, WMMA_LDS_Swizzled and GEMM_Naive,
+// all provided below)
 // with the sizes in the compile-time globals DIM_I/DIM_J/DIM_K (mmm.cpp:13-15, 1214-1215,
 // 1461-1472, 1496), and the tensor variant with the packed G (mmmTensor.cpp:44-45, 345-371).
 // Its template parameters fix the block tile: (WAVES_I*WAVE_M*16) x (WAVES_J*WAVE_N*16)
@@ -41,6 +43,35 @@ inline hipError_t WMMA_Swizzled_Full(const mmm_half* A, const mmm_half* B, float
     return mmm_gemm_f16f32(A, B, C, DIM_I, DIM_J, DIM_K, DIM_K, DIM_J, DIM_J, stream);
 }
 
+// The reference's earlier kernels of the same lineage -- WMMA_Templated_Base (mmm.cpp:694-798),
+// WMMA_LDS_Padded (mmm.cpp:821-1002) and WMMA_LDS_Swizzled (mmm.cpp:1018-1198) -- take the same
+// template parameters and compute the same C as WMMA_Swizzled_Full; they differ from it only in
+// how they lay out and read their LDS tiles on RDNA4 (padding, swizzles, hoisted address math).
+// The MI355X kernels have their own layout, so these names run WMMA_Swizzled_Full's kernels, with
+// the same reading of the parameters.
+template <int WAVE_M, int WAVE_N, int WAVES_I, int WAVES_J>
+inline hipError_t WMMA_Templated_Base(const mmm_half* A, const mmm_half* B, float* C, int DIM_I, int DIM_J,
+                                      int DIM_K, hipStream_t stream = nullptr) {
+  return WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>(A, B, C, DIM_I, DIM_J, DIM_K, stream);
+}
+template <int WAVE_M, int WAVE_N, int WAVES_I, int WAVES_J>
+inline hipError_t WMMA_LDS_Padded(const mmm_half* A, const mmm_half* B, float* C, int DIM_I, int DIM_J, int DIM_K,
+                                  hipStream_t stream = nullptr) {
+  return WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>(A, B, C, DIM_I, DIM_J, DIM_K, stream);
+}
+template <int WAVE_M, int WAVE_N, int WAVES_I, int WAVES_J>
+inline hipError_t WMMA_LDS_Swizzled(const mmm_half* A, const mmm_half* B, float* C, int DIM_I, int DIM_J, int DIM_K,
+                                    hipStream_t stream = nullptr) {
+  return WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>(A, B, C, DIM_I, DIM_J, DIM_K, stream);
+}
+
+// The reference's GEMM_Naive (mmm.cpp:52-62): one output per thread, its fp32 sum taken in
+// ascending k, on the device (mmm_gemm_naive_f16f32, the same order bit for bit).
+inline hipError_t GEMM_Naive(const mmm_half* A, const mmm_half* B, float* C, int DIM_I, int DIM_J, int DIM_K,
+                             hipStream_t stream = nullptr) {
+  return mmm_gemm_naive_f16f32(A, B, C, DIM_I, DIM_J, DIM_K, DIM_K, DIM_J, DIM_J, stream);
+}
+
 // Library-chosen kernel (recommended: includes the M <= 64 streaming kernel).  With a workspace
 // of mmm_gemm_workspace_f16f32's size, under-filled launches split K (mmm_gemm_f16f32_ws).
 inline hipError_t WMMA_Auto(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K, int64_t lda,
@@ -73,6 +104,30 @@ inline hipError_t WMMA_Swizzled_Full(HA* A, HB* B, float* C, int DIM_I, int DIM_
                                      hipStream_t stream = nullptr) {
   return WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>((const mmm_half*)A, (const mmm_half*)B, C, DIM_I,
                                                               DIM_J, DIM_K, stream);
+}
+
+template <int WAVE_M, int WAVE_N, int WAVES_I, int WAVES_J, class HA, class HB, if_f16<HA> = 0, if_f16<HB> = 0>
+inline hipError_t WMMA_Templated_Base(HA* A, HB* B, float* C, int DIM_I, int DIM_J, int DIM_K,
+                                      hipStream_t stream = nullptr) {
+  return WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>((const mmm_half*)A, (const mmm_half*)B, C, DIM_I,
+                                                              DIM_J, DIM_K, stream);
+}
+template <int WAVE_M, int WAVE_N, int WAVES_I, int WAVES_J, class HA, class HB, if_f16<HA> = 0, if_f16<HB> = 0>
+inline hipError_t WMMA_LDS_Padded(HA* A, HB* B, float* C, int DIM_I, int DIM_J, int DIM_K,
+                                  hipStream_t stream = nullptr) {
+  return WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>((const mmm_half*)A, (const mmm_half*)B, C, DIM_I,
+                                                              DIM_J, DIM_K, stream);
+}
+template <int WAVE_M, int WAVE_N, int WAVES_I, int WAVES_J, class HA, class HB, if_f16<HA> = 0, if_f16<HB> = 0>
+inline hipError_t WMMA_LDS_Swizzled(HA* A, HB* B, float* C, int DIM_I, int DIM_J, int DIM_K,
+                                    hipStream_t stream = nullptr) {
+  return WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>((const mmm_half*)A, (const mmm_half*)B, C, DIM_I,
+                                                              DIM_J, DIM_K, stream);
+}
+
+template <class HA, class HB, if_f16<HA> = 0, if_f16<HB> = 0>
+inline hipError_t GEMM_Naive(HA* A, HB* B, float* C, int DIM_I, int DIM_J, int DIM_K, hipStream_t stream = nullptr) {
+  return GEMM_Naive((const mmm_half*)A, (const mmm_half*)B, C, DIM_I, DIM_J, DIM_K, stream);
 }
 
 template <class HA, class HB, if_f16<HA> = 0, if_f16<HB> = 0>

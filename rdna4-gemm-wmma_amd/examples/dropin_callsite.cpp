@@ -11,9 +11,12 @@
 //
 // Inputs and output are raw binary files (fp16 bit patterns in, fp32 out) so that a test can
 // generate the operands and check C on its side:
-//   dropin_callsite gemm   M N K            A.bin B.bin C.bin
+//   dropin_callsite gemm   M N K            A.bin B.bin C.bin [kernel]
 //   dropin_callsite tensor mt bt rt nt rt_l G.bin In.bin Out.bin
-// Prints one line: the best of the timed launches in ms (the reference's best-of-N, mmm.cpp:1376-1385).
+// The gemm mode's optional last argument names the kernel (default WMMA_Swizzled_Full; also the
+// lineage's WMMA_Templated_Base, WMMA_LDS_Padded, WMMA_LDS_Swizzled and GEMM_Naive, mmm.cpp:52-62,
+// 694-1215).  Prints one line: the best of the timed launches in ms (the reference's best-of-N,
+// mmm.cpp:1376-1385).
 #include <cstdio>
 #include <cstdlib>
 #include <string_view>
@@ -79,7 +82,8 @@ static float time_best(F&& launch, int nbRun) {
   return best;
 }
 
-static int run_gemm(int DIM_I, int DIM_J, int DIM_K, const char* a_path, const char* b_path, const char* c_path) {
+static int run_gemm(int DIM_I, int DIM_J, int DIM_K, const char* a_path, const char* b_path, const char* c_path,
+                    std::string_view kernel) {
   _Float16 *hA = nullptr, *hB = nullptr, *dA = nullptr, *dB = nullptr;
   float *hC = nullptr, *dC = nullptr;
   const size_t na = (size_t)DIM_I * DIM_K, nb = (size_t)DIM_K * DIM_J, nc = (size_t)DIM_I * DIM_J;
@@ -94,14 +98,26 @@ static int run_gemm(int DIM_I, int DIM_J, int DIM_K, const char* a_path, const c
   HIP_CHECK(hipMemcpy(dA, hA, na * sizeof(_Float16), hipMemcpyHostToDevice));
   HIP_CHECK(hipMemcpy(dB, hB, nb * sizeof(_Float16), hipMemcpyHostToDevice));
 
-  // The reference's launched template parameters (mmm.cpp:1462-1465)
+  // The reference's launched template parameters (mmm.cpp:1462-1465), on the kernel named on the
+  // command line (the reference's main launches one of these names at a time)
   constexpr int WAVE_M = 2, WAVE_N = 2, WAVES_I = 4, WAVES_J = 4;
-  const float best = time_best(
-      [&] { return mmm::WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>(dA, dB, dC, DIM_I, DIM_J, DIM_K); }, 50);
+  auto launch = [&]() -> hipError_t {
+    if (kernel == "WMMA_Swizzled_Full")
+      return mmm::WMMA_Swizzled_Full<WAVE_M, WAVE_N, WAVES_I, WAVES_J>(dA, dB, dC, DIM_I, DIM_J, DIM_K);
+    if (kernel == "WMMA_Templated_Base")
+      return mmm::WMMA_Templated_Base<WAVE_M, WAVE_N, WAVES_I, WAVES_J>(dA, dB, dC, DIM_I, DIM_J, DIM_K);
+    if (kernel == "WMMA_LDS_Padded")
+      return mmm::WMMA_LDS_Padded<WAVE_M, WAVE_N, WAVES_I, WAVES_J>(dA, dB, dC, DIM_I, DIM_J, DIM_K);
+    if (kernel == "WMMA_LDS_Swizzled")
+      return mmm::WMMA_LDS_Swizzled<WAVE_M, WAVE_N, WAVES_I, WAVES_J>(dA, dB, dC, DIM_I, DIM_J, DIM_K);
+    if (kernel == "GEMM_Naive") return mmm::GEMM_Naive(dA, dB, dC, DIM_I, DIM_J, DIM_K);
+    return hipErrorInvalidValue;
+  };
+  const float best = time_best(launch, 50);
 
   HIP_CHECK(hipMemcpy(hC, dC, nc * sizeof(float), hipMemcpyDeviceToHost));
   write_file(c_path, hC, nc);
-  std::printf("gemm %dx%dx%d best %.6f ms\n", DIM_I, DIM_J, DIM_K, best);
+  std::printf("gemm %dx%dx%d %.*s best %.6f ms\n", DIM_I, DIM_J, DIM_K, (int)kernel.size(), kernel.data(), best);
   HIP_CHECK(hipHostFree(hA));
   HIP_CHECK(hipHostFree(hB));
   HIP_CHECK(hipHostFree(hC));
@@ -140,13 +156,15 @@ static int run_tensor(int mt, int bt, int rt, int nt, int rt_l, const char* g_pa
 }
 
 int main(int argc, char** argv) {
-  if (argc == 8 && std::string_view(argv[1]) == "gemm")
-    return run_gemm(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]), argv[5], argv[6], argv[7]);
+  if ((argc == 8 || argc == 9) && std::string_view(argv[1]) == "gemm")
+    return run_gemm(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]), argv[5], argv[6], argv[7],
+                    argc == 9 ? std::string_view(argv[8]) : std::string_view("WMMA_Swizzled_Full"));
   if (argc == 10 && std::string_view(argv[1]) == "tensor")
     return run_tensor(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]), std::atoi(argv[5]),
                       std::atoi(argv[6]), argv[7], argv[8], argv[9]);
   std::fprintf(stderr,
-               "usage: %s gemm M N K A.bin B.bin C.bin\n"
+               "usage: %s gemm M N K A.bin B.bin C.bin [WMMA_Swizzled_Full | WMMA_Templated_Base |\n"
+               "            WMMA_LDS_Padded | WMMA_LDS_Swizzled | GEMM_Naive]\n"
                "       %s tensor mt bt rt nt rt_l G.bin In.bin Out.bin\n",
                argv[0], argv[0]);
   return 2;

@@ -5,7 +5,9 @@ library's Makefile) is the reference's benchmark program shape -- `_Float16*` ho
 buffers, hipMemcpy in, one warm-up, timed launches on the null stream, hipMemcpy out
 (mmm.cpp:1441-1500; mmmTensor.cpp:345-371) -- with the kernel launch replaced by
 `mmm::WMMA_Swizzled_Full<2,2,4,4>(dA, dB, dC, DIM_I, DIM_J, DIM_K)` and
-`mmm::WMMA_Tensor(dG, d_Input, d_Output, mt, bt, rt, nt, rt_l)` from include/mmm.hpp.  Its
+`mmm::WMMA_Tensor(dG, d_Input, d_Output, mt, bt, rt, nt, rt_l)` from include/mmm.hpp (and, by name
+on its command line, the lineage's WMMA_Templated_Base / WMMA_LDS_Padded / WMMA_LDS_Swizzled and
+GEMM_Naive).  Its
 outputs are checked here against the CPU oracle: within the tolerance against the fp64 truth on
 the seeded configuration-1 inputs, bit for bit on integer-valued inputs.
 """
@@ -29,14 +31,14 @@ def _run(args, tmp_path):
     return r.stdout
 
 
-def _gemm(tmp_path, A, B):
+def _gemm(tmp_path, A, B, kernel="WMMA_Swizzled_Full"):
     M, K = A.shape
     N = B.shape[1]
     a, b, c = tmp_path / "A.bin", tmp_path / "B.bin", tmp_path / "C.bin"
     np.ascontiguousarray(A, dtype=np.float16).tofile(a)
     np.ascontiguousarray(B, dtype=np.float16).tofile(b)
-    out = _run(["gemm", M, N, K, a, b, c], tmp_path)
-    assert out.startswith(f"gemm {M}x{N}x{K} best ")
+    out = _run(["gemm", M, N, K, a, b, c, kernel], tmp_path)
+    assert out.startswith(f"gemm {M}x{N}x{K} {kernel} best ")
     C = np.fromfile(c, dtype=np.float32)
     assert C.size == M * N
     return C.reshape(M, N)
@@ -55,6 +57,29 @@ def test_callsite_gemm_config1(orc, tmp_path):
     R = orc.gemm_refkernel_f32(A, B)
     bad, worst = orc.check_tol(C, R.astype(np.float64), S)
     assert bad == 0, f"{bad} outputs outside tolerance of the reference-kernel restatement (worst {worst:.3g})"
+
+
+@pytest.mark.parametrize("kernel", ["WMMA_Templated_Base", "WMMA_LDS_Padded", "WMMA_LDS_Swizzled"])
+def test_callsite_lineage_names(orc, tmp_path, kernel):
+    """The reference's earlier names for the same GEMM (mmm.cpp:694-1198), spelled <2,2,4,4> at
+    configuration 1: every output within 1e-3 * sum|a*b| of the fp64 truth."""
+    A = orc.uniform_f16((256, 256), 0, 0)
+    B = orc.uniform_f16((256, 256), 0, 1)
+    C = _gemm(tmp_path, A, B, kernel)
+    T, S = orc.gemm_f64(A, B)
+    bad, worst = orc.check_tol(C, T, S)
+    assert bad == 0, f"{kernel}: {bad} outputs outside tolerance (worst {worst:.3g})"
+
+
+def test_callsite_gemm_naive(orc, tmp_path):
+    """mmm::GEMM_Naive at the reference's GEMM_Naive call shape (mmm.cpp:52-62): bit for bit the
+    oracle's restatement of its fp32, k-ascending sum, on configuration 1 and on a ragged shape."""
+    for M, N, K, seed in ((256, 256, 256, 0), (37, 141, 203, 8)):
+        A = orc.uniform_f16((M, K), seed, 0)
+        B = orc.uniform_f16((K, N), seed, 1)
+        C = _gemm(tmp_path, A, B, "GEMM_Naive")
+        R = orc.gemm_naive_f32(A, B)
+        assert np.array_equal(C, R), f"{M}x{N}x{K}: {int((C != R).sum())} outputs differ from the k-ascending sum"
 
 
 def test_callsite_gemm_exact_ragged(orc, tmp_path):

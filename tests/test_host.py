@@ -177,8 +177,9 @@ def test_header_is_plain_c():
 
 
 def test_cpp_header_drop_in(mm, tmp_path):
-    """include/mmm.hpp (the reference's template spelling) compiles and links against the
-    library; with null pointers every entry point reports hipErrorInvalidValue (no GPU needed)."""
+    """include/mmm.hpp (the reference's template spelling: WMMA_Swizzled_Full and the lineage's
+    other names, GEMM_Naive) compiles and links against the library; with null pointers every
+    entry point reports hipErrorInvalidValue (no GPU needed)."""
     src = tmp_path / "use_mmm.cpp"
     src.write_text("""
 #include <cstdio>
@@ -187,6 +188,10 @@ int main() {
   int bad = 0;
   bad += mmm::WMMA_Swizzled_Full<2, 2, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
   bad += mmm::WMMA_Swizzled_Full<4, 4, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_Templated_Base<2, 2, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_LDS_Padded<2, 2, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_LDS_Swizzled<2, 2, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::GEMM_Naive(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
   bad += mmm::WMMA_Auto(nullptr, nullptr, nullptr, 8, 8, 8, 8, 8, 8) != hipErrorInvalidValue;
   bad += mmm::WMMA_Tensor(nullptr, nullptr, nullptr, 2, 3, 4, 5, 6) != hipErrorInvalidValue;
   std::printf("%d\\n", bad);
@@ -219,6 +224,10 @@ int main() {
   int bad = 0;
   bad += mmm::WMMA_Swizzled_Full<2, 2, 4, 4>(dA, dA, dC, 64, 64, 64) != hipErrorInvalidValue;
   bad += mmm::WMMA_Swizzled_Full<2, 2, 4, 4>(nullptr, nullptr, nullptr, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_Templated_Base<2, 2, 4, 4>(dA, dA, dC, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_LDS_Padded<2, 2, 4, 4>(dA, dA, dC, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::WMMA_LDS_Swizzled<2, 2, 4, 4>(dA, dA, dC, 64, 64, 64) != hipErrorInvalidValue;
+  bad += mmm::GEMM_Naive(cG, cG, dC, 64, 64, 64) != hipErrorInvalidValue;
   bad += mmm::WMMA_Auto(dA, cG, dC, 8, 8, 8, 8, 8, 8) != hipErrorInvalidValue;
   bad += mmm::WMMA_Tensor(cG, cG, dC, 2, 3, 4, 5, 6) != hipErrorInvalidValue;
   std::printf("%d\\n", bad);
