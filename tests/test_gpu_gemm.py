@@ -1055,6 +1055,64 @@ def test_contraction_random_folds_exact(mm, cuda, seed):
     assert np.array_equal(got, truth), f"{ext} {order_a} {order_b} {order_c}: {int((got != truth).sum())} mismatches"
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_contraction_random_large_folds(mm, cuda, seed):
+    """Random 2-level folds over grids of many tiles: even seeds with the K sub-index innermost in
+    both operands and k_lo a multiple of 8 (the direct-to-LDS fold kernel; K tiles mostly cross k
+    blocks; M and N up to 4000, K up to 2048), odd seeds with every sub-index in a random memory
+    order (the gathering kernel unless K happens to be contiguous; up to 1500 x 1500 x 1000).
+    C's sub-indices in a random order too.  Integer inputs, bit-exact against a device fp64
+    product of the operands permuted to [M][K] x [K][N]; C starts as NaN and every element is
+    compared."""
+    torch = cuda
+    rng = np.random.default_rng(3000 + seed)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3000 + seed)
+    if seed % 2 == 0:
+        kl = int(rng.choice([8, 16, 24, 40, 56, 72, 96, 120, 128, 192, 256]))
+        ext = {"mh": int(rng.integers(2, 9)), "ml": int(rng.integers(100, 501)), "nh": int(rng.integers(2, 9)),
+               "nl": int(rng.integers(100, 501)), "kh": int(rng.integers(1, 9)), "kl": kl}
+        order_a = [str(a) for a in rng.permutation(["mh", "ml", "kh"])] + ["kl"]
+        order_b = [str(a) for a in rng.permutation(["kh", "nh", "nl"])] + ["kl"]
+    else:
+        ext = {"mh": int(rng.integers(2, 6)), "ml": int(rng.integers(50, 301)), "nh": int(rng.integers(2, 6)),
+               "nl": int(rng.integers(50, 301)), "kh": int(rng.integers(1, 6)), "kl": int(rng.integers(1, 201))}
+        order_a = [str(a) for a in rng.permutation(["mh", "ml", "kh", "kl"])]
+        order_b = [str(a) for a in rng.permutation(["kh", "kl", "nh", "nl"])]
+    order_c = [str(a) for a in rng.permutation(["mh", "ml", "nh", "nl"])]
+
+    def make(order, operand):
+        shape = tuple(ext[a] for a in order)
+        if operand:
+            x = torch.randint(-4, 5, shape, generator=gen, device="cuda", dtype=torch.int8).to(torch.float16)
+        else:
+            x = torch.full(shape, float("nan"), dtype=torch.float32, device="cuda")
+        return x, {a: x.stride(i) for i, a in enumerate(order)}
+
+    A, sa = make(order_a, True)
+    B, sb = make(order_b, True)
+    Cd, sc = make(order_c, False)
+    d = mm.ContractDesc()
+    for f, h, l in (("m_ext", "mh", "ml"), ("n_ext", "nh", "nl"), ("k_ext", "kh", "kl")):
+        getattr(d, f)[0], getattr(d, f)[1] = ext[h], ext[l]
+    for f, s, h, l in (("a_m_stride", sa, "mh", "ml"), ("a_k_stride", sa, "kh", "kl"), ("b_k_stride", sb, "kh", "kl"),
+                       ("b_n_stride", sb, "nh", "nl"), ("c_m_stride", sc, "mh", "ml"), ("c_n_stride", sc, "nh", "nl")):
+        getattr(d, f)[0], getattr(d, f)[1] = s[h], s[l]
+    M, N, K = ext["mh"] * ext["ml"], ext["nh"] * ext["nl"], ext["kh"] * ext["kl"]
+    where = f"{ext} A {order_a} B {order_b} C {order_c} (M {M} N {N} K {K})"
+    print(f"[random_large_fold] {where}", flush=True)
+    mm.contract(d, A, B, Cd)
+    torch.cuda.synchronize()
+    A2 = A.permute(*[order_a.index(a) for a in ("mh", "ml", "kh", "kl")]).reshape(M, K).double()
+    B2 = B.permute(*[order_b.index(a) for a in ("kh", "kl", "nh", "nl")]).reshape(K, N).double()
+    T = (A2 @ B2).reshape(ext["mh"], ext["ml"], ext["nh"], ext["nl"])
+    T = T.permute(*[("mh", "ml", "nh", "nl").index(a) for a in order_c]).float()
+    same = torch.equal(Cd, T)
+    assert same, f"{where}: {int((Cd != T).sum().item())} outputs differ"
+    del A, B, Cd, A2, B2, T
+    torch.cuda.empty_cache()
+
+
 def test_contraction_fold_dma_path_exact(mm, cuda):
     """A fold whose K sub-index is contiguous in both operands, in whole 64-deep tiles (the
     direct-to-LDS fold kernel) with permuted M and N sub-indices and a permuted C."""
