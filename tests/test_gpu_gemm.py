@@ -665,12 +665,16 @@ def test_tile_split_deterministic_and_graph(mm, cuda, orc):
 
 
 def test_concurrent_host_threads(mm, cuda):
-    """Four host threads, each with its own stream, issue split launches (tile K split and the
-    streaming split) at the same time: each stream gets its own workspace, results exact."""
+    """Six host threads, each with its own stream, issue split launches (tile K splits, the
+    streaming split, the tile+stream split) at the same time (ctypes releases the GIL during a
+    call, so the calls overlap inside the library): each stream gets its own workspace, results
+    exact.  (mmm_gemm_f16f32_noalloc is left out: its calls share one scratch array per GPU, and
+    overlapping calls on one GPU race by contract.)"""
     import threading
 
     rng = np.random.default_rng(12)
-    cases = [_exact_case(rng, *shp) for shp in [(16, 8192, 2048), (1024, 512, 4096), (8, 4096, 4096), (300, 264, 4096)]]
+    cases = [_exact_case(rng, *shp) for shp in [(16, 8192, 2048), (1024, 512, 4096), (8, 4096, 4096), (300, 264, 4096),
+                                                (4097, 512, 300), (2304, 2304, 1024)]]
     dev = [(to_dev(cuda, A), to_dev(cuda, B), truth) for A, B, truth in cases]
     results, errors = {}, []
 
