@@ -98,8 +98,10 @@ DESCRIPTIONS = {
                 "U[-1,1) seed 1",
     "lds_mfma_nobarrier": "operand-path probe: the 8192x8192x8192 persistent tile kernel's fragment reads and MFMAs "
                           "on operands staged in LDS once, no barrier (no operand loads, no C stores), U[-1,1) seed 1",
-    "read_ceiling": "HBM read ceiling probe: one pass over 1 GiB with 16-byte loads into registers, zeros",
-    "read_ceiling_lds": "HBM read ceiling probe: one pass over 1 GiB with direct-to-LDS 16-byte loads, zeros",
+    "read_ceiling": "HBM read ceiling probe: one pass over 1 GiB with non-temporal 16-byte loads into registers "
+                    "(8192 workgroups, 4 in flight per lane), zeros",
+    "read_ceiling_lds": "HBM read ceiling probe: one pass over 1 GiB with direct-to-LDS 16-byte loads (8192 "
+                        "workgroups, 32-slot rings), zeros",
 }
 
 
@@ -138,7 +140,7 @@ def make_workload(name, torch, mmm, tile=None):
                 "bytes": 2.0 * src.numel() * 4}
     if kind in ("read", "read_lds"):
         src = torch.zeros(M, dtype=torch.uint8, device=dev)
-        out = torch.empty(2048 * 256, dtype=torch.int32, device=dev)
+        out = torch.empty(8192 * 256, dtype=torch.int32, device=dev)
         lds = kind == "read_lds"
         return {"launch": lambda: mmm.probe_read(src, out, direct_to_lds=lds), "witness": None, "host_inputs": None,
                 "M": M, "N": N, "K": K, "bytes": float(M)}

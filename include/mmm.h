@@ -292,10 +292,10 @@ hipError_t mmm_tile_of_block(int block, int tiles_m, int tiles_n, int* tm, int* 
  *   sum of its accumulators; a workgroup's outputs sum to (tiles * K / 128) * (1^T A0)(B0 1),
  *   tiles its number of output tiles, A0 and B0 its first tile's rows of A and columns of B
  *   over K 0 .. 127.  M, N multiples of 256, K of 128.  clock as for mmm_probe_mfma_ceiling.
- * mmm_probe_read: streams `bytes` (a multiple of 1024, 16-byte-aligned src) once: with plain
- *   16-byte loads into registers (direct_to_lds == 0; out receives 2048 * 256 words), or with
- *   the tile kernels' direct-to-LDS loads (direct_to_lds != 0, bytes < 2^31; out receives 2048
- *   words).
+ * mmm_probe_read: streams `bytes` (a multiple of 1024, 16-byte-aligned src) once over 8192
+ *   workgroups: with plain non-temporal 16-byte loads into registers (direct_to_lds == 0; out
+ *   receives 8192 * 256 words), or with the tile kernels' direct-to-LDS loads into 32-slot rings
+ *   (direct_to_lds != 0, bytes < 2^31; out receives 8192 words).
  */
 hipError_t mmm_probe_clock(uint64_t* out, int64_t ticks, hipStream_t stream);
 hipError_t mmm_probe_mfma_ceiling(const mmm_half* A, const mmm_half* B, float* C, int M, int N, int K,

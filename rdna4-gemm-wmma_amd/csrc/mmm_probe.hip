@@ -111,18 +111,23 @@ __global__ __launch_bounds__(512, 1) void mfma_ceiling_kernel(const mmm_half* A,
 }
 
 // HBM read ceiling, plain loads: lanes stream 16-byte chunks (global_load_dwordx4) over
-// `n16` chunks, grid-stride, eight loads in flight per lane, XOR-folded into one dword per
-// thread so the loads stay live.
+// `n16` chunks, grid-stride, kReadInFlight non-temporal loads in flight per lane, XOR-folded into
+// one dword per thread so the loads stay live.  Launched as kReadBlocks workgroups: of the
+// configurations swept on MI355X (1024-16384 workgroups, 4, 8 or 16 loads in flight, cached or
+// non-temporal, 1 and 2 GiB), 8192 x 4 non-temporal read fastest over 1 GiB (5.87 TB/s; 2048 x 8,
+// this probe's earlier shape, 5.40).
+constexpr int kReadInFlight = 4;
+constexpr int kReadBlocks = 8192;  // both read probes
 __global__ __launch_bounds__(256) void read_ceiling_kernel(const u32x4* src, int64_t n16, uint32_t* out) {
   const int64_t stride = (int64_t)gridDim.x * 256;
   int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   u32x4 x = {0, 0, 0, 0};
-  for (; i + 7 * stride < n16; i += 8 * stride) {
-    u32x4 v[8];
+  for (; i + (kReadInFlight - 1) * stride < n16; i += kReadInFlight * stride) {
+    u32x4 v[kReadInFlight];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = __builtin_nontemporal_load(src + i + j * stride);
+    for (int j = 0; j < kReadInFlight; ++j) v[j] = __builtin_nontemporal_load(src + i + j * stride);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x ^= v[j];
+    for (int j = 0; j < kReadInFlight; ++j) x ^= v[j];
   }
   for (; i < n16; i += stride) x ^= src[i];
   out[(int64_t)blockIdx.x * 256 + threadIdx.x] = x[0] ^ x[1] ^ x[2] ^ x[3];
@@ -130,22 +135,25 @@ __global__ __launch_bounds__(256) void read_ceiling_kernel(const u32x4* src, int
 
 // HBM read ceiling, direct to LDS (the tile kernels' staging path): each wave streams 1 KB
 // pieces (64 lanes x 16 bytes, buffer_load_dwordx4 ... lds, non-temporal like the register
-// probe's loads) into an 8-slot LDS ring, grid-stride over the waves, keeping at most 8 loads in
-// flight.  Nothing reads the ring.
+// probe's loads) into a kLdsSlots-slot LDS ring, grid-stride over the waves, keeping at most
+// kLdsSlots loads in flight.  Nothing reads the ring.  Swept on MI355X over 1024-8192 workgroups
+// and 8-, 16- and 32-slot rings: 8192 workgroups of 32-slot rings (128 KB, one workgroup per CU)
+// read fastest (6.59 TB/s over 1 GiB; 2048 x 8 slots, this probe's earlier shape, 5.45).
+constexpr int kLdsSlots = 32;
 __global__ __launch_bounds__(256) void read_lds_ceiling_kernel(const void* src, uint32_t bytes, uint32_t* out) {
-  __shared__ __attribute__((aligned(1024))) char ring[4 * 8 * 1024];
+  __shared__ __attribute__((aligned(1024))) char ring[4 * kLdsSlots * 1024];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const i32x4 rsrc = make_rsrc(src, bytes);
   const uint32_t waves = gridDim.x * 4, wid = blockIdx.x * 4 + w;
   const uint32_t pieces = bytes / 1024;
-  const uint32_t ring_base = (uint32_t)(uintptr_t)(ring + w * 8 * 1024);
+  const uint32_t ring_base = (uint32_t)(uintptr_t)(ring + w * kLdsSlots * 1024);
   int slot = 0;
   for (uint32_t piece = wid; piece < pieces; piece += waves) {
     const uint32_t voff = piece * 1024 + lane * 16;
     dma_b128_nt(ring_base + slot * 1024, rsrc, voff);
-    wait_vmcnt<7>();
-    slot = (slot + 1) & 7;
+    wait_vmcnt<kLdsSlots - 1>();
+    slot = slot + 1 == kLdsSlots ? 0 : slot + 1;
   }
   wait_vmcnt<0>();
   __syncthreads();
@@ -201,7 +209,7 @@ hipError_t mmm_probe_lds_mfma(const mmm_half* A, const mmm_half* B, float* out, 
 hipError_t mmm_probe_read(const void* src, int64_t bytes, int direct_to_lds, uint32_t* out, int64_t out_words,
                           hipStream_t stream) {
   if (!src || !out || bytes <= 0 || (bytes & 1023) || ((uintptr_t)src & 15)) return hipErrorInvalidValue;
-  const int blocks = 2048;
+  const int blocks = kReadBlocks;
   if (direct_to_lds) {
     if (bytes >= 0x7fffffff || out_words < blocks) return hipErrorInvalidValue;
     hipLaunchKernelGGL(read_lds_ceiling_kernel, dim3(blocks), dim3(256), 0, stream, src, (uint32_t)bytes, out);

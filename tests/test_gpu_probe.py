@@ -105,7 +105,7 @@ def test_probe_read_runs(mm, cuda, lds):
     """The streaming-read probe reads every byte: an all-zero buffer XOR-folds to zeros, and a
     single planted word shows up in the plain-load fold."""
     src = cuda.zeros(1 << 24, dtype=cuda.uint8, device="cuda")
-    out = cuda.full((2048 * 256,), -1, dtype=cuda.int32, device="cuda")
+    out = cuda.full((8192 * 256,), -1, dtype=cuda.int32, device="cuda")
     mm.probe_read(src, out, direct_to_lds=lds)
     cuda.cuda.synchronize()
     if not lds:
@@ -120,21 +120,23 @@ def test_probe_read_runs(mm, cuda, lds):
 def test_probe_read_lds_pieces(mm, cuda):
     """The direct-to-LDS read probe loads the pieces it claims: each 1 KB piece p starts with the
     word p + 1, and workgroup b reports the first word of wave 0's ring slot 0, which is the last
-    piece that wave put there.  Wave 4b (2048 workgroups x 4 waves) takes pieces 4b + 8192 j and
-    ring slot j % 8; with 131072 pieces (128 MiB) that is j = 8, piece 4b + 65536."""
-    pieces = 1 << 17
+    piece that wave put there.  Wave 4b (8192 workgroups x 4 waves) takes pieces 4b + 32768 j and
+    ring slot j % 32; with 2^21 - 1 pieces (2 GiB less 1 KB) that is j = 32, piece 4b + 2^20."""
+    pieces = (1 << 21) - 1
     src = cuda.zeros(pieces * 1024, dtype=cuda.uint8, device="cuda")
     src.view(cuda.int32)[::256] = cuda.arange(1, pieces + 1, dtype=cuda.int32, device="cuda")
-    out = cuda.full((2048,), -1, dtype=cuda.int32, device="cuda")
+    out = cuda.full((8192,), -1, dtype=cuda.int32, device="cuda")
     mm.probe_read(src, out, direct_to_lds=True)
     cuda.cuda.synchronize()
-    waves = 2048 * 4
+    waves = 8192 * 4
     expect = []
-    for b in range(2048):
+    for b in range(8192):
         wid = 4 * b
-        j_last = max(j for j in range(0, pieces // waves + 1, 8) if wid + j * waves < pieces)
+        j_last = max(j for j in range(0, pieces // waves + 1, 32) if wid + j * waves < pieces)
         expect.append(wid + j_last * waves + 1)
     assert np.array_equal(out.cpu().numpy(), np.array(expect, dtype=np.int32))
+    del src
+    cuda.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("shape", [(256, 256, 256), (1000, 777, 320), (16, 4096, 4096)])
