@@ -443,6 +443,7 @@ hipError_t mmm_gemm_plan_f16f32(const mmm_half* A, const mmm_half* B, const floa
     plan->stream_rows = pr.M;
     plan->stream_workgroups = skinny_workgroups(pr);
     plan->stream_splits = skinny_splits(pr);
+    plan->stream_columns = skinny_columns(pr);
   }
   plan->workspace_bytes = (int64_t)plan_workspace_bytes(p, pl);
   return hipSuccess;

@@ -1,10 +1,10 @@
 // Streaming GEMM for M <= 64 (decode-shaped, e.g. 16 x 8192 x 8192): HBM-bound, so the design
 // goal is to stream B once at full bandwidth with the MFMA work hidden underneath.  Two kernels:
 //
-//  * gemm_stream_wide_kernel<MR> (MR = 1, 2, 4 groups of 16 rows): one workgroup per 128-column
-//    strip and K range; every wave streams the strip's full 256-byte rows of B over its quarter
-//    of the range; K partials summed through LDS, K ranges across workgroups summed by
-//    reduce_splits_kernel in a fixed order.
+//  * gemm_stream_wide_kernel<MR, NS> (MR = 1, 2, 4 groups of 16 rows): one workgroup per
+//    NS-column strip (128; 256 for long streams of M <= 16) and K range; every wave streams the
+//    strip's full 256- or 512-byte rows of B over its quarter of the range; K partials summed
+//    through LDS, K ranges across workgroups summed by reduce_splits_kernel in a fixed order.
 //  * gemm_skinny_kernel (M <= 16 without a caller workspace): one workgroup per
 //    32-column strip, XCD-contiguous; the four waves split K; partials summed through LDS.
 //
@@ -229,17 +229,17 @@ __global__ __launch_bounds__(256, 1) void gemm_skinny_kernel(GemmProblem p, int 
   }
 }
 
-// C[row][strip * 128 + c] = sum over q = 0 .. splits-1 (in that order) of the strip's
-// partials; one thread per 4 consecutive elements of the ROWS x 128 strip tiles.  All of a
+// C[row][strip * NS + c] = sum over q = 0 .. splits-1 (in that order) of the strip's
+// partials; one thread per 4 consecutive elements of the ROWS x NS strip tiles.  All of a
 // thread's split loads are issued before the sum (splits <= kMaxSplits), so the kernel costs
 // one memory round trip.
 constexpr int kMaxSplits = 16;
-template <int ROWS>
+template <int ROWS, int NS>
 __global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int strips, int splits,
                                                             const float* partials) {
-  constexpr int TILE = ROWS * 128;
+  constexpr int TILE = ROWS * NS;
   const int idx = blockIdx.x * 256 + threadIdx.x;
-  const int strip = idx / (TILE / 4), e = 4 * (idx % (TILE / 4)), row = e >> 7, col = strip * 128 + (e & 127);
+  const int strip = idx / (TILE / 4), e = 4 * (idx % (TILE / 4)), row = e / NS, col = strip * NS + e % NS;
   if (strip >= strips) return;
   const f32x4* base = (const f32x4*)(partials + (int64_t)strip * splits * TILE + e);
   f32x4 v[kMaxSplits];
@@ -262,30 +262,36 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int s
 }
 
 // ------------------------------------------------------------------------------------
-// Split streaming kernel (M <= 64, enough K): one workgroup per 128-column strip and K range
-// q of `splits`.  Each wave streams the whole strip -- 256 contiguous bytes of every B row --
-// over its own quarter of the workgroup's K range, through a private LDS ring (no barrier in
+// Split streaming kernel (M <= 64, enough K): one workgroup per NS-column strip and K range
+// q of `splits`.  Each wave streams the whole strip -- NS * 2 contiguous bytes of every B row
+// -- over its own quarter of the workgroup's K range, through a private LDS ring (no barrier in
 // the loop); the four K partials are summed through LDS in wave order.  With splits == 1 the
 // sum goes to C; otherwise to the workspace, and reduce_splits_kernel, launched next on the
 // same stream, sums the splits of every strip in split order (fixed orders throughout:
 // deterministic; the kernel boundary orders the partial stores before their reads).  B slots
-// [KS][128] have 256-byte rows -- one row of the 64 banks each -- so a chunk's banks depend only
-// on its slot position.  One pass of a 16x16x32 transposing read takes rows k .. k+3 and
-// k+8 .. k+11 at two chunks each; chunk c of row k sits at c ^ swz_b(k), swz_b(k) =
-// {0,6,10,12}[k & 3] ^ 2 * ((k >> 3) & 1): eight distinct XOR values, so the pass's 16 chunks hit
-// all 64 banks once (without the k >> 3 term rows k and k+8 collide: measured 45% of the LDS
-// cycles in bank conflicts).  MR 16-row groups of A
+// [KS][NS] have 256- or 512-byte rows -- one or two rows of the 64 banks each -- so a chunk's
+// banks depend only on its slot position (mod 16 chunks).  One pass of a 16x16x32 transposing
+// read takes rows k .. k+3 and k+8 .. k+11 at two chunks each; chunk c of row k sits at
+// c ^ swz_b(k), swz_b(k) = {0,6,10,12}[k & 3] ^ 2 * ((k >> 3) & 1): eight distinct XOR values
+// below 16, so the pass's 16 chunks hit all 64 banks once (without the k >> 3 term rows k and
+// k+8 collide: measured 45% of the LDS cycles in bank conflicts).  MR 16-row groups of A
 // (MR = 1, 2, 4 for up to 16, 32, 64 rows) share every B fragment: MR MFMAs per B read.
+// 512-byte row pieces stream faster from HBM than 256-byte ones (16 x 8192 x 8192: 23.9 against
+// 25.1 us for the streaming kernel), at twice the partial sums per workgroup.
 // ------------------------------------------------------------------------------------
-template <int MR>
+template <int MR, int NSW>
 struct Wide {
-  static constexpr int NS = 128;
+  static constexpr int NS = NSW;  // columns per strip: 128 (256-byte rows) or 256 (512-byte rows, MR = 1)
   static constexpr int ROWS = 16 * MR;
-  static constexpr int KS = MR == 4 ? 32 : 64;     // K rows per slot
-  static constexpr int SLOTS = MR == 4 ? 3 : 2;    // ring slots per wave
+  static constexpr int KS = MR == 4 || NS == 256 ? 32 : 64;  // K rows per slot
+  static constexpr int SLOTS = MR == 4 ? 3 : 2;              // ring slots per wave
   static constexpr int ABYTES = ROWS * KS * 2, BBYTES = KS * NS * 2, SLOT = ABYTES + BBYTES;
   static constexpr int NA = ABYTES / 1024, NB = BBYTES / 1024, LOADS = NA + NB;
-  static constexpr int NT = NS / 16, CPR = NS / 8, RPI = 64 / CPR;  // 8 tiles, 16 chunks per row, 4 rows
+  static constexpr int NT = NS / 16, CPR = NS / 8, RPI = 64 / CPR;  // tiles, chunks per row, rows per load
+  // B rows of load i are RPI * i + (lane / CPR); their swz_b takes PH values, by phase(i)
+  static constexpr int PH = RPI == 4 ? 2 : 4;
+  __host__ __device__ static constexpr int phase(int i) { return RPI == 4 ? (i >> 1) & 1 : (i & 1) | ((i >> 2) & 1) << 1; }
+  __host__ __device__ static constexpr int phase_load(int ph) { return RPI == 4 ? 2 * ph : (ph & 1) | (ph >> 1) << 2; }
   static constexpr int CA = KS / 8, RPI_A = 64 / CA;
   static constexpr int RING_BYTES = kWaves * SLOTS * SLOT;
   // [wave][ROWS][PS] fp32 partial sums; rows padded by 4 floats so the four 4-row lane groups of
@@ -294,16 +300,17 @@ struct Wide {
   static constexpr int PART_BYTES = kWaves * ROWS * PS * 4;
   static constexpr int LDS_BYTES = RING_BYTES > PART_BYTES ? RING_BYTES : PART_BYTES;
   static_assert(KS == 32 || KS == 64, "K rows per slot");
+  static_assert(NS == 128 || (NS == 256 && MR == 1), "strip widths");
   static_assert(LDS_BYTES <= 160 * 1024, "rings and partials must fit the LDS");
   __device__ static __forceinline__ int swz_a(int row) { return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
   __device__ static __forceinline__ int swz_b(int k) { return ((0xCA60 >> (4 * (k & 3))) & 15) ^ (((k >> 3) & 1) << 1); }
 };
 
 // NTB: B's loads are non-temporal (launch_wide: B of at least kNtStreamBytes).
-template <int MR, bool NTB>
+template <int MR, int NSW, bool NTB>
 __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p, int strips, int splits,
                                                                   float* partials) {
-  using W = Wide<MR>;
+  using W = Wide<MR, NSW>;
   constexpr int NS = W::NS, ROWS = W::ROWS, KS = W::KS, SLOTS = W::SLOTS, ABYTES = W::ABYTES, SLOT = W::SLOT;
   constexpr int NA = W::NA, NB = W::NB, LOADS = W::LOADS, NT = W::NT, CPR = W::CPR, RPI = W::RPI;
   constexpr int CA = W::CA, RPI_A = W::RPI_A;
@@ -337,12 +344,16 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     a_kc[i] = 8 * ((lane % CA) ^ W::swz_a(row));
     a_goff[i] = (uint32_t)((row * lda + a_kc[i]) * 2);
   }
-  // B rows of load i are 4i + b_row (RPI = 4): swz_b(4i + b_row) = swz_b(b_row) ^ 2 when
-  // (i >> 1) is odd, i.e. chunk slot c holds logical chunk c ^ swz_b(b_row) or its ^ 2 partner
+  // B rows of load i are RPI * i + b_row, and swz_b of them depends on W::phase(i) only: chunk
+  // slot c holds logical chunk c ^ swz_b(row of that phase)
   const int b_row = lane / CPR;
-  static_assert(RPI == 4, "the B swizzle's row phases assume four rows per load");
-  const int b_nc0 = 8 * ((lane % CPR) ^ W::swz_b(b_row)), b_nc1 = b_nc0 ^ 16;
-  const uint32_t b_goff0 = (uint32_t)((b_row * ldb + b_nc0) * 2), b_goff1 = (uint32_t)((b_row * ldb + b_nc1) * 2);
+  int b_nc[W::PH];
+  uint32_t b_goff[W::PH];
+#pragma unroll
+  for (int ph = 0; ph < W::PH; ++ph) {
+    b_nc[ph] = 8 * ((lane % CPR) ^ W::swz_b(W::phase_load(ph) * RPI + b_row));
+    b_goff[ph] = (uint32_t)((b_row * ldb + b_nc[ph]) * 2);
+  }
   const uint32_t b_rstep = (uint32_t)(RPI * ldb * 2);
   const i32x4 rb_full = make_rsrc(p.B + n0, clip_records(((int64_t)(K - 1) * ldb + N - n0) * 2));
 
@@ -358,7 +369,7 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     const uint32_t bk = (uint32_t)((int64_t)k0 * ldb * 2);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const uint32_t voff = bk + ((i >> 1) & 1 ? b_goff1 : b_goff0) + i * b_rstep;
+      const uint32_t voff = bk + b_goff[W::phase(i)] + i * b_rstep;
       if constexpr (NTB)
         dma_b128_nt(dst + ABYTES + i * 1024, rb_full, voff);
       else
@@ -384,7 +395,7 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const int k = k0 + i * RPI + b_row, n = n0 + ((i >> 1) & 1 ? b_nc1 : b_nc0);
+      const int k = k0 + i * RPI + b_row, n = n0 + b_nc[W::phase(i)];
       half8 v = {};
       if (k < K) {
 #pragma unroll
@@ -442,10 +453,12 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
     if (s < nst) fill(s, s);
   int cur = 0, nxt = P;
   int t = 0;
+  // The next slot's loads go out before the wait for the current one, so P to P + 1 slots are
+  // in flight per wave, not P - 1 to P (16 x 8192 x 8192: 25.5 -> 24.8 us on 128-column strips).
   for (; t + P < nst - 1; ++t) {
-    wait_vmcnt<(P - 1) * LOADS>();
-    wait_lgkm0();
+    wait_lgkm0();  // the previous compute's reads of slot nxt are done
     issue(t + P, nxt);
+    wait_vmcnt<P * LOADS>();  // slot cur has landed; the P slots after it may stay in flight
     compute(cur);
     cur = cur + 1 == SLOTS ? 0 : cur + 1;
     nxt = nxt + 1 == SLOTS ? 0 : nxt + 1;
@@ -489,7 +502,8 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
   }
 }
 
-// ---- launch shape.  Split kernel: 128-column strips x `splits` K ranges.  Every variant
+// ---- launch shape.  Split kernel: 128-column strips (256 on the long streams that
+// stream_shape names) x `splits` K ranges.  Every variant
 // holds one workgroup per CU (LDS), so the grid is kept to one round of 256 workgroups:
 // splits = the most that fit (at most 16, at least four 64-deep K steps each).  A second,
 // partly filled round costs more than the extra parallelism gains (measured: 112 strips run
@@ -502,6 +516,7 @@ static_assert((size_t)kWsTiles * 64 * 128 * 4 <= kMaxWorkspaceBytes, "partials m
 
 struct StreamShape {
   int mr;              // 16-row groups of the split kernel (1, 2, 4)
+  int ns;              // split kernel: columns per strip (128, or 256 for mr == 1)
   int strips, splits;  // split kernel: grid strips * splits; splits == 0: wave-split kernel
 };
 
@@ -518,18 +533,37 @@ static StreamShape stream_shape(const GemmProblem& p) {
   // the chip and B is at most 64 MiB.
   const bool b_unaligned = ((uintptr_t)p.B & 15) || p.ldb % 8;
   if (mr == 1 && b_unaligned && (p.N + kNS - 1) / kNS >= 128 && (int64_t)p.K * p.ldb * 2 <= ((int64_t)64 << 20))
-    return {mr, strips, 0};
+    return {mr, 128, strips, 0};
   const int nst_all = (p.K + 63) / 64;  // 64-deep K steps
-  int splits = 256 / strips;
-  splits = splits < kMaxSplits ? splits : kMaxSplits;
-  splits = splits < nst_all / 4 ? splits : nst_all / 4;
-  if (splits > kWsTiles / strips) splits = kWsTiles / strips;
-  if (splits < 1) splits = 1;
-  if (splits == 1 && strips < 128 && mr == 1) return {mr, strips, 0};
-  return {mr, strips, splits};
+  auto splits_for = [&](int ns, int nstrips) {
+    int splits = 256 / nstrips;
+    splits = splits < kMaxSplits ? splits : kMaxSplits;
+    splits = splits < nst_all / 4 ? splits : nst_all / 4;
+    if (splits > kWsTiles * 128 / ns / nstrips) splits = kWsTiles * 128 / ns / nstrips;
+    return splits < 1 ? 1 : splits;
+  };
+  const int splits = splits_for(128, strips);
+  if (splits == 1 && strips < 128 && mr == 1) return {mr, 128, strips, 0};
+  // M <= 16, aligned B, a workspace, and a 128-column grid already split: 256-column strips
+  // (512-byte row pieces) when every wave still streams at least 256 K rows and K >= 8192.
+  // Measured per call (B rotating through HBM, 256- against 128-column strips): 16 x 8192 x
+  // 8192 +2.8%, 16 x 16384 x 8192 +6.4%, 16 x 8192 x 28672 +8.7%, 1 x 8192 x 8192 +4.5%; with
+  // shorter streams per wave they lose: 16 x 4096 x 8192 (128 rows per wave) -4.8%, 16 x 4096 x
+  // 4096 -25%, 16 x 4096 x 14336 (224) -0.4%, 16 x 14336 x 4096 (K 4096) -1.8%; from an
+  // unsplit grid (no reduction) 16 x 32768 x 4096 -4.3%, 16 x 28672 x 8192 -1.0%.  17 to 32
+  // rows gained on some shapes and lost on others (32 x 8192 x 28672 +4.5%, 32 x 8192 x 8192
+  // -1.3%), so they keep 128 columns.
+  if (mr == 1 && !p.ws_absent && !b_unaligned && splits >= 2 && p.K >= 8192) {
+    const int strips2 = (p.N + 255) / 256, splits2 = splits_for(256, strips2);
+    if (splits2 >= 2 && strips2 * splits2 >= strips * splits && p.K / (4 * splits2) >= 256)
+      return {mr, 256, strips2, splits2};
+  }
+  return {mr, 128, strips, splits};
 }
 
 int skinny_splits(const GemmProblem& p) { return stream_shape(p).splits; }
+
+int skinny_columns(const GemmProblem& p) { return stream_shape(p).splits ? stream_shape(p).ns : kNS; }
 
 // More 128-column strips than CUs, on B rows that are not 16-byte aligned or with rounds less than
 // 2/3 filled on average: the tile kernels run the problem faster.  Measured (B rotating through
@@ -556,7 +590,7 @@ bool skinny_prefers_tiles(const GemmProblem& p) {
 
 size_t skinny_workspace_bytes(const GemmProblem& p) {
   const StreamShape sh = stream_shape(p);
-  return sh.splits > 1 ? (size_t)sh.strips * sh.splits * (16 * sh.mr) * 128 * 4 : 0;
+  return sh.splits > 1 ? (size_t)sh.strips * sh.splits * (16 * sh.mr) * sh.ns * 4 : 0;
 }
 
 int skinny_workgroups(const GemmProblem& p) {
@@ -572,7 +606,7 @@ bool skinny_ok(const GemmProblem& p) {
   // B offsets are taken from the strip base: the whole operand must fit a 32-bit offset (a
   // larger B goes to the tile kernels, whose descriptors are rebased per K tile; with per-slot
   // descriptors here, 16 x 33001 x 66000 ran 1005 us against 915 on 64 x 64 tiles)
-  if (((int64_t)p.K * p.ldb + 128) * 2 >= (int64_t)kOobOffset) return false;
+  if (((int64_t)p.K * p.ldb + 256) * 2 >= (int64_t)kOobOffset) return false;
   return true;
 }
 
@@ -583,19 +617,19 @@ bool skinny_ok(const GemmProblem& p) {
 // The in-workgroup kernel's 64-byte strips ran 30-40% slower with them (not used there).
 constexpr int64_t kNtStreamBytes = 96ll << 20;
 
-template <int MR>
+template <int MR, int NS>
 static hipError_t launch_wide(const GemmProblem& p, int strips, int splits, float* ws, hipStream_t stream) {
   if ((int64_t)p.K * p.N * 2 >= kNtStreamBytes)
-    hipLaunchKernelGGL((gemm_stream_wide_kernel<MR, true>), dim3(strips * splits), dim3(256), 0, stream, p, strips,
+    hipLaunchKernelGGL((gemm_stream_wide_kernel<MR, NS, true>), dim3(strips * splits), dim3(256), 0, stream, p, strips,
                        splits, ws);
   else
-    hipLaunchKernelGGL((gemm_stream_wide_kernel<MR, false>), dim3(strips * splits), dim3(256), 0, stream, p, strips,
-                       splits, ws);
+    hipLaunchKernelGGL((gemm_stream_wide_kernel<MR, NS, false>), dim3(strips * splits), dim3(256), 0, stream, p,
+                       strips, splits, ws);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   constexpr int ROWS = 16 * MR;
-  hipLaunchKernelGGL(reduce_splits_kernel<ROWS>, dim3(strips * (ROWS * 128 / 4 / 256)), dim3(256), 0, stream, p, strips,
-                     splits, (const float*)ws);
+  hipLaunchKernelGGL((reduce_splits_kernel<ROWS, NS>), dim3(strips * (ROWS * NS / 4 / 256)), dim3(256), 0, stream, p,
+                     strips, splits, (const float*)ws);
   return hipGetLastError();
 }
 
@@ -610,11 +644,12 @@ hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
   if (sh.splits == 1 || ws) {
     switch (sh.mr) {
       case 1:
-        return launch_wide<1>(p, sh.strips, sh.splits, ws, stream);
+        return sh.ns == 256 ? launch_wide<1, 256>(p, sh.strips, sh.splits, ws, stream)
+                            : launch_wide<1, 128>(p, sh.strips, sh.splits, ws, stream);
       case 2:
-        return launch_wide<2>(p, sh.strips, sh.splits, ws, stream);
+        return launch_wide<2, 128>(p, sh.strips, sh.splits, ws, stream);
       default:
-        return launch_wide<4>(p, sh.strips, sh.splits, ws, stream);
+        return launch_wide<4, 128>(p, sh.strips, sh.splits, ws, stream);
     }
   }
   // wave-split kernel (M <= 16): no caller workspace

@@ -52,7 +52,8 @@ class GemmPlan(C.Structure):
                 ("waves_j", C.c_int), ("block_m", C.c_int), ("block_n", C.c_int), ("direct_to_lds", C.c_int),
                 ("tile_rows", C.c_int), ("stream_rows", C.c_int), ("tile_workgroups", C.c_int64),
                 ("stream_workgroups", C.c_int64), ("stream_splits", C.c_int), ("tile_splits", C.c_int),
-                ("tile_split_tiles", C.c_int), ("tile_persistent", C.c_int), ("workspace_bytes", C.c_int64)]
+                ("tile_split_tiles", C.c_int), ("tile_persistent", C.c_int), ("workspace_bytes", C.c_int64),
+                ("stream_columns", C.c_int)]
 
 
 class ContractDesc(C.Structure):

@@ -369,18 +369,24 @@ def _exact_case(rng, M, N, K):
     return A, B, (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float32)
 
 
-# (M, N, K) -> K ranges the streaming kernel reduces across workgroups (0: within one workgroup)
-STREAM_SPLITS = [((16, 8192, 8192), 4), ((7, 16384, 4096), 2), ((16, 4096, 8192), 8), ((5, 1024, 8192), 16),
-                 ((16, 32768, 512), 1), ((3, 2000, 4000), 15), ((16, 4095, 4111), 0), ((16, 6001, 4111), 0), ((16, 8191, 4111), 4), ((16, 2047, 4111), 16), ((1, 130, 9000), 16),
-                 ((16, 8192, 256), 0), ((2, 264, 200), 0)]
+# (M, N, K) -> K ranges the streaming kernel reduces across workgroups (0: within one workgroup),
+# columns per workgroup strip
+STREAM_SPLITS = [((16, 8192, 8192), 8, 256), ((1, 16384, 8192), 4, 256), ((13, 8200, 8192), 7, 256),
+                 ((9, 8200, 8197), 7, 256), ((7, 16384, 4096), 2, 128), ((16, 4096, 8192), 8, 128),
+                 ((5, 1024, 8192), 16, 128), ((16, 32768, 512), 1, 128), ((3, 2000, 4000), 15, 128),
+                 ((16, 4095, 4111), 0, 32), ((16, 6001, 4111), 0, 32), ((16, 8191, 4111), 4, 128),
+                 ((16, 2047, 4111), 16, 128), ((1, 130, 9000), 16, 128), ((16, 8192, 256), 0, 32), ((2, 264, 200), 0, 32)]
 
 
-@pytest.mark.parametrize("case", STREAM_SPLITS, ids=lambda c: "x".join(map(str, c[0])) + f"-s{c[1]}")
+@pytest.mark.parametrize("case", STREAM_SPLITS, ids=lambda c: "x".join(map(str, c[0])) + f"-s{c[1]}-n{c[2]}")
 def test_exact_stream_splits(mm, cuda, case):
-    """The streaming kernel at every K-split count, the unsplit wide launch and the in-workgroup
-    split; exact against int64 (the partial sums are integers, so any order is exact)."""
-    (M, N, K), splits = case
-    assert mm.gemm_plan(M, N, K)["stream_splits"] == splits
+    """The streaming kernel at every K-split count and strip width (256-column strips with a
+    ragged last strip and a gathered K tail among them), the unsplit wide launch and the
+    in-workgroup split; exact against int64 (the partial sums are integers, so any order is
+    exact)."""
+    (M, N, K), splits, cols = case
+    plan = mm.gemm_plan(M, N, K)
+    assert plan["stream_splits"] == splits and plan["stream_columns"] == cols
     A, B, truth = _exact_case(np.random.default_rng(M * 7 + N + K), M, N, K)
     Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
     mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)

@@ -279,9 +279,9 @@ def test_gemm_plan(mm):
     p = mm.gemm_plan(4097, 4095, 4111)  # one row past 16 tile rows: that row streams
     assert p["kernel"] == "tile+stream" and p["tile_rows"] == 4096 and p["stream_rows"] == 1
     # B rows 2-byte aligned: 128 strips of 32 columns, K reduced inside each workgroup
-    assert p["stream_workgroups"] == 128 and p["stream_splits"] == 0
+    assert p["stream_workgroups"] == 128 and p["stream_splits"] == 0 and p["stream_columns"] == 32
     p = mm.gemm_plan(4097, 4096, 4112)  # aligned rows: 32 strips of 128 columns, K split 8 ways
-    assert p["stream_workgroups"] == 32 * 8 and p["stream_splits"] == 8
+    assert p["stream_workgroups"] == 32 * 8 and p["stream_splits"] == 8 and p["stream_columns"] == 128
     # the in-workgroup kernel's bounds for M <= 16: B rows not 16-byte aligned, at least 128
     # strips of 32 columns (N >= 4065), B at most 64 MiB; otherwise the split kernel
     for (M, N, K, ldb), splits in [((16, 4065, 4111, None), 0), ((16, 4063, 4111, None), 8),
@@ -290,14 +290,23 @@ def test_gemm_plan(mm):
         assert mm.gemm_plan(M, N, K, ldb=ldb)["stream_splits"] == splits, (M, N, K, ldb)
     p = mm.gemm_plan(16, 8192, 8192)
     assert p["kernel"] == "stream" and p["stream_rows"] == 16 and p["tile_workgroups"] == 0
-    assert p["stream_splits"] == 4 and p["stream_workgroups"] == 64 * 4
-    assert p["workspace_bytes"] == 64 * 4 * 16 * 128 * 4  # [strip][split][16][128] fp32 partials
+    # long K streams: 32 strips of 256 columns (512-byte row pieces), K split 8 ways
+    assert p["stream_splits"] == 8 and p["stream_workgroups"] == 32 * 8 and p["stream_columns"] == 256
+    assert p["workspace_bytes"] == 32 * 8 * 16 * 256 * 4  # [strip][split][16][256] fp32 partials
     need = C.c_size_t(0)
     assert mm.lib().mmm_gemm_workspace_f16f32(None, None, None, 16, 8192, 8192, 8192, 8192, 8192,
                                               C.byref(need)) == 0 and need.value == p["workspace_bytes"]
     # too little K to split: 32-column strips, K split among each workgroup's waves
     p = mm.gemm_plan(16, 8192, 128)
-    assert p["stream_splits"] == 0 and p["stream_workgroups"] == 8192 // 32
+    assert p["stream_splits"] == 0 and p["stream_workgroups"] == 8192 // 32 and p["stream_columns"] == 32
+    # 256-column strips only where each wave streams >= 256 K rows, K >= 8192 and the 128-column
+    # grid is split; otherwise 128 columns (17 rows and more: always 128)
+    for (M, N, K), cols in [((16, 16384, 8192), 256), ((1, 8192, 28672), 256), ((13, 8200, 8192), 256),
+                            ((16, 4096, 8192), 128), ((16, 4096, 14336), 128), ((16, 14336, 4096), 128),
+                            ((16, 28672, 8192), 128), ((17, 8192, 8192), 128)]:
+        assert mm.gemm_plan(M, N, K)["stream_columns"] == cols, (M, N, K)
+    assert mm.gemm_plan(16, 8192, 8192, ldb=8196)["stream_columns"] == 128  # B rows not 16-byte aligned
+    assert mm.gemm_plan(8192, 8192, 8192)["stream_columns"] == 0
     # the split grid stays within one round of 256 workgroups: 112 strips x 2, not x 3
     p = mm.gemm_plan(64, 14336, 4096)
     assert p["kernel"] == "stream" and p["stream_splits"] == 2 and p["stream_workgroups"] == 224
