@@ -2,7 +2,7 @@
 // goal is to stream B once at full bandwidth with the MFMA work hidden underneath.  Two kernels:
 //
 //  * gemm_stream_wide_kernel<MR, NS> (MR = 1, 2, 4 groups of 16 rows): one workgroup per
-//    NS-column strip (128; 256 for long streams of M <= 16) and K range; every wave streams the
+//    NS-column strip (128; 256 for long streams of M <= 32) and K range; every wave streams the
 //    strip's full 256- or 512-byte rows of B over its quarter of the range; K partials summed
 //    through LDS, K ranges across workgroups summed by reduce_splits_kernel in a fixed order.
 //  * gemm_skinny_kernel (M <= 16 without a caller workspace): one workgroup per
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int s
 // ------------------------------------------------------------------------------------
 template <int MR, int NSW>
 struct Wide {
-  static constexpr int NS = NSW;  // columns per strip: 128 (256-byte rows) or 256 (512-byte rows, MR = 1)
+  static constexpr int NS = NSW;  // columns per strip: 128 (256-byte rows) or 256 (512-byte rows, MR <= 2)
   static constexpr int ROWS = 16 * MR;
   static constexpr int KS = MR == 4 || NS == 256 ? 32 : 64;  // K rows per slot
   static constexpr int SLOTS = MR == 4 ? 3 : 2;              // ring slots per wave
@@ -300,7 +300,7 @@ struct Wide {
   static constexpr int PART_BYTES = kWaves * ROWS * PS * 4;
   static constexpr int LDS_BYTES = RING_BYTES > PART_BYTES ? RING_BYTES : PART_BYTES;
   static_assert(KS == 32 || KS == 64, "K rows per slot");
-  static_assert(NS == 128 || (NS == 256 && MR == 1), "strip widths");
+  static_assert(NS == 128 || (NS == 256 && MR <= 2), "strip widths");
   static_assert(LDS_BYTES <= 160 * 1024, "rings and partials must fit the LDS");
   __device__ static __forceinline__ int swz_a(int row) { return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
   __device__ static __forceinline__ int swz_b(int k) { return ((0xCA60 >> (4 * (k & 3))) & 15) ^ (((k >> 3) & 1) << 1); }
@@ -544,18 +544,20 @@ static StreamShape stream_shape(const GemmProblem& p) {
   };
   const int splits = splits_for(128, strips);
   if (splits == 1 && strips < 128 && mr == 1) return {mr, 128, strips, 0};
-  // M <= 16, aligned B, a workspace, and a 128-column grid already split: 256-column strips
-  // (512-byte row pieces) when every wave still streams at least 256 K rows and K >= 8192.
-  // Measured per call (B rotating through HBM, 256- against 128-column strips): 16 x 8192 x
-  // 8192 +2.8%, 16 x 16384 x 8192 +6.4%, 16 x 8192 x 28672 +8.7%, 1 x 8192 x 8192 +4.5%; with
-  // shorter streams per wave they lose: 16 x 4096 x 8192 (128 rows per wave) -4.8%, 16 x 4096 x
-  // 4096 -25%, 16 x 4096 x 14336 (224) -0.4%, 16 x 14336 x 4096 (K 4096) -1.8%; from an
-  // unsplit grid (no reduction) 16 x 32768 x 4096 -4.3%, 16 x 28672 x 8192 -1.0%.  17 to 32
-  // rows gained on some shapes and lost on others (32 x 8192 x 28672 +4.5%, 32 x 8192 x 8192
-  // -1.3%), so they keep 128 columns.
-  if (mr == 1 && !p.ws_absent && !b_unaligned && splits >= 2 && p.K >= 8192) {
+  // M <= 32, aligned B, a workspace, and a 128-column grid already split: 256-column strips
+  // (512-byte row pieces) when K >= 8192 and every wave still streams at least 256 K rows (512
+  // for 17 to 32 rows).  Measured per call (B rotating through HBM, 256- against 128-column
+  // strips): 16 x 8192 x 8192 +2.8%, 16 x 16384 x 8192 +6.4%, 16 x 8192 x 28672 +8.7%, 1 x 8192 x
+  // 8192 +4.5%; with shorter streams per wave they lose: 16 x 4096 x 8192 (128 rows per wave)
+  // -4.8%, 16 x 4096 x 4096 -25%, 16 x 4096 x 14336 (224) -0.4%, 16 x 14336 x 4096 (K 4096)
+  // -1.8%; from an unsplit grid (no reduction) 16 x 32768 x 4096 -4.3%, 16 x 28672 x 8192 -1.0%.
+  // 17 to 32 rows: 32 x 12288 x 16384 (819 rows per wave) +8.8%, 17 x 16384 x 16384 (1024)
+  // +5.2%, 32 x 8192 x 28672 (896) +3.8%, 24 x 8192 x 16384 (512) +2.3%, 32 x 16384 x 8192 (512)
+  // +0.9%; 32 x 8192 x 12288 (384) +-0, 32 x 6144 x 16384 (410) -2.2%, 32 x 8192 x 8192 (256)
+  // -1.3%, 32 x 4096 x 8192 (128) -11%.
+  if (mr <= 2 && !p.ws_absent && !b_unaligned && splits >= 2 && p.K >= 8192) {
     const int strips2 = (p.N + 255) / 256, splits2 = splits_for(256, strips2);
-    if (splits2 >= 2 && strips2 * splits2 >= strips * splits && p.K / (4 * splits2) >= 256)
+    if (splits2 >= 2 && strips2 * splits2 >= strips * splits && p.K / (4 * splits2) >= 256 * mr)
       return {mr, 256, strips2, splits2};
   }
   return {mr, 128, strips, splits};
@@ -647,7 +649,8 @@ hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
         return sh.ns == 256 ? launch_wide<1, 256>(p, sh.strips, sh.splits, ws, stream)
                             : launch_wide<1, 128>(p, sh.strips, sh.splits, ws, stream);
       case 2:
-        return launch_wide<2, 128>(p, sh.strips, sh.splits, ws, stream);
+        return sh.ns == 256 ? launch_wide<2, 256>(p, sh.strips, sh.splits, ws, stream)
+                            : launch_wide<2, 128>(p, sh.strips, sh.splits, ws, stream);
       default:
         return launch_wide<4, 128>(p, sh.strips, sh.splits, ws, stream);
     }

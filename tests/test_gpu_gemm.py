@@ -394,19 +394,21 @@ def test_exact_stream_splits(mm, cuda, case):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
-# 17 <= M <= 64: 32- and 64-row variants of the split streaming kernel -> K splits
-STREAM_ROWS = [((17, 8192, 8192), 4), ((24, 14336, 4096), 2), ((32, 4095, 4111), 8), ((33, 1000, 3000), 11),
-               ((48, 130, 9000), 16), ((64, 8192, 1024), 4), ((63, 28672, 512), 1), ((40, 128, 64), 1),
-               ((64, 264, 200), 1), ((57, 777, 1031), 4)]
+# 17 <= M <= 64: 32- and 64-row variants of the split streaming kernel -> K splits, columns per strip
+STREAM_ROWS = [((17, 8192, 8192), 4, 128), ((24, 14336, 4096), 2, 128), ((32, 4095, 4111), 8, 128),
+               ((33, 1000, 3000), 11, 128), ((48, 130, 9000), 16, 128), ((64, 8192, 1024), 4, 128),
+               ((63, 28672, 512), 1, 128), ((40, 128, 64), 1, 128), ((64, 264, 200), 1, 128),
+               ((57, 777, 1031), 4, 128), ((20, 16384, 8192), 4, 256), ((29, 16200, 8195), 4, 256)]
 
 
-@pytest.mark.parametrize("case", STREAM_ROWS, ids=lambda c: "x".join(map(str, c[0])) + f"-s{c[1]}")
+@pytest.mark.parametrize("case", STREAM_ROWS, ids=lambda c: "x".join(map(str, c[0])) + f"-s{c[1]}-n{c[2]}")
 def test_exact_stream_rows(mm, cuda, case):
     """Up to 64 rows on the streaming kernel (two or four 16-row groups sharing every B
-    fragment), split and unsplit, aligned and gathered tails: exact against int64."""
-    (M, N, K), splits = case
+    fragment), split and unsplit, aligned and gathered tails, 256-column strips for 17-32 rows
+    (one with a ragged last strip and a gathered K tail): exact against int64."""
+    (M, N, K), splits, cols = case
     plan = mm.gemm_plan(M, N, K)
-    assert plan["kernel"] == "stream" and plan["stream_splits"] == splits
+    assert plan["kernel"] == "stream" and plan["stream_splits"] == splits and plan["stream_columns"] == cols
     A, B, truth = _exact_case(np.random.default_rng(M * 5 + N + 3 * K), M, N, K)
     Cd = cuda.full((M, N), float("nan"), dtype=cuda.float32, device="cuda")
     mm.gemm(to_dev(cuda, A), to_dev(cuda, B), Cd)
