@@ -160,8 +160,8 @@ typedef struct mmm_gemm_plan {
                                               fill rounds of 256 workgroups less than 1/1.8 run
                                               on the streaming kernel, not on tiles */
     int stream_columns;                    /* columns of C per streaming workgroup: 32 (K split
-                                              among one workgroup's waves), 128, or 256 (M <= 32
-                                              with long K streams); 0: no streaming kernel */
+                                              among one workgroup's waves), 128, or 256 (long
+                                              K streams); 0: no streaming kernel */
 } mmm_gemm_plan;
 
 /*

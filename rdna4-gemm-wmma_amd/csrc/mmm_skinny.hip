@@ -2,7 +2,7 @@
 // goal is to stream B once at full bandwidth with the MFMA work hidden underneath.  Two kernels:
 //
 //  * gemm_stream_wide_kernel<MR, NS> (MR = 1, 2, 4 groups of 16 rows): one workgroup per
-//    NS-column strip (128; 256 for long streams of M <= 32) and K range; every wave streams the
+//    NS-column strip (128; 256 for long K streams) and K range; every wave streams the
 //    strip's full 256- or 512-byte rows of B over its quarter of the range; K partials summed
 //    through LDS, K ranges across workgroups summed by reduce_splits_kernel in a fixed order.
 //  * gemm_skinny_kernel (M <= 16 without a caller workspace): one workgroup per
@@ -281,10 +281,10 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(GemmProblem p, int s
 // ------------------------------------------------------------------------------------
 template <int MR, int NSW>
 struct Wide {
-  static constexpr int NS = NSW;  // columns per strip: 128 (256-byte rows) or 256 (512-byte rows, MR <= 2)
+  static constexpr int NS = NSW;  // columns per strip: 128 (256-byte rows) or 256 (512-byte rows)
   static constexpr int ROWS = 16 * MR;
   static constexpr int KS = MR == 4 || NS == 256 ? 32 : 64;  // K rows per slot
-  static constexpr int SLOTS = MR == 4 ? 3 : 2;              // ring slots per wave
+  static constexpr int SLOTS = MR == 4 && NS == 128 ? 3 : 2;  // ring slots per wave
   static constexpr int ABYTES = ROWS * KS * 2, BBYTES = KS * NS * 2, SLOT = ABYTES + BBYTES;
   static constexpr int NA = ABYTES / 1024, NB = BBYTES / 1024, LOADS = NA + NB;
   static constexpr int NT = NS / 16, CPR = NS / 8, RPI = 64 / CPR;  // tiles, chunks per row, rows per load
@@ -297,10 +297,12 @@ struct Wide {
   // [wave][ROWS][PS] fp32 partial sums; rows padded by 4 floats so the four 4-row lane groups of
   // an accumulator store (rows 4 apart) land 16 banks apart instead of on the same banks
   static constexpr int PS = NS + 4;
-  static constexpr int PART_BYTES = kWaves * ROWS * PS * 4;
+  // partial sums pass through the LDS in PASSES row blocks of PR rows when all of them do not fit
+  static constexpr int PASSES = kWaves * ROWS * PS * 4 > 160 * 1024 ? 2 : 1, PR = ROWS / PASSES;
+  static constexpr int PART_BYTES = kWaves * PR * PS * 4;
   static constexpr int LDS_BYTES = RING_BYTES > PART_BYTES ? RING_BYTES : PART_BYTES;
   static_assert(KS == 32 || KS == 64, "K rows per slot");
-  static_assert(NS == 128 || (NS == 256 && MR <= 2), "strip widths");
+  static_assert(NS == 128 || NS == 256, "strip widths");
   static_assert(LDS_BYTES <= 160 * 1024, "rings and partials must fit the LDS");
   __device__ static __forceinline__ int swz_a(int row) { return KS == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
   __device__ static __forceinline__ int swz_b(int k) { return ((0xCA60 >> (4 * (k & 3))) & 15) ^ (((k >> 3) & 1) << 1); }
@@ -478,27 +480,30 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
   }
 
   // four K partials -> LDS, summed in wave order, to C (one split) or the workspace
-  __syncthreads();
-  constexpr int PS = W::PS;
-  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][ROWS][PS]
-#pragma unroll
-  for (int g = 0; g < MR; ++g)
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) part[(w * ROWS + 16 * g + 4 * fg + v) * PS + 16 * j + fr] = acc[g][j][v];
-  __syncthreads();
+  constexpr int PS = W::PS, PR = W::PR, GP = MR / W::PASSES;  // rows and 16-row groups per pass
+  float LDS_AS* part = (float LDS_AS*)lds;  // [wave][PR][PS]
   float* mine = splits > 1 ? partials + (int64_t)(strip * splits + q) * (ROWS * NS) : nullptr;
 #pragma unroll
-  for (int e = 0; e < ROWS * NS / 256; ++e) {
-    const int idx = tid + 256 * e, row = idx / NS, col = idx % NS;
-    const float sum = ((part[(0 * ROWS + row) * PS + col] + part[(1 * ROWS + row) * PS + col]) +
-                       part[(2 * ROWS + row) * PS + col]) +
-                      part[(3 * ROWS + row) * PS + col];
-    if (mine)  // written through (sc0 sc1): the reduction reads them on other XCDs (+0.2-1.4% per call)
-      asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(mine + idx), "v"(sum) : "memory");
-    else if (row < M && n0 + col < N)
-      p.C[(int64_t)row * p.ldc + n0 + col] = sum;
+  for (int h = 0; h < W::PASSES; ++h) {
+    __syncthreads();  // the ring's last reads (h = 0), the previous pass's sums (h = 1)
+#pragma unroll
+    for (int g = 0; g < GP; ++g)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) part[(w * PR + 16 * g + 4 * fg + v) * PS + 16 * j + fr] = acc[h * GP + g][j][v];
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < PR * NS / 256; ++e) {
+      const int idx = tid + 256 * e, rl = idx / NS, col = idx % NS, row = h * PR + rl;
+      const float sum = ((part[(0 * PR + rl) * PS + col] + part[(1 * PR + rl) * PS + col]) +
+                         part[(2 * PR + rl) * PS + col]) +
+                        part[(3 * PR + rl) * PS + col];
+      if (mine)  // written through (sc0 sc1): the reduction reads them on other XCDs (+0.2-1.4% per call)
+        asm volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(mine + h * PR * NS + idx), "v"(sum) : "memory");
+      else if (row < M && n0 + col < N)
+        p.C[(int64_t)row * p.ldc + n0 + col] = sum;
+    }
   }
 }
 
@@ -544,9 +549,9 @@ static StreamShape stream_shape(const GemmProblem& p) {
   };
   const int splits = splits_for(128, strips);
   if (splits == 1 && strips < 128 && mr == 1) return {mr, 128, strips, 0};
-  // M <= 32, aligned B, a workspace, and a 128-column grid already split: 256-column strips
-  // (512-byte row pieces) when K >= 8192 and every wave still streams at least 256 K rows (512
-  // for 17 to 32 rows).  Measured per call (B rotating through HBM, 256- against 128-column
+  // Aligned B, a workspace, and a 128-column grid already split: 256-column strips (512-byte
+  // row pieces) when K >= 8192 and every wave still streams at least 256 K rows (512 for more
+  // than 16 rows).  Measured per call (B rotating through HBM, 256- against 128-column
   // strips): 16 x 8192 x 8192 +2.8%, 16 x 16384 x 8192 +6.4%, 16 x 8192 x 28672 +8.7%, 1 x 8192 x
   // 8192 +4.5%; with shorter streams per wave they lose: 16 x 4096 x 8192 (128 rows per wave)
   // -4.8%, 16 x 4096 x 4096 -25%, 16 x 4096 x 14336 (224) -0.4%, 16 x 14336 x 4096 (K 4096)
@@ -554,10 +559,13 @@ static StreamShape stream_shape(const GemmProblem& p) {
   // 17 to 32 rows: 32 x 12288 x 16384 (819 rows per wave) +8.8%, 17 x 16384 x 16384 (1024)
   // +5.2%, 32 x 8192 x 28672 (896) +3.8%, 24 x 8192 x 16384 (512) +2.3%, 32 x 16384 x 8192 (512)
   // +0.9%; 32 x 8192 x 12288 (384) +-0, 32 x 6144 x 16384 (410) -2.2%, 32 x 8192 x 8192 (256)
-  // -1.3%, 32 x 4096 x 8192 (128) -11%.
-  if (mr <= 2 && !p.ws_absent && !b_unaligned && splits >= 2 && p.K >= 8192) {
+  // -1.3%, 32 x 4096 x 8192 (128) -11%.  33 to 64 rows: 48 x 12288 x 16384 (819) +19.5% (240
+  // workgroups instead of 192), 64 x 8192 x 28672 (896) +4.2%, 64 x 8192 x 16384 (512) +1.9%,
+  // 40 x 16384 x 16384 (1024) +1.2%, 64 x 16384 x 8192 (512) +1.0%; 48 x 8192 x 12288 (384)
+  // -2.5%, 64 x 4096 x 14336 (224) -1.0%, 64 x 8192 x 8192 (256) -0.4%.
+  if (!p.ws_absent && !b_unaligned && splits >= 2 && p.K >= 8192) {
     const int strips2 = (p.N + 255) / 256, splits2 = splits_for(256, strips2);
-    if (splits2 >= 2 && strips2 * splits2 >= strips * splits && p.K / (4 * splits2) >= 256 * mr)
+    if (splits2 >= 2 && strips2 * splits2 >= strips * splits && p.K / (4 * splits2) >= (mr == 1 ? 256 : 512))
       return {mr, 256, strips2, splits2};
   }
   return {mr, 128, strips, splits};
@@ -652,7 +660,8 @@ hipError_t launch_gemm_skinny(const GemmProblem& p0, hipStream_t stream) {
         return sh.ns == 256 ? launch_wide<2, 256>(p, sh.strips, sh.splits, ws, stream)
                             : launch_wide<2, 128>(p, sh.strips, sh.splits, ws, stream);
       default:
-        return launch_wide<4, 128>(p, sh.strips, sh.splits, ws, stream);
+        return sh.ns == 256 ? launch_wide<4, 256>(p, sh.strips, sh.splits, ws, stream)
+                            : launch_wide<4, 128>(p, sh.strips, sh.splits, ws, stream);
     }
   }
   // wave-split kernel (M <= 16): no caller workspace

@@ -398,14 +398,16 @@ def test_exact_stream_splits(mm, cuda, case):
 STREAM_ROWS = [((17, 8192, 8192), 4, 128), ((24, 14336, 4096), 2, 128), ((32, 4095, 4111), 8, 128),
                ((33, 1000, 3000), 11, 128), ((48, 130, 9000), 16, 128), ((64, 8192, 1024), 4, 128),
                ((63, 28672, 512), 1, 128), ((40, 128, 64), 1, 128), ((64, 264, 200), 1, 128),
-               ((57, 777, 1031), 4, 128), ((20, 16384, 8192), 4, 256), ((29, 16200, 8195), 4, 256)]
+               ((57, 777, 1031), 4, 128), ((20, 16384, 8192), 4, 256), ((29, 16200, 8195), 4, 256),
+               ((57, 16200, 9001), 4, 256), ((40, 8192, 16384), 8, 256)]
 
 
 @pytest.mark.parametrize("case", STREAM_ROWS, ids=lambda c: "x".join(map(str, c[0])) + f"-s{c[1]}-n{c[2]}")
 def test_exact_stream_rows(mm, cuda, case):
     """Up to 64 rows on the streaming kernel (two or four 16-row groups sharing every B
-    fragment), split and unsplit, aligned and gathered tails, 256-column strips for 17-32 rows
-    (one with a ragged last strip and a gathered K tail): exact against int64."""
+    fragment), split and unsplit, aligned and gathered tails, 256-column strips for 17-64 rows
+    (with ragged last strips and gathered K tails; 64 rows sum their partials in two passes):
+    exact against int64."""
     (M, N, K), splits, cols = case
     plan = mm.gemm_plan(M, N, K)
     assert plan["kernel"] == "stream" and plan["stream_splits"] == splits and plan["stream_columns"] == cols

@@ -299,12 +299,13 @@ def test_gemm_plan(mm):
     # too little K to split: 32-column strips, K split among each workgroup's waves
     p = mm.gemm_plan(16, 8192, 128)
     assert p["stream_splits"] == 0 and p["stream_workgroups"] == 8192 // 32 and p["stream_columns"] == 32
-    # 256-column strips only where each wave streams >= 256 K rows (512 for 17 to 32 rows),
-    # K >= 8192 and the 128-column grid is split; otherwise 128 columns (33 rows and more: always)
+    # 256-column strips only where each wave streams >= 256 K rows (512 for more than 16 rows),
+    # K >= 8192 and the 128-column grid is split; otherwise 128 columns
     for (M, N, K), cols in [((16, 16384, 8192), 256), ((1, 8192, 28672), 256), ((13, 8200, 8192), 256),
                             ((16, 4096, 8192), 128), ((16, 4096, 14336), 128), ((16, 14336, 4096), 128),
                             ((16, 28672, 8192), 128), ((17, 8192, 8192), 128), ((32, 8192, 16384), 256),
-                            ((20, 16384, 8192), 256), ((32, 8192, 12288), 128), ((33, 16384, 16384), 128)]:
+                            ((20, 16384, 8192), 256), ((32, 8192, 12288), 128), ((33, 16384, 16384), 256),
+                            ((64, 8192, 16384), 256), ((48, 8192, 12288), 128), ((64, 8192, 8192), 128)]:
         assert mm.gemm_plan(M, N, K)["stream_columns"] == cols, (M, N, K)
     assert mm.gemm_plan(16, 8192, 8192, ldb=8196)["stream_columns"] == 128  # B rows not 16-byte aligned
     assert mm.gemm_plan(8192, 8192, 8192)["stream_columns"] == 0
