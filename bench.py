@@ -33,6 +33,7 @@ crossing n blocks and with a G of 2 GiB).  One GPU only: --gpus above 1 exits wi
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import re
@@ -609,10 +610,22 @@ SWEEP_SHAPES_LLM = [(2048, 4096, 4096), (4096, 11008, 4096), (4096, 4096, 11008)
                     (256, 4096, 4096), (128, 14336, 4096), (8192, 8192, 4096), (8192, 1024, 8192)]
 
 
+# decode-step GEMMs (1-64 tokens x out-features x in-features) of 8B- and 70B-class layers: the
+# M <= 64 streaming kernel's range (--sweep PATH --shapes decode; B rotates through HBM)
+SWEEP_SHAPES_DECODE = [(m, n, k) for m in (1, 16, 32, 64)
+                       for (n, k) in ((4096, 4096), (6144, 4096), (14336, 4096), (4096, 14336), (8192, 8192),
+                                      (10240, 8192), (28672, 8192), (8192, 28672))]
+# --shapes decode: each column cycles through B buffers totalling at least this much (more than the
+# 256 MB Infinity Cache), so B comes from HBM as a model's weights would
+SWEEP_ROTATE_BYTES = 512 << 20
+
+
 def parse_shapes(text: str):
-    """"MxNxK,MxNxK,..." -> [(M, N, K), ...]; "llm" -> SWEEP_SHAPES_LLM"""
+    """"MxNxK,MxNxK,..." -> [(M, N, K), ...]; "llm" -> SWEEP_SHAPES_LLM; "decode" -> SWEEP_SHAPES_DECODE"""
     if text.strip().lower() == "llm":
         return list(SWEEP_SHAPES_LLM)
+    if text.strip().lower() == "decode":
+        return list(SWEEP_SHAPES_DECODE)
     shapes = []
     for item in text.split(","):
         dims = tuple(int(x) for x in item.lower().split("x"))
@@ -622,17 +635,36 @@ def parse_shapes(text: str):
     return shapes
 
 
-def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool, shapes=None) -> None:
+def _cycle(fns):
+    """One launcher that runs fns in turn (the first alone when there is one)."""
+    if len(fns) == 1:
+        return fns[0]
+    it = itertools.cycle(fns)
+
+    def launch():
+        next(it)()
+
+    launch.tuning = getattr(fns[0], "tuning", None)
+    return launch
+
+
+def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool, shapes=None,
+              rotate_bytes: int = 0) -> None:
     """Every instantiated tile and the library's own choice on each problem of `shapes`
-    (SWEEP_SHAPES by default); median per-launch TFLOP/s, written as a markdown table to path."""
+    (SWEEP_SHAPES by default); median per-launch TFLOP/s, written as a markdown table to path.
+    With rotate_bytes, every column cycles through ceil(rotate_bytes / bytes of B) copies of B
+    (at most 16), so that B is read from HBM rather than from the Infinity Cache."""
     tiles = list(mmm.TILES)
     lines = ["| M x N x K | library pick | pick TFLOP/s | " + " | ".join(tiles) + " | best | pick / best | hipBLASLt | hipBLASLt candidate |",
              "|" + "---|" * (len(tiles) + 7)]
     for (M, N, K) in (shapes or SWEEP_SHAPES):
         A = torch.empty((M, K), dtype=torch.float16, device="cuda")
-        B = torch.empty((K, N), dtype=torch.float16, device="cuda")
+        nb = min(16, max(1, -(-rotate_bytes // (2 * K * N)))) if rotate_bytes else 1
+        Bs = [torch.empty((K, N), dtype=torch.float16, device="cuda") for _ in range(nb)]
+        B = Bs[0]
         mmm.fill_uniform(A, 7, 0)
-        mmm.fill_uniform(B, 7, 1)
+        for i, Bi in enumerate(Bs):
+            mmm.fill_uniform(Bi, 7, 1 + i)
         Cm = torch.empty((M, N), dtype=torch.float32, device="cuda")
         flops = 2.0 * M * N * K
 
@@ -645,11 +677,12 @@ def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool
         if plan["kernel"] == "tile+stream":
             pick = f"{plan['block_m']}x{plan['block_n']} + stream {plan['stream_rows']}"
         # every launcher bound once (checks, marshalling and hipBLASLt's planning outside the timing)
-        launchers = {"pick": mmm.bind_gemm(A, B, Cm)}
-        launchers.update({t: mmm.bind_gemm(A, B, Cm, tile=t) for t in tiles})
+        launchers = {"pick": _cycle([mmm.bind_gemm(A, Bi, Cm) for Bi in Bs])}
+        launchers.update({t: _cycle([mmm.bind_gemm(A, Bi, Cm, tile=t) for Bi in Bs]) for t in tiles})
         if with_witness:
             try:
-                launchers["hipblaslt"] = mmm.bind_witness_hipblaslt(A, B, Cm)
+                w0 = mmm.bind_witness_hipblaslt(A, B, Cm)  # candidates timed on the first B
+                launchers["hipblaslt"] = _cycle([w0] + [w0.with_operands(A, Bi, Cm) for Bi in Bs[1:]])
             except Exception as e:  # witness library absent or hipBLASLt refused the shape
                 _log(f"[sweep] hipBLASLt unavailable for {M}x{N}x{K}: {e}")
         # The chip's power controller takes tens of milliseconds to settle after the load changes,
@@ -677,7 +710,7 @@ def run_sweep(path: str, torch, mmm, steps: int, warmup: int, with_witness: bool
                + (f"#{wpick['best_index']} of {wpick['algos']}" if wpick else "") + " |")
         lines.append(row)
         _log("[sweep] " + row)
-        del A, B, Cm, launchers
+        del A, B, Bs, Cm, launchers
         torch.cuda.empty_cache()
     with open(path, "w") as f:
         f.write("\n".join(lines) + "\n")
@@ -709,8 +742,10 @@ def main() -> int:
     ap.add_argument("--shape", metavar="MxNxK", help="measure this GEMM (U[-1,1) inputs, seed 7) instead of --workload")
     ap.add_argument("--tile", metavar="BMxBN", help="with --shape: force this block tile (one of the library's six; "
                                                     "default: the library's own pick)")
-    ap.add_argument("--shapes", metavar="MxNxK,...", help="the problems --sweep runs: a list, or `llm` for the "
-                                                          "transformer-layer set (default: the built-in list)")
+    ap.add_argument("--shapes", metavar="MxNxK,...", help="the problems --sweep runs: a list, `llm` for the "
+                                                          "transformer-layer set, or `decode` for 1-64-token "
+                                                          "layer GEMMs with B rotating through HBM (default: the "
+                                                          "built-in list)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -730,8 +765,10 @@ def main() -> int:
     mmm.lib()
 
     if args.sweep:
+        decode = bool(args.shapes) and args.shapes.strip().lower() == "decode"
         run_sweep(args.sweep, torch, mmm, args.steps, args.warmup, with_witness=not args.no_witness,
-                  shapes=parse_shapes(args.shapes) if args.shapes else None)
+                  shapes=parse_shapes(args.shapes) if args.shapes else None,
+                  rotate_bytes=SWEEP_ROTATE_BYTES if decode else 0)
 
     if args.decompose:
         run_decompose(args.decompose, torch, mmm, args.decompose_seconds)

@@ -217,7 +217,7 @@ static GemmPlan plan_gemm(const GemmProblem& p) {
   if (p.M == 0 || p.N == 0) return {MMM_KERNEL_NONE, -1, 0};
   if (p.K == 0) return {MMM_KERNEL_ZERO, -1, 0};
   // M <= 64: HBM-bound streaming kernel, unless its strips run better as tiles
-  if (skinny_ok(p) && !skinny_prefers_tiles(p)) return {MMM_KERNEL_STREAM, -1, 0};
+  if (skinny_ok(p) && !skinny_prefers_tiles(p) && !skinny_tiles_faster(p)) return {MMM_KERNEL_STREAM, -1, 0};
   // A few rows past a whole number of 256-row tiles (4097 = 16*256 + 1) would cost a full
   // extra round of tiles; those rows go to the streaming kernel instead when that saves a round.
   const int rem = p.M % 256;

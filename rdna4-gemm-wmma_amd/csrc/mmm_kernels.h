@@ -84,6 +84,7 @@ hipError_t launch_gemm_skinny(const GemmProblem& p, hipStream_t stream);
 int skinny_workgroups(const GemmProblem& p);
 int skinny_splits(const GemmProblem& p);  // K ranges reduced across workgroups (0: within one)
 int skinny_columns(const GemmProblem& p);  // columns of C per workgroup strip (32, 128, 256)
+bool skinny_tiles_faster(const GemmProblem& p);   // 33-64 rows on short, many-strip grids: tiles win
 bool skinny_prefers_tiles(const GemmProblem& p);  // several rounds of strips that the tile kernels run faster
 size_t skinny_workspace_bytes(const GemmProblem& p);  // workspace its split needs (0: none)
 hipError_t launch_fill_uniform(mmm_half* out, int64_t n, uint64_t seed, uint32_t tensor_id, hipStream_t stream);

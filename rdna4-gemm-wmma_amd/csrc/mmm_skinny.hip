@@ -562,8 +562,10 @@ static StreamShape stream_shape(const GemmProblem& p) {
   // -1.3%, 32 x 4096 x 8192 (128) -11%.  33 to 64 rows: 48 x 12288 x 16384 (819) +19.5% (240
   // workgroups instead of 192), 64 x 8192 x 28672 (896) +4.2%, 64 x 8192 x 16384 (512) +1.9%,
   // 40 x 16384 x 16384 (1024) +1.2%, 64 x 16384 x 8192 (512) +1.0%; 48 x 8192 x 12288 (384)
-  // -2.5%, 64 x 4096 x 14336 (224) -1.0%, 64 x 8192 x 8192 (256) -0.4%.
-  if (!p.ws_absent && !b_unaligned && splits >= 2 && p.K >= 8192) {
+  // -2.5%, 64 x 4096 x 14336 (224) -1.0%, 64 x 8192 x 8192 (256) -0.4%.  From an unsplit
+  // 128-column grid only 33 to 64 rows, whose 128-column slots are one third A: 64 x 28672 x 8192
+  // +6.6% (1024 rows per wave), 48 x 28672 x 8192 +2.7% (16 rows: -1.0%, above).
+  if (!p.ws_absent && !b_unaligned && (splits >= 2 || mr == 4) && p.K >= 8192) {
     const int strips2 = (p.N + 255) / 256, splits2 = splits_for(256, strips2);
     if (splits2 >= 2 && strips2 * splits2 >= strips * splits && p.K / (4 * splits2) >= (mr == 1 ? 256 : 512))
       return {mr, 256, strips2, splits2};
@@ -596,6 +598,18 @@ bool skinny_prefers_tiles(const GemmProblem& p) {
   const bool b_unaligned = ((uintptr_t)p.B & 15) || p.ldb % 8;
   const double fill = (double)((wgs + 255) / 256) * 256.0 / wgs;  // rounds' slots per workgroup
   return b_unaligned || fill > (p.ws_absent ? 1.8 : 1.5);
+}
+
+// 33 to 64 rows on a 128-column grid of 2 or 3 K splits with K <= 4096 (many strips, short
+// streams): the 64 x 64 tile kernel, whose B panels the M <= 64 rows share, runs them faster.
+// Measured (B rotating through HBM, whole calls): 64 x 14336 x 4096 225.1 against 214.4 TFLOP/s
+// streamed, 64 x 16384 x 4096 264.2 against 236.0, 64 x 11008 x 4096 190.5 against 180.8,
+// 56 x 14336 x 4096 200.7 against 191.4, 48 x 14336 x 4096 174.3 against 166.7, 40 x 11008 x
+// 4096 124.9 against 121.9.  At K = 8192 the same grids stream faster than the tile picked for
+// them (64 x 10240 x 8192: 249.7 streamed, 175 on 64 x 64 tiles).
+bool skinny_tiles_faster(const GemmProblem& p) {
+  const StreamShape sh = stream_shape(p);
+  return !p.ws_absent && sh.mr == 4 && sh.ns == 128 && sh.splits >= 2 && sh.splits <= 3 && p.K <= 4096;
 }
 
 size_t skinny_workspace_bytes(const GemmProblem& p) {

@@ -635,4 +635,16 @@ def bind_witness_hipblaslt(A, B, C_out, stream=None, tune: bool = True):
     launch = _bound(W.mmm_witness_hipblaslt_run, "mmm_witness_hipblaslt_run", args, (A, B, C_out, ws))
     launch.plan = plan  # keeps the plan alive as long as the launcher
     launch.tuning = plan.tune(A, B, C_out, ws, stream) if tune else {"algos": plan.info()[0], "best_index": 0}
+
+    def with_operands(A2, B2, C2):
+        """The same plan and bound candidate on other tensors of the same shapes and strides."""
+        if (A2.shape, B2.shape, C2.shape) != (A.shape, B.shape, C_out.shape) or \
+                (A2.stride(0), B2.stride(0), C2.stride(0)) != (A.stride(0), B.stride(0), C_out.stride(0)):
+            raise ValueError("with_operands: shapes and row strides must match the bound plan")
+        args2 = (plan.ptr, _ptr(A2), _ptr(B2), _ptr(C2), _ptr(ws), ws.numel(), _stream(stream))
+        other = _bound(W.mmm_witness_hipblaslt_run, "mmm_witness_hipblaslt_run", args2, (A2, B2, C2, ws))
+        other.plan, other.tuning = plan, launch.tuning
+        return other
+
+    launch.with_operands = with_operands
     return launch

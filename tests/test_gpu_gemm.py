@@ -399,7 +399,7 @@ STREAM_ROWS = [((17, 8192, 8192), 4, 128), ((24, 14336, 4096), 2, 128), ((32, 40
                ((33, 1000, 3000), 11, 128), ((48, 130, 9000), 16, 128), ((64, 8192, 1024), 4, 128),
                ((63, 28672, 512), 1, 128), ((40, 128, 64), 1, 128), ((64, 264, 200), 1, 128),
                ((57, 777, 1031), 4, 128), ((20, 16384, 8192), 4, 256), ((29, 16200, 8195), 4, 256),
-               ((57, 16200, 9001), 4, 256), ((40, 8192, 16384), 8, 256)]
+               ((57, 16200, 9001), 4, 256), ((40, 8192, 16384), 8, 256), ((61, 16520, 8195), 3, 256)]
 
 
 @pytest.mark.parametrize("case", STREAM_ROWS, ids=lambda c: "x".join(map(str, c[0])) + f"-s{c[1]}-n{c[2]}")

@@ -310,10 +310,20 @@ def test_gemm_plan(mm):
     assert mm.gemm_plan(16, 8192, 8192, ldb=8196)["stream_columns"] == 128  # B rows not 16-byte aligned
     assert mm.gemm_plan(8192, 8192, 8192)["stream_columns"] == 0
     # the split grid stays within one round of 256 workgroups: 112 strips x 2, not x 3
-    p = mm.gemm_plan(64, 14336, 4096)
+    p = mm.gemm_plan(24, 14336, 4096)
     assert p["kernel"] == "stream" and p["stream_splits"] == 2 and p["stream_workgroups"] == 224
     p = mm.gemm_plan(32, 28672, 8192)  # 224 strips fill the chip unsplit
     assert p["stream_splits"] == 1 and p["stream_workgroups"] == 224
+    # 33-64 rows: from an unsplit 128-column grid to 256 columns on long K; short K over many
+    # strips (2-3 splits, K <= 4096) on 64 x 64 tiles
+    p = mm.gemm_plan(64, 28672, 8192)
+    assert p["stream_columns"] == 256 and p["stream_splits"] == 2 and p["stream_workgroups"] == 224
+    for (M, N, K), kernel in [((64, 14336, 4096), "tile"), ((40, 11008, 4096), "tile"), ((64, 16384, 4096), "tile"),
+                              ((64, 10240, 8192), "stream"), ((64, 6144, 4096), "stream"), ((32, 14336, 4096), "stream")]:
+        p = mm.gemm_plan(M, N, K)
+        assert p["kernel"] == kernel, (M, N, K, p["kernel"])
+        if kernel == "tile":
+            assert (p["block_m"], p["block_n"]) == (64, 64) and p["stream_rows"] == 0
     assert mm.gemm_plan(65, 8192, 8192)["kernel"] == "tile"
     # more 128-column strips than CUs: B rows that are not 16-byte aligned, or rounds less than 2/3
     # filled on average, run on the tile kernels; fuller rounds stream unsplit
@@ -404,3 +414,23 @@ def test_line_store_lane_map(fm, fn):
     assert len(written) == fm * 16 * fn * 16
     for a, v in written.items():
         assert v == value(a // ldc, a % ldc)
+
+
+def test_bench_shape_sets():
+    """bench.py's sweep shape sets and its rotating launcher (no GPU)."""
+    sys.path.insert(0, REPO)
+    import bench
+
+    assert bench.parse_shapes("llm") == bench.SWEEP_SHAPES_LLM
+    decode = bench.parse_shapes("decode")
+    assert len(decode) == 32 and all(1 <= m <= 64 for m, _, _ in decode)
+    assert bench.parse_shapes("16x8192x8192, 1x2x3") == [(16, 8192, 8192), (1, 2, 3)]
+    with pytest.raises(ValueError):
+        bench.parse_shapes("1x2")
+    calls = []
+    launch = bench._cycle([lambda: calls.append(0), lambda: calls.append(1), lambda: calls.append(2)])
+    for _ in range(7):
+        launch()
+    assert calls == [0, 1, 2, 0, 1, 2, 0]
+    single = lambda: None
+    assert bench._cycle([single]) is single
