@@ -52,12 +52,14 @@ def test_noalloc_matches_workspace_entry(mm, cuda):
             assert torch.equal(out, ref), f"{M}x{N}x{K} rep {rep}"
 
 
-@pytest.mark.parametrize("shape", [(2304, 2304, 8192), (16, 4096, 4096)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", [(2304, 2304, 8192), (16, 4096, 4096), (16, 8192, 8192)],
+                         ids=lambda s: "x".join(map(str, s)))
 def test_noalloc_graph_capture(mm, cuda, shape):
     """The documented order for callers under graph capture: one eager call (looks the array's
-    address up), then a captured call, replayed.  Both shapes split K into the array (a tile
-    split with its reduction launch; the streaming kernel's split).  Every replay, with eager
-    work and synchronisation in between, equals mmm_gemm_f16f32_ws's result bit for bit."""
+    address up), then a captured call, replayed.  Every shape splits K into the array (a tile
+    split with its reduction launch; the streaming kernel's split on 128- and 256-column
+    strips).  Every replay, with eager work and synchronisation in between, equals
+    mmm_gemm_f16f32_ws's result bit for bit."""
     torch = cuda
     M, N, K = shape
     assert mm.gemm_plan(M, N, K)["workspace_bytes"] > 0
