@@ -125,7 +125,7 @@ hipError_t launch_zero_fold(const FoldProblem& p, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------- tile selection
-constexpr double kPartialRoundBoost = 0.6;
+constexpr double kPartialRoundBoost = 0.3;
 
 // Estimated time of a tile launch, in seconds: rounds of 256 concurrent workgroups (one per
 // CU) times the MFMA time of one tile's K range at the tile's relative efficiency -- its MFMA
@@ -136,16 +136,28 @@ constexpr double kPartialRoundBoost = 0.6;
 // the smaller tiles' rate is operand loads per flop ((BM + BN) / (BM * BN): 1.5x for the narrow
 // tiles, 2x for 128x128, 4x for 64x64), which saturate the address unit (TA busy 0.48 for
 // 256x256, 0.59-0.65 narrow, 0.83 for 128x128, 0.89 for 64x64); no tile has LDS bank conflicts.
-// The narrow tiles are priced at 0.82 and 128x128 at 0.76; 192x192 and 64x64 at 0.91 and 0.45,
+// The narrow tiles are priced at 0.82 and 128x128 at 0.76; 192x192 and 64x64 at 0.86 and 0.30,
 // the values that pick the faster tile on the shapes
 // measured for them: 192x192 on 3072^3, 3072^2 x 8192, 4357 x 4095 x 4111 and the 4-way K split
-// of 1536^2 x 12288 (937 TFLOP/s against 864 for a 7-way split of 256x256 tiles; at 0.90 the
-// estimates were 2.6% apart and the larger tile kept it), 256x256 on 2304^2 x 8192, 4608^2 x
-// 8192, 6144^3, 6144^2 x 2048 and 3000 x 5000 x 1000; 64x64 on 256^3 to 1024^2 x 2048, 128x128
-// from 1536^3) plus a fixed per-round cost (prologue, epilogue).
+// of 1536^2 x 12288 (937 TFLOP/s against 864 for a 7-way split of 256x256 tiles), 256x256 on
+// 2304^2 x 8192, 4608^2 x 8192, 6144^3, 6144^2 x 2048 and 3000 x 5000 x 1000; 64x64 on 256^3 to
+// 1024^2 x 2048, 128x128 from 1536^3) plus a fixed per-round cost (prologue, epilogue).
 // With a K split (gemm_nn_split) the split tiles' round runs K / splits, and the reduction's
-// traffic and launch are added.
-constexpr double kEff64 = 0.45, kEff128 = 0.76, kEffNarrow = 0.82, kEff192 = 0.91;
+// traffic (priced at kSplitCostBps) and launch are added.
+// The prices (kEff64, kEff192, kPartialRoundBoost, kSplitCostBps) were fitted, with an offline
+// restatement of this function, to every forced-tile time measured on MI355X: the 39 shapes of
+// the tile and transformer-layer sweeps, which they pick exactly as before (within 0.13% of the
+// fastest tile on average), and 40 shapes of 136 to 256 rows (4096 to 28672 wide, K 4096 to
+// 28672), timed with B resident and with B rotating through HBM as a model's weights are.  On
+// those the pick went from 3.3% (resident) and 6.2% (rotating) behind the fastest tile on
+// average to 0.8% and 0.5%: 64x64 gave way to 128x128 at 136-192 x 4096 x 4096 (rotating B:
+// 30.1 -> 23.6 us at 192 rows), 192x192 to 256x128 at 136-192 x 28672 x 8192 (141.0 -> 126.1 us
+// at 192 rows), and 256x256 with an 8-way K split to 256x128 at 224-256 x 8192 x 8192 (59.3 ->
+// 49.9 us at 256 rows, B resident).
+constexpr double kEff64 = 0.30, kEff128 = 0.76, kEffNarrow = 0.82, kEff192 = 0.86;
+// Reduction traffic of a K split as tile_cost prices it against other tiles (the split decision
+// itself, gemm_nn_split, uses kSplitTrafficBps).
+constexpr double kSplitCostBps = 5e12;
 // The 128x128 tile in an unsplit launch of one round runs its 3-stage ring (DeepTile128), faster
 // per CU than the 2-stage multi-round version the 0.76 was measured on: priced at 0.80, which
 // picks it at 512 x 8192 x 8192 (867-919 TFLOP/s against 842-876 for a 4-way K split of 64
@@ -159,9 +171,9 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
   const double tile_eff = tile == kTile128x128 && sp.splits <= 1 && tiles <= 256.0 ? kEff128Deep : eff_of[tile];
   const double per_cu_flops = 4.8e12;  // sustained MFMA rate of one CU under load (256x256 at 8192^3)
   // A round with `active` of its 256 slots busy runs each CU faster: the chip is then below its
-  // power cap and keeps a higher clock.  Fitted to the forced-tile times of the 23-shape sweep
-  // (any factor from 0.5 to 0.8 picks the fastest measured tile on every shape; 3072^3 ran 878
-  // TFLOP/s on 144 256x256 tiles against 811 on the 128x256 tile the full-load rate preferred).
+  // power cap and keeps a higher clock.  Fitted with the prices above (3072^3 ran 878 TFLOP/s
+  // on 144 256x256 tiles against 811 on the 128x256 tile the full-load rate preferred; with the
+  // refitted tile prices, 0.3 keeps that pick and every other pick of the sweeps).
   auto round = [&](double k, double active) {
     const double boost = 1.0 + kPartialRoundBoost * (1.0 - std::min(active, 256.0) / 256.0);
     return 2.0 * bm * bn * k / (per_cu_flops * tile_eff * boost) + 3e-6;
@@ -181,7 +193,7 @@ static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
   if (sp.splits > 1) {
     t = rounds(tiles - sp.tiles, k_full) +
         round(std::ceil((double)p.K / sp.splits / 64.0) * 64.0, (double)sp.tiles * sp.splits) +
-        (double)sp.tiles * bm * bn * 4.0 * (2.0 * sp.splits + 1) / kSplitTrafficBps + 3e-6;
+        (double)sp.tiles * bm * bn * 4.0 * (2.0 * sp.splits + 1) / kSplitCostBps + 3e-6;
   } else {
     t = rounds(tiles, k_full);
   }

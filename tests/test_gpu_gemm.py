@@ -558,7 +558,7 @@ def test_exact_persistent(mm, cuda, case):
 # full, so its tiles run as K ranges while the rest run over all of K (0 split tiles: declined,
 # the reduction would cost more than the round it saves)
 TAIL_SPLITS = [((6144, 6144, 4096), ("256x256", 4, 64)), ((1792, 5120, 8192), ("256x128", 10, 24)),
-               ((1408, 6656, 8192), ("128x256", 8, 30)), ((1280, 7168, 4096), ("192x192", 8, 10)),
+               ((1408, 6656, 8192), ("128x256", 8, 30)), ((1344, 7168, 4096), ("192x192", 8, 10)),
                ((4608, 4608, 8192), ("256x256", 3, 68)), ((7168, 7168, 7168), ("256x256", 14, 16)),
                ((4357, 4095, 8191), ("256x256", 8, 32)), ((2304, 2304, 8192), ("256x256", 3, 81)),
                ((6150, 6144, 1030), ("256x256", 1, 0))]
