@@ -610,6 +610,11 @@ SWEEP_SHAPES_LLM = [(2048, 4096, 4096), (4096, 11008, 4096), (4096, 4096, 11008)
                     (256, 4096, 4096), (128, 14336, 4096), (8192, 8192, 4096), (8192, 1024, 8192)]
 
 
+# 136-256 tokens x out-features x in-features (prefill chunks, large decode batches): the shapes the
+# tile prices were refitted on (--sweep PATH --shapes small_m, with and without --rotate)
+SWEEP_SHAPES_SMALL_M = [(m, n, k) for m in (136, 160, 192, 224, 256)
+                        for (n, k) in ((4096, 4096), (14336, 4096), (4096, 14336), (8192, 8192), (28672, 8192),
+                                       (8192, 28672), (11008, 4096), (4096, 11008))]
 # decode-step GEMMs (1-64 tokens x out-features x in-features) of 8B- and 70B-class layers: the
 # M <= 64 streaming kernel's range (--sweep PATH --shapes decode; B rotates through HBM)
 SWEEP_SHAPES_DECODE = [(m, n, k) for m in (1, 16, 32, 64)
@@ -621,9 +626,11 @@ SWEEP_ROTATE_BYTES = 512 << 20
 
 
 def parse_shapes(text: str):
-    """"MxNxK,MxNxK,..." -> [(M, N, K), ...]; "llm" -> SWEEP_SHAPES_LLM; "decode" -> SWEEP_SHAPES_DECODE"""
+    """"MxNxK,MxNxK,..." -> [(M, N, K), ...]; "llm", "small_m", "decode" -> those sets"""
     if text.strip().lower() == "llm":
         return list(SWEEP_SHAPES_LLM)
+    if text.strip().lower() == "small_m":
+        return list(SWEEP_SHAPES_SMALL_M)
     if text.strip().lower() == "decode":
         return list(SWEEP_SHAPES_DECODE)
     shapes = []
@@ -743,9 +750,13 @@ def main() -> int:
     ap.add_argument("--tile", metavar="BMxBN", help="with --shape: force this block tile (one of the library's six; "
                                                     "default: the library's own pick)")
     ap.add_argument("--shapes", metavar="MxNxK,...", help="the problems --sweep runs: a list, `llm` for the "
-                                                          "transformer-layer set, or `decode` for 1-64-token "
-                                                          "layer GEMMs with B rotating through HBM (default: the "
-                                                          "built-in list)")
+                                                          "transformer-layer set, `small_m` for 136-256-token "
+                                                          "layer GEMMs, or `decode` for 1-64-token layer GEMMs "
+                                                          "with B rotating through HBM (default: the built-in "
+                                                          "list)")
+    ap.add_argument("--rotate", action="store_true",
+                    help="with --sweep: cycle every column through copies of B totalling 512 MiB (read from "
+                         "HBM, not the Infinity Cache); always on for --shapes decode")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -768,7 +779,7 @@ def main() -> int:
         decode = bool(args.shapes) and args.shapes.strip().lower() == "decode"
         run_sweep(args.sweep, torch, mmm, args.steps, args.warmup, with_witness=not args.no_witness,
                   shapes=parse_shapes(args.shapes) if args.shapes else None,
-                  rotate_bytes=SWEEP_ROTATE_BYTES if decode else 0)
+                  rotate_bytes=SWEEP_ROTATE_BYTES if decode or args.rotate else 0)
 
     if args.decompose:
         run_decompose(args.decompose, torch, mmm, args.decompose_seconds)

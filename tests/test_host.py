@@ -424,6 +424,8 @@ def test_bench_shape_sets():
     assert bench.parse_shapes("llm") == bench.SWEEP_SHAPES_LLM
     decode = bench.parse_shapes("decode")
     assert len(decode) == 32 and all(1 <= m <= 64 for m, _, _ in decode)
+    small = bench.parse_shapes("small_m")
+    assert len(small) == 40 and all(128 < m <= 256 for m, _, _ in small)
     assert bench.parse_shapes("16x8192x8192, 1x2x3") == [(16, 8192, 8192), (1, 2, 3)]
     with pytest.raises(ValueError):
         bench.parse_shapes("1x2")
