@@ -159,10 +159,12 @@ constexpr double kEff64 = 0.30, kEff128 = 0.76, kEffNarrow = 0.82, kEff192 = 0.8
 // itself, gemm_nn_split, uses kSplitTrafficBps).
 constexpr double kSplitCostBps = 5e12;
 // The 128x128 tile in an unsplit launch of one round runs its 3-stage ring (DeepTile128), faster
-// per CU than the 2-stage multi-round version the 0.76 was measured on: priced at 0.80, which
-// picks it at 512 x 8192 x 8192 (867-919 TFLOP/s against 842-876 for a 4-way K split of 64
-// 256x256 tiles, the estimate that tied at 0.76).
-constexpr double kEff128Deep = 0.80;
+// per CU than the 2-stage multi-round version the 0.76 was measured on.  Priced at 0.70: that
+// still picks it at 512 x 8192 x 8192 (867-919 TFLOP/s against 842-876 for a 4-way K split of 64
+// 256x256 tiles) and gives 448-512 x 4096 x 4096 to 256x128 tiles (measured with B rotating
+// through HBM 521 against 399 TFLOP/s at 512 rows, B resident +8%), which the earlier 0.80 put on
+// 128x128; no other pick of the measured sets changes.
+constexpr double kEff128Deep = 0.70;
 static double tile_cost(const GemmProblem& p, int tile, int* splits_out) {
   static const double eff_of[kTileCount] = {1.0, kEffNarrow, kEffNarrow, kEff128, kEff64, kEff192};
   const int bm = tile_bm(tile), bn = tile_bn(tile);
