@@ -406,10 +406,24 @@ __device__ __forceinline__ void ktile_last_step(const char LDS_AS* ns, const uin
 // 0 .. S-1 already (KT >= S).  pre = 2: as 1, and NST further vector-memory operations (the
 // previous tile's C stores) were issued after them; the first wait lets those stay
 // outstanding (vmcnt retires in issue order).
-template <class T, bool BKM, int NST = 0, class Prep, class DmaOne, class IssueTile>
+//
+// first_wait() runs once tile 0 has landed, before the barrier that publishes it;
+// tail_patch(slot) runs once this wave's loads of the last tile (in ring slot `slot`) have
+// landed, before the barrier that publishes it: a thread may overwrite the chunks its own
+// loads put there.
+struct NoHook {
+  __device__ __forceinline__ void operator()() const {}
+};
+struct NoSlotHook {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
+template <class T, bool BKM, int NST = 0, class Prep, class DmaOne, class IssueTile, class FirstWait = NoHook,
+          class TailPatch = NoSlotHook>
 __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool tail_regs, const uint32_t (&a_off)[kMaxOff],
                                             const uint32_t (&b_off)[kMaxOff], AccT<T> (&acc)[T::FM][T::FN], Prep&& prep,
-                                            DmaOne&& dma_one, IssueTile&& issue_tile, int pre = 0) {
+                                            DmaOne&& dma_one, IssueTile&& issue_tile, int pre = 0,
+                                            FirstWait&& first_wait = FirstWait{}, TailPatch&& tail_patch = TailPatch{}) {
   // Ring of S slots, tile u in slot u % S.  Cross-stage pipeline: during the last K-step of
   // tile t, this wave waits for its own loads of tile t+1, then the barrier (a) publishes
   // tile t+1 -- every wave's loads of it have landed -- and (b) retires slot t % S: every
@@ -429,6 +443,8 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
   } else {
     wait_tiles<T::LPT, S - 1>(first - 1 - ((tail_regs && first == KT) ? 1 : 0));
   }
+  first_wait();
+  if (KT == 1) tail_patch(0);
   block_sync();
   Frags<T> f[2];
   load_frags<T, BKM>(lds_base, lds_base + T::A_BYTES, a_off, b_off, 0, f[0]);
@@ -444,8 +460,9 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
     int ahead = issued - (t + 2);                // of those, after t+1 (may stay in flight)
     if (tail_regs && issued == KT && ahead > 0) --ahead;
     wait_tiles<T::LPT, (S > 2 ? S - 2 : 0)>(ahead);
-    block_sync();
     const int nslot = cur + 1 == S ? 0 : cur + 1;
+    if (t + 1 == KT - 1) tail_patch(nslot);
+    block_sync();
     const char LDS_AS* ns = lds_base + nslot * T::STAGE;
     load_frags<T, BKM>(ns, ns + T::A_BYTES, a_off, b_off, 0, f[0]);
     refill();
@@ -483,21 +500,36 @@ __device__ __forceinline__ void cross_stage(char LDS_AS* lds_base, int KT, bool 
   mfma_frags<T>(f[1], acc);
 }
 
-struct NoHook {
-  __device__ __forceinline__ void operator()() const {}
-};
-
-
 // GENERIC = false: direct-to-LDS buffer loads; needs 2-byte-aligned A and B and per-tile byte
 //                  offsets within 32 bits (dma_ok).  Rows that are not 16-byte aligned are read
-//                  by unaligned buffer loads; the last K tile of an unaligned problem is gathered
-//                  through VGPRs (tail_regs).
+//                  by unaligned buffer loads.  The last K tile of an unaligned problem
+//                  (tail_regs) is loaded like the others with its chunks across K (A) and
+//                  across N in B's last row patched from a copy gathered at the start, or,
+//                  for operands narrower than the tile (ldb < BN or lda < 8), gathered
+//                  through VGPRs.
 // GENERIC = true : element-wise masked loads through VGPRs; any shape and alignment.
 // CPOL: how C's 16-byte pieces are stored (CStore): plain, non-temporal or system-scope
 //       write-through (sc0 sc1); the last two for 16-byte-aligned C rows only (see launch_nn).
-template <class T, bool GENERIC, int CPOL = kStorePlain>
-__global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, int tiles_m, int tiles_n) {
+// TAIL: the direct-to-LDS kernel handles an unaligned last K tile (p.tail_regs); launches
+//       without one run the instantiation with TAIL = false, which carries none of that code.
+// Launch bounds: the 64x64 tile declares the three workgroups per CU its LDS ring allows.  With
+// one, the compiler kept that tile's accumulators in AGPRs and copied them to and from VGPRs
+// every K tile of the instantiation without the tail code (20 copies per 8 MFMAs; 1024^2 x 2048
+// ran 14.7 against 14.1 us); with three it keeps them in VGPRs.
+template <class T>
+constexpr int nn_launch_occupancy() {
+  return T::BM == 64 && T::BN == 64 ? 3 : T::OCC;
+}
+template <class T, bool GENERIC, int CPOL = kStorePlain, bool TAIL = true>
+__global__ __launch_bounds__(T::NT, nn_launch_occupancy<T>()) void gemm_nn_kernel(GemmProblem p, int tiles_m,
+                                                                                  int tiles_n) {
   __shared__ __attribute__((aligned(1024))) char lds[T::STAGES * T::STAGE];
+  // The last K tile's straddling chunks, gathered at the start: A's chunk across K of each
+  // tile row (entry = row in the tile), then B's chunk across N in row K-1 (entry BM).
+  constexpr int kSpare = TAIL && !GENERIC ? T::BM + 1 : 1;
+  __shared__ half8 tail_spare[kSpare];
+  static_assert(GENERIC || T::OCC * (T::STAGES * T::STAGE + kSpare * 16) <= 160 * 1024,
+                "LDS rings and the tail copy must fit the 160 KB LDS");
   record_clock(p.clk, 0);
 
   // K split (direct-to-LDS path only).  Blocks [0, whole) compute tiles 0 .. whole-1 of the
@@ -600,6 +632,20 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       for (int r = 0; r < T::RB; ++r) b_goffr[r] = (uint32_t)((b_row_of(r) * ldb + b_col_of(r)) * 2);
     }
 
+    // The last K tile of an unaligned problem (p.tail_regs: K or N not a multiple of 8, or rows
+    // not 16-byte aligned), in the block that holds it.  When B's rows are at least a tile wide
+    // and A's at least a chunk (dma_tail), no chunk of any tile reaches across a descriptor's
+    // range end other than two of the last tile: A's chunk across K in row M-1 and B's chunk
+    // across N in row K-1.  The last tile's ranges end before those two, so they read as zero
+    // like every chunk past the ends, and its chunks across K (every row of A: past K they hold
+    // the next row's values) and across N in B's row K-1 are overwritten from tail_spare before
+    // the tile is published (tail_fix).  Narrower operands gather the whole last tile through
+    // VGPRs instead (tail_regs).
+    const bool tail_block = TAIL && p.tail_regs && t_end == KT_all;
+    const bool dma_tail = ldb >= T::BN && lda >= 8;
+    const bool tail_regs = tail_block && !dma_tail;
+    const bool tail_fix = tail_block && dma_tail;
+
     // DMA of K tile t into ring slot `stage`: RA + RB buffer_load_dwordx4 ... lds per thread.
     // Each range ends at the operand's last element (row M-1, column K-1 of A; row K-1,
     // column N-1 of B), so nothing past the caller's data is ever fetched; rows past the end
@@ -645,16 +691,18 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
       for (int j = 0; j < T::LPT; ++j) dma_one(d, j);
     };
 
-    // The last K tile of an unaligned problem (K or N not a multiple of 8, or rows not
-    // 16-byte aligned) is gathered element by element through VGPRs into the same slot
-    // layout: its chunks may straddle K, N or the end of an operand, which the descriptor's
-    // range check cannot mask exactly.  Every earlier tile lies wholly inside both operands.
+    // tail_regs: the last K tile gathered element by element through VGPRs into the same slot
+    // layout.
     const _Float16* Ah = (const _Float16*)p.A;
     const _Float16* Bh = (const _Float16*)p.B;
     auto fill_regs = [&](int t, int stage) {
       const int k0 = (t_begin + t) * T::BK;
       char LDS_AS* a_dst = lds_base + stage * T::STAGE + (w * 64 + lane) * 16;
       char LDS_AS* b_dst = a_dst + T::A_BYTES;
+      // Element loads under lane conditions, one memory round trip each: this path serves
+      // operands narrower than the tile only, and it runs in the refill peeled off the K loop,
+      // where the registers that would keep a chunk's loads in flight together are not free
+      // (they spilled).
 #pragma unroll
       for (int r = 0; r < T::RA; ++r) {
         const int m = m0 + a_row0 + r * RPA, k = k0 + a_kc;
@@ -680,16 +728,105 @@ __global__ __launch_bounds__(T::NT, T::OCC) void gemm_nn_kernel(GemmProblem p, i
         *(half8 LDS_AS*)(b_dst + r * T::NT * 16) = v;
       }
     };
-    // only the block holding the globally last K tile gathers it
-    const bool tail_regs = p.tail_regs && t_end == KT_all;
-    auto issue_tile = [&](int t, int stage) {
-      if (tail_regs && t == KT - 1)
-        fill_regs(t, stage);
-      else
-        issue(t, stage);
+    // tail_fix: the chunk of the last K tile across K (column k0t + a_kcs .. +7 of each row of
+    // A, K % 8 of them valid) and across N in B's row K-1 (columns n0 + n_cs .. +7, N % 8
+    // valid), gathered here (their loads overlap the first tiles'), kept in tail_spare from
+    // the first tile's wait on, and copied over what the DMA put in their slots.  Thread
+    // (w, lane) owns the same chunks in every tile: its A chunks when its chunk column is
+    // a_kcs, and B slot r when that slot is row K-1, column n_cs.
+    const int k0t = (KT_all - 1) * T::BK;
+    const int a_kcs = (K - k0t) & ~7, n_cs = (N - n0) & ~7;
+    const bool a_fix = tail_fix && (K & 7) != 0 && a_kc == a_kcs;
+    // What the last tile needs, packed into one scalar that lives through the K loop: bit 0
+    // tail_fix, then K % 8, N % 8, a_kcs (< 64), K-1 as a row of the last tile (< 64) and n_cs
+    // clamped to BN (no chunk of the tile when the tile does not reach N).
+    const uint32_t tp = !TAIL ? 0u
+                              : __builtin_amdgcn_readfirstlane(
+                                    (uint32_t)tail_fix | (uint32_t)(K & 7) << 1 | (uint32_t)(N & 7) << 4 |
+                                    (uint32_t)a_kcs << 7 | (uint32_t)(K - 1 - k0t) << 13 |
+                                    (uint32_t)(n_cs < T::BN ? n_cs : T::BN) << 19);
+    // Both the gather and the store sit behind the scalar test of tp: the wait for the gathered
+    // registers (a full vmcnt drain, the compiler not seeing the DMA loads) must not reach the
+    // prologue of a launch without a patched tail.
+    half8 a_fixv[T::RA];
+    int b_fix_r = -1;
+    half8 b_fixv = {};
+    // Every lane loads (addresses clamped into the operands, values masked afterwards), so the
+    // loads carry no branches and go out together: a load under a lane condition is merged
+    // into its vector before the next one issues, one memory round trip each.
+    if (tp & 1) {
+      const int ka = K & 7, kb = N & 7;
+      if (ka != 0) {
+#pragma unroll
+        for (int r = 0; r < T::RA; ++r) {
+          const int m = m0 + a_row0 + r * RPA;
+          const _Float16* src = Ah + (int64_t)(m < M ? m : M - 1) * lda + k0t + a_kcs;
+          _Float16 x[7];
+#pragma unroll
+          for (int e = 0; e < 7; ++e) x[e] = src[e < ka ? e : ka - 1];  // columns below K
+          half8 v = {};
+#pragma unroll
+          for (int e = 0; e < 7; ++e) v[e] = (e < ka && m < M) ? x[e] : (_Float16)0;
+          a_fixv[r] = v;
+        }
+      }
+      if (kb != 0) {
+#pragma unroll
+        for (int r = 0; r < T::RB; ++r)
+          if (k0t + b_row_of(r) == K - 1 && b_col_of(r) == n_cs) b_fix_r = r;
+        const _Float16* src = Bh + (int64_t)(K - 1) * ldb;
+        const int c0 = n0 + n_cs;
+        _Float16 x[7];
+#pragma unroll
+        for (int e = 0; e < 7; ++e) x[e] = src[c0 + e < N ? c0 + e : N - 1];
+#pragma unroll
+        for (int e = 0; e < 7; ++e) b_fixv[e] = e < kb ? x[e] : (_Float16)0;
+      }
+    }
+    auto spare_store = [&] {
+      if (tp & 1) {
+        if (a_fix) {
+#pragma unroll
+          for (int r = 0; r < T::RA; ++r) tail_spare[a_row0 + r * RPA] = a_fixv[r];
+        }
+        if (b_fix_r >= 0) tail_spare[kSpare - 1] = b_fixv;  // entry BM
+      }
+    };
+    // At the last tile the lane-derived values are rebuilt from a fresh lane index rather than
+    // kept live through the K loop.
+    auto tail_patch = [&](int slot) {
+      if (!(tp & 1)) return;
+      const int ln = lane_id_fresh();
+      char LDS_AS* a_dst = lds_base + slot * T::STAGE + (w * 64 + ln) * 16;
+      const int row0 = w * (64 / T::CA) + ln / T::CA;
+      if ((tp >> 1 & 7) != 0 && 8 * ((ln % T::CA) ^ T::swz_a(row0)) == (int)(tp >> 7 & 63)) {
+#pragma unroll
+        for (int r = 0; r < T::RA; ++r) *(half8 LDS_AS*)(a_dst + r * T::NT * 16) = tail_spare[row0 + r * RPA];
+      }
+      if ((tp >> 4 & 7) != 0) {
+#pragma unroll
+        for (int r = 0; r < T::RB; ++r) {
+          const int sl = r * T::NT + w * 64 + ln;
+          const int row = sl / T::CB, col = 8 * ((sl % T::CB) ^ T::swz_bk(row));
+          if (row == (int)(tp >> 13 & 63) && col == (int)(tp >> 19))
+            *(half8 LDS_AS*)(a_dst + T::A_BYTES + r * T::NT * 16) = tail_spare[kSpare - 1];
+        }
+      }
     };
 
-    cross_stage<T, false>(lds_base, KT, tail_regs, a_off, b_off, acc, prep, dma_one, issue_tile);
+    // The last tile is issued by the prologue or by the refill peeled off the steady loop
+    // (cross_stage), never by the steady loop's own refill.
+    auto issue_tile = [&](int t, int stage) {
+      if (tail_regs && t == KT - 1) {
+        fill_regs(t, stage);
+      } else {
+        if ((tp & 1) && t == KT - 1) a_left -= (tp >> 1 & 7) * 2, b_left -= (tp >> 4 & 7) * 2;  // the cut ranges
+        issue(t, stage);
+      }
+    };
+
+    cross_stage<T, false>(lds_base, KT, tail_regs, a_off, b_off, acc, prep, dma_one, issue_tile, 0, spare_store,
+                          tail_patch);
   } else {
     static_assert(!GENERIC || T::STAGES == 2, "the register-staged path double-buffers");
     (void)t_begin;
@@ -1671,17 +1808,28 @@ static hipError_t launch_nn(const GemmProblem& p, hipStream_t stream) {
                   (c_lines_ok<T>() || (double)p.M * p.N * 4.0 > 32.0 * (1 << 20));
   // (Multi-round grids keep plain stores: non-temporal whole lines there measured -4.6% at
   // 5000^3, -1% at 4096^3 on 256x128, +7% at 8192^2 x 2048 on 256x128, +-0 elsewhere.)
-  if constexpr (!GENERIC && (c_lines_ok<T>() || (T::BM == 256 && T::BN == 256))) {
-    if (wt)
-      hipLaunchKernelGGL((gemm_nn_kernel<T, false, kStoreWriteThrough>), dim3((unsigned)blocks), dim3(T::NT), 0, stream,
-                         p, tiles_m, tiles_n);
+  // the direct-to-LDS kernel with or without the unaligned-tail code
+  auto launch_dma = [&](auto cpol) {
+    constexpr int CP = decltype(cpol)::value;
+    if (p.tail_regs)
+      hipLaunchKernelGGL((gemm_nn_kernel<T, false, CP, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p,
+                         tiles_m, tiles_n);
     else
-      hipLaunchKernelGGL((gemm_nn_kernel<T, false>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
-                         tiles_n);
+      hipLaunchKernelGGL((gemm_nn_kernel<T, false, CP, false>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p,
+                         tiles_m, tiles_n);
+  };
+  if constexpr (GENERIC) {
+    (void)wt;
+    (void)launch_dma;
+    hipLaunchKernelGGL((gemm_nn_kernel<T, true>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m, tiles_n);
+  } else if constexpr (c_lines_ok<T>() || (T::BM == 256 && T::BN == 256)) {
+    if (wt)
+      launch_dma(std::integral_constant<int, kStoreWriteThrough>{});
+    else
+      launch_dma(std::integral_constant<int, kStorePlain>{});
   } else {
     (void)wt;
-    hipLaunchKernelGGL((gemm_nn_kernel<T, GENERIC>), dim3((unsigned)blocks), dim3(T::NT), 0, stream, p, tiles_m,
-                       tiles_n);
+    launch_dma(std::integral_constant<int, kStorePlain>{});
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;

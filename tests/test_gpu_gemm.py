@@ -255,6 +255,40 @@ def test_exact_ragged_full_size(mm, cuda, tile):
     assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches"
 
 
+TAIL_PADDING = [
+    ((333, 517, 263, 5, 3), None),       # 64x64 tiles; chunks across K and across N in B's row K-1
+    ((333, 517, 263, 5, 3), "256x256"),  # the same through every tile shape
+    ((333, 517, 263, 5, 3), "192x192"),
+    ((333, 517, 263, 5, 3), "256x128"),
+    ((333, 517, 263, 5, 3), "128x256"),
+    ((333, 517, 263, 5, 3), "128x128"),
+    ((100, 300, 37, 3, 3), None),        # one K tile: the prologue publishes the patched tile
+    ((333, 520, 264, 3, 0), "256x256"),  # unaligned rows, K and N multiples of 8: nothing to patch
+    ((257, 129, 77, 5, 3), "256x256"),   # B rows narrower than the tile: gathered through VGPRs
+    ((333, 517, 8191, 5, 3), None),      # 128x128 tiles split 16 ways: the last split patches
+    ((1000, 777, 6151, 1, 1), None),     # a 4-way split of the partial last round
+]
+
+
+@pytest.mark.parametrize("case", TAIL_PADDING, ids=lambda c: "x".join(map(str, c[0])) + "-" + str(c[1]))
+def test_exact_tail_padding(mm, cuda, case):
+    """Rows of A and B padded past K and N with NaN (lda = K + pa, ldb = N + pb).  The last K
+    tile's chunks across K read that padding (or the next row) before the kernel overwrites them
+    from its gathered copy; a value left there would meet B's zero rows past K as NaN * 0.  The
+    chunks across N in B's padding only reach columns that are never stored.  Exact on integer
+    inputs."""
+    (M, N, K, pa, pb), tile = case
+    rng = np.random.default_rng(M + 5 * N + 11 * K)
+    A, B, truth = _int_inputs(rng, M, N, K)
+    Ap = np.full((M, K + pa), np.nan, dtype=np.float16)
+    Ap[:, :K] = A
+    Bp = np.full((K, N + pb), np.nan, dtype=np.float16)
+    Bp[:, :N] = B
+    Ad, Bd = to_dev(cuda, Ap), to_dev(cuda, Bp)
+    C = mm.gemm(Ad[:, :K], Bd[:, :N], tile=tile).cpu().numpy()
+    assert np.array_equal(C, truth), f"{int((C != truth).sum())} mismatches, {int(np.isnan(C).sum())} NaN"
+
+
 @pytest.mark.parametrize("shape", [(300, 270, 1001), (129, 65, 2055), (64, 4100, 515)], ids=lambda s: "x".join(map(str, s)))
 def test_exact_unaligned_rows(mm, cuda, shape):
     """Odd leading dimensions across many K tiles (unaligned direct-to-LDS rows)."""
