@@ -1929,7 +1929,8 @@ static bool dma_ok(const GemmProblem& p, int bm) {
 }
 
 // True when every DMA chunk of the last K tile also lies wholly inside the operands (K and
-// N multiples of 8, 16-byte aligned rows); otherwise that tile is gathered through VGPRs.
+// N multiples of 8, 16-byte aligned rows); otherwise gemm_nn_kernel patches that tile's
+// straddling chunks or gathers it through VGPRs, and the persistent kernels do not run.
 static bool tail_aligned(const GemmProblem& p) {
   const uintptr_t a = (uintptr_t)p.A, b = (uintptr_t)p.B;
   return !((a & 15) || (b & 15) || p.lda % 8 || p.ldb % 8 || p.K % 8 || p.N % 8);
@@ -1982,7 +1983,7 @@ size_t gemm_nn_workspace_bytes(const GemmProblem& p, int tile_id) {
 }
 
 // The persistent kernel's conditions: whole interior tiles (256x256, or 192x192 without a K
-// split) over more than one round of 256 workgroups, aligned operands (no gathered K tile),
+// split) over more than one round of 256 workgroups, aligned operands (no masked last K tile),
 // 4-byte-aligned C, and at least S + 1 K tiles.  Measured against one workgroup per tile (same
 // box): 8192^3 +1%, 8192^2 x 2048 +3.7%, 16384 x 8192 x 1024 +3.8%; 192x192 at 6144^2 x 2048 +4%.
 template <class TP = DmaTile<256, 256>>

@@ -16,7 +16,8 @@ struct GemmProblem {
   int M, N, K;
   int64_t lda, ldb, ldc;
   bool c_vec4;     // set by the launcher: C 4-byte aligned (16-byte stores of C rows allowed)
-  bool tail_regs;  // set by the launcher: gather the last K tile through VGPRs
+  bool tail_regs;  // set by the launcher: the last K tile needs masking (K or N not a multiple
+                   // of 8, or rows not 16-byte aligned): patched chunks or a VGPR gather
   int k_splits;    // tile kernel: K ranges computed by separate workgroups (<= 1: none)
   int split_tiles; // k_splits > 1: the last split_tiles tiles in dispatch order are split
   float* partials; // k_splits > 1: [split tile][split][BM][BN] fp32 partial tiles

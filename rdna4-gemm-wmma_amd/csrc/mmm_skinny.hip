@@ -102,29 +102,42 @@ __device__ __forceinline__ void stream_columns(const GemmProblem& p, int n0, int
   // is all the gathered slot needs.
   const _Float16* Ah = (const _Float16*)p.A;
   const _Float16* Bh = (const _Float16*)p.B;
+  // Every element is loaded from an address clamped into its operand and masked afterwards, all
+  // loads before any store: a load under a lane condition would be merged into its vector before
+  // the next one issued, one memory round trip per element.
   auto gather = [&](int s, int slot) {
     const int k0 = (s_begin + s) * kKS;
     char LDS_AS* dst = ring + slot * kSlot + lane * 16;
+    constexpr int NB = kBBytes / 1024;
+    _Float16 xa[NA][8], xb[NB][8];
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int row = a_row + i * RPI_A, k = k0 + a_kc[i];
-      half8 v = {};
-      if (row < M) {
+      const _Float16* src = Ah + (int64_t)(row < M ? row : M - 1) * lda;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (k + e < K) v[e] = Ah[(int64_t)row * lda + k + e];
-      }
+      for (int e = 0; e < 8; ++e) xa[i][e] = src[k + e < K ? k + e : K - 1];
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int k = k0 + i * (64 / kCPR) + lane / kCPR, n = n0 + 8 * ((lane % kCPR) ^ b_sw);
+      const _Float16* src = Bh + (int64_t)(k < K ? k : K - 1) * ldb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xb[i][e] = src[n + e < N ? n + e : N - 1];
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int row = a_row + i * RPI_A, k = k0 + a_kc[i];
+      half8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (row < M && k + e < K) ? xa[i][e] : (_Float16)0;
       *(half8 LDS_AS*)(dst + i * 1024) = v;
     }
 #pragma unroll
-    for (int i = 0; i < kBBytes / 1024; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const int k = k0 + i * (64 / kCPR) + lane / kCPR, n = n0 + 8 * ((lane % kCPR) ^ b_sw);
-      half8 v = {};
-      if (k < K) {
+      half8 v;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (n + e < N) v[e] = Bh[(int64_t)k * ldb + n + e];
-      }
+      for (int e = 0; e < 8; ++e) v[e] = (k < K && n + e < N) ? xb[i][e] : (_Float16)0;
       *(half8 LDS_AS*)(dst + kABytes + i * 1024) = v;
     }
   };
@@ -381,29 +394,34 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
   // globally last K slot of an unaligned problem: gathered element by element (same layout)
   const _Float16* Ah = (const _Float16*)p.A;
   const _Float16* Bh = (const _Float16*)p.B;
+  // Clamped addresses, masked values, a chunk's loads before its store: no load sits under a lane
+  // condition (that would cost a memory round trip per element).  Chunk by chunk, as the widest
+  // instantiations have no registers for more loads in flight.
   auto gather = [&](int s, int slot) {
     const int k0 = (s_begin + s) * KS;
     char LDS_AS* dst = ring + slot * SLOT + lane * 16;
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const int row = a_row + i * RPI_A, k = k0 + a_kc[i];
-      half8 v = {};
-      if (row < M) {
+      const _Float16* src = Ah + (int64_t)(row < M ? row : M - 1) * lda;
+      _Float16 x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (k + e < K) v[e] = Ah[(int64_t)row * lda + k + e];
-      }
+      for (int e = 0; e < 8; ++e) x[e] = src[k + e < K ? k + e : K - 1];
+      half8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (row < M && k + e < K) ? x[e] : (_Float16)0;
       *(half8 LDS_AS*)(dst + i * 1024) = v;
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int k = k0 + i * RPI + b_row, n = n0 + b_nc[W::phase(i)];
-      half8 v = {};
-      if (k < K) {
+      const _Float16* src = Bh + (int64_t)(k < K ? k : K - 1) * ldb;
+      _Float16 x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (n + e < N) v[e] = Bh[(int64_t)k * ldb + n + e];
-      }
+      for (int e = 0; e < 8; ++e) x[e] = src[n + e < N ? n + e : N - 1];
+      half8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (k < K && n + e < N) ? x[e] : (_Float16)0;
       *(half8 LDS_AS*)(dst + ABYTES + i * 1024) = v;
     }
   };

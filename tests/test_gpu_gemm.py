@@ -178,7 +178,7 @@ def test_config5_skinny_full(orc, mm, cuda):
 EXACT_SHAPES = [
     (256, 256, 256),   # aligned, direct-to-LDS path, one tile
     (300, 264, 200),   # direct-to-LDS path with M/N edge tiles, K tail of 8
-    (257, 129, 77),    # odd K and N: gathered last K tile
+    (257, 129, 77),    # odd K and N: masked last K tile
     (513, 1000, 1032), # several tiles, K tail 8
     (33, 40, 16),      # smaller than one tile
     (1, 1, 1),
@@ -197,8 +197,9 @@ def test_exact_integer(mm, cuda, shape):
 @pytest.mark.parametrize("tile", ["256x256", "128x256", "256x128", "128x128", "64x64", "192x192"])
 @pytest.mark.parametrize("K", [264, 263])
 def test_exact_every_tile(mm, cuda, tile, K):
-    """Every instantiated tile, with whole K tiles (K=264) and a last K tile gathered through VGPRs
-    (K=263, odd N): the direct-to-LDS path (the register-staged one has its own test)."""
+    """Every instantiated tile, with whole K tiles (K=264) and a last K tile whose chunks across K
+    and N are patched (K=263, odd N): the direct-to-LDS path (the register-staged one has its own
+    test)."""
     M, N = 333, (520 if K % 8 == 0 else 517)
     rng = np.random.default_rng(K)
     A, B, truth = _int_inputs(rng, M, N, K)
@@ -244,8 +245,8 @@ def test_exact_register_staged_path(mm, cuda, tile):
 @pytest.mark.parametrize("tile", [None, "128x128"])
 def test_exact_ragged_full_size(mm, cuda, tile):
     """The ragged configuration's shape with integer inputs: every output bit-exact.  Rows of
-    A and B are only 2-byte aligned (unaligned direct-to-LDS loads) and the last K tile is
-    gathered through VGPRs.  fp64 BLAS is exact here (all partial sums below 2^53)."""
+    A and B are only 2-byte aligned (unaligned direct-to-LDS loads) and the last K tile's chunks
+    across K and N are patched.  fp64 BLAS is exact here (all partial sums below 2^53)."""
     M, N, K = 4097, 4095, 4111
     rng = np.random.default_rng(4111)
     A = rng.integers(-4, 5, size=(M, K)).astype(np.float16)
@@ -532,7 +533,7 @@ def test_tile_graph_capture(mm, cuda, shape):
 
 
 # shapes whose launch splits K: streaming (16 and 40 rows), one small round of tiles, a partly
-# filled last round (with a gathered K tail), and the 128x128 tile
+# filled last round (with a masked K tail), and the 128x128 tile
 WS_SHAPES = [(16, 8192, 2048), (40, 4096, 4096), (1024, 1024, 8192), (4357, 4095, 8191), (300, 264, 4096)]
 
 
@@ -602,7 +603,7 @@ TAIL_SPLITS = [((6144, 6144, 4096), ("256x256", 4, 64)), ((1792, 5120, 8192), ("
                          ids=lambda s: "x".join(map(str, s)))
 def test_exact_192_full_round(mm, cuda, shape):
     """Shapes the library runs as one round of 192x192 tiles (16 x 16 of them at 3072^2; edges
-    and a gathered K tail in the last case): exact against the on-device fp64 truth."""
+    and a masked K tail in the last case): exact against the on-device fp64 truth."""
     M, N, K = shape
     plan = mm.gemm_plan(M, N, K)
     assert (plan["kernel"], plan["block_m"], plan["block_n"], plan["tile_splits"]) == ("tile", 192, 192, 1)
@@ -643,7 +644,7 @@ TILE_SPLITS = [((1024, 1024, 8192, None), 4), ((65, 4096, 4096, None), 8), ((300
 
 @pytest.mark.parametrize("case", TILE_SPLITS, ids=lambda c: "x".join(map(str, c[0][:3])) + f"-{c[0][3]}-s{c[1]}")
 def test_exact_tile_splits(mm, cuda, case):
-    """K split across workgroups on every tile (and with a gathered last K tile): exact."""
+    """K split across workgroups on every tile (and with a masked last K tile): exact."""
     (M, N, K, tile), splits = case
     if tile is None:
         assert mm.gemm_plan(M, N, K)["tile_splits"] == splits
