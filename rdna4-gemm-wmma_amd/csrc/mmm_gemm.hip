@@ -46,6 +46,12 @@ namespace mmm {
 // Fragment offsets a wave keeps per K-step (A) or per B fragment: at most kMaxOff of each.
 constexpr int kMaxOff = 8;
 
+// Eight zero halves in global memory, never written.  The element gathers of the register-staged
+// kernels load an element past an operand's edge from here instead of masking the loaded value:
+// a value that a later select may discard lets the compiler sink its load into a branch of its
+// own, whose wait then holds back every load after it (one memory round trip per element).
+__device__ __attribute__((aligned(16))) _Float16 kZeroHalves[8];
+
 // Block tile BM x BN, K step BK (32 or 64), WGM x WGN waves, STAGES-deep LDS ring, OCC
 // workgroups per CU targeted by the launch bounds (OCC > 1 caps registers accordingly), MFMA
 // shape MF: 32 = v_mfma_f32_32x32x16_f16, 16 = v_mfma_f32_16x16x32_f16 (same MACs per LDS byte;
@@ -836,27 +842,24 @@ __global__ __launch_bounds__(T::NT, nn_launch_occupancy<T>()) void gemm_nn_kerne
     auto load = [&](int t) {
       const int k0 = t * T::BK;
 #pragma unroll
+      // Elements past the operands load from kZeroHalves: no load sits under a lane condition,
+      // so a stage's loads go out together (a conditional load is merged into its vector before
+      // the next one issues).
       for (int r = 0; r < T::RA; ++r) {
         const int m = m0 + a_row0 + r * RPA, k = k0 + a_kc;
-        half8 v = {};
-        if (m < M) {
-          const _Float16* src = A + (int64_t)m * lda + k;
+        const _Float16* src = A + (int64_t)m * lda + k;
+        half8 v;
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (k + e < K) v[e] = src[e];
-        }
+        for (int e = 0; e < 8; ++e) v[e] = *(m < M && k + e < K ? src + e : kZeroHalves);
         ra[r] = __builtin_bit_cast(u32x4, v);
       }
 #pragma unroll
       for (int r = 0; r < T::RB; ++r) {
         const int k = k0 + b_row0 + r * RPB, n = n0 + b_nc;
-        half8 v = {};
-        if (k < K) {
-          const _Float16* src = B + (int64_t)k * ldb + n;
+        const _Float16* src = B + (int64_t)k * ldb + n;
+        half8 v;
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (n + e < N) v[e] = src[e];
-        }
+        for (int e = 0; e < 8; ++e) v[e] = *(k < K && n + e < N ? src + e : kZeroHalves);
         rb[r] = __builtin_bit_cast(u32x4, v);
       }
     };
@@ -1332,16 +1335,16 @@ __device__ __forceinline__ int64_t fold_off(int i, int lo, int64_t s_hi, int64_t
 
 // X at the 8 consecutive fold indices i .. i+7 past base (index j at base + fold_off(j, ...)),
 // with one division for i and the rest stepped (the low sub-index carrying into the high one);
-// indices at or past `end` read as zero and are not dereferenced.
+// indices at or past `end` read as zero, from kZeroHalves (end = 0: all of them).
 __device__ __forceinline__ half8 gather8(const _Float16* X, int64_t base, int i, int end, int lo, int64_t s_hi,
                                          int64_t s_lo) {
-  half8 v = {};
+  half8 v;
   int l = i % lo;
   int64_t off = base + (int64_t)(i / lo) * s_hi + (int64_t)l * s_lo;
   const int64_t carry = s_hi - (int64_t)lo * s_lo;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    if (i + e < end) v[e] = X[off];
+    v[e] = *(i + e < end ? X + off : kZeroHalves);
     off += s_lo;
     if (++l == lo) l = 0, off += carry;
   }
@@ -1350,20 +1353,19 @@ __device__ __forceinline__ half8 gather8(const _Float16* X, int64_t base, int i,
 
 // gather8 for a contiguous low sub-index (s_lo == 1) whose extent, high stride and row bases are
 // multiples of G, with X + base 2G-byte aligned: groups of G elements never cross a block, so each
-// is one 2G-byte load (end is then a multiple of G too: a group is wholly in or out).
+// is one 2G-byte load (end is then a multiple of G too: a group is wholly in or out).  A group
+// past `end` loads zeros from kZeroHalves, as in gather8.
 template <int G>
 __device__ __forceinline__ half8 gather8_vec(const _Float16* X, int64_t base, int i, int end, int lo, int64_t s_hi) {
   typedef _Float16 halfG __attribute__((ext_vector_type(G)));
-  half8 v = {};
+  half8 v;
   int l = i % lo;
   int64_t off = base + (int64_t)(i / lo) * s_hi + l;
 #pragma unroll
   for (int j = 0; j < 8 / G; ++j) {
-    if (i + j * G < end) {
-      const halfG g = *(const halfG*)(X + off);
+    const halfG g = *(const halfG*)(i + j * G < end ? X + off : kZeroHalves);
 #pragma unroll
-      for (int e = 0; e < G; ++e) v[j * G + e] = g[e];
-    }
+    for (int e = 0; e < G; ++e) v[j * G + e] = g[e];
     off += G, l += G;
     if (l == lo) l = 0, off += s_hi - lo;
   }
@@ -1380,13 +1382,29 @@ __device__ __forceinline__ int gather_width(const void* X, int lo, int64_t s_hi,
   return 1;
 }
 
-// gather8 at the widest group width gw (uniform: the branch is scalar).
-__device__ __forceinline__ half8 gather8_w(int gw, const _Float16* X, int64_t base, int i, int end, int lo, int64_t s_hi,
+// gather8 at group width G (1: element by element through the strides).
+template <int G>
+__device__ __forceinline__ half8 gather8_g(const _Float16* X, int64_t base, int i, int end, int lo, int64_t s_hi,
                                            int64_t s_lo) {
-  if (gw == 8) return gather8_vec<8>(X, base, i, end, lo, s_hi);
-  if (gw == 4) return gather8_vec<4>(X, base, i, end, lo, s_hi);
-  if (gw == 2) return gather8_vec<2>(X, base, i, end, lo, s_hi);
-  return gather8(X, base, i, end, lo, s_hi, s_lo);
+  if constexpr (G == 1)
+    return gather8(X, base, i, end, lo, s_hi, s_lo);
+  else
+    return gather8_vec<G>(X, base, i, end, lo, s_hi);
+}
+
+// f(std::integral_constant<int, gw>) for a uniform group width gw: the branch is scalar and is taken
+// once per operand and stage, so each arm holds all of that operand's loads of the stage, which go
+// out together (a branch per chunk kept each chunk's loads waiting in their own arm).
+template <class F>
+__device__ __forceinline__ void with_width(int gw, F&& f) {
+  if (gw == 8)
+    f(std::integral_constant<int, 8>{});
+  else if (gw == 4)
+    f(std::integral_constant<int, 4>{});
+  else if (gw == 2)
+    f(std::integral_constant<int, 2>{});
+  else
+    f(std::integral_constant<int, 1>{});
 }
 
 template <class T, bool BKM>
@@ -1469,25 +1487,32 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_fold_kernel(FoldProblem p, int 
   u32x4 ra[T::RA], rb[RBK];
   auto load = [&](int t) {
     const int k0 = t * T::BK;
+    // Rows, columns and K rows past the operands gather with end = 0 (every element from
+    // kZeroHalves): no load sits under a lane condition.
+    with_width(a_gw, [&](auto g) {
+      constexpr int G = decltype(g)::value;
 #pragma unroll
-    for (int r = 0; r < T::RA; ++r) {
-      const int k = k0 + a_kc[r];
-      half8 v = {};
-      if (m0 + a_row[r] < M) v = gather8_w(a_gw, A, a_base[r], k, K, p.k_lo, p.ak[0], p.ak[1]);
-      ra[r] = __builtin_bit_cast(u32x4, v);
-    }
-#pragma unroll
-    for (int r = 0; r < RBK; ++r) {
-      half8 v = {};
-      if constexpr (BKM) {
-        const int k = k0 + b_c[r];
-        if (n0 + b_row[r] < N) v = gather8_w(b_gw, B, b_base[r], k, K, p.k_lo, p.bk[0], p.bk[1]);
-      } else {
-        const int k = k0 + b_row[r], n = n0 + b_c[r];
-        if (k < K) v = gather8_w(b_gw, B, fold_off(k, p.k_lo, p.bk[0], p.bk[1]), n, N, p.n_lo, p.bn[0], p.bn[1]);
+      for (int r = 0; r < T::RA; ++r) {
+        const int k = k0 + a_kc[r];
+        ra[r] = __builtin_bit_cast(
+            u32x4, gather8_g<G>(A, a_base[r], k, m0 + a_row[r] < M ? K : 0, p.k_lo, p.ak[0], p.ak[1]));
       }
-      rb[r] = __builtin_bit_cast(u32x4, v);
-    }
+    });
+    with_width(b_gw, [&](auto g) {
+      constexpr int G = decltype(g)::value;
+#pragma unroll
+      for (int r = 0; r < RBK; ++r) {
+        if constexpr (BKM) {
+          const int k = k0 + b_c[r];
+          rb[r] = __builtin_bit_cast(
+              u32x4, gather8_g<G>(B, b_base[r], k, n0 + b_row[r] < N ? K : 0, p.k_lo, p.bk[0], p.bk[1]));
+        } else {
+          const int k = k0 + b_row[r], n = n0 + b_c[r];
+          rb[r] = __builtin_bit_cast(u32x4, gather8_g<G>(B, fold_off(k < K ? k : 0, p.k_lo, p.bk[0], p.bk[1]), n,
+                                                         k < K ? N : 0, p.n_lo, p.bn[0], p.bn[1]));
+        }
+      }
+    });
   };
   char LDS_AS* lds_base = (char LDS_AS*)lds;
   auto store = [&](int stage) {
