@@ -744,12 +744,15 @@ __global__ __launch_bounds__(T::NT, nn_launch_occupancy<T>()) void gemm_nn_kerne
     const int a_kcs = (K - k0t) & ~7, n_cs = (N - n0) & ~7;
     const bool a_fix = tail_fix && (K & 7) != 0 && a_kc == a_kcs;
     // What the last tile needs, packed into one scalar that lives through the K loop: bit 0
-    // tail_fix, then K % 8, N % 8, a_kcs (< 64), K-1 as a row of the last tile (< 64) and n_cs
-    // clamped to BN (no chunk of the tile when the tile does not reach N).
+    // tail_fix, then K % 8, N % 8, a_kcs (6 bits), K-1 as a row of the last tile (< 64) and n_cs
+    // clamped to BN (no chunk of the tile when the tile does not reach N).  a_kcs is used only
+    // when K % 8 != 0, where it is at most 56; with K a multiple of 64 it is 64 and is masked to
+    // keep it out of the row field (whose low bit it would otherwise set: that field is then 63,
+    // so the OR changed nothing, but the mask does not rely on that).
     const uint32_t tp = !TAIL ? 0u
                               : __builtin_amdgcn_readfirstlane(
                                     (uint32_t)tail_fix | (uint32_t)(K & 7) << 1 | (uint32_t)(N & 7) << 4 |
-                                    (uint32_t)a_kcs << 7 | (uint32_t)(K - 1 - k0t) << 13 |
+                                    (uint32_t)(a_kcs & 63) << 7 | (uint32_t)(K - 1 - k0t) << 13 |
                                     (uint32_t)(n_cs < T::BN ? n_cs : T::BN) << 19);
     // Both the gather and the store sit behind the scalar test of tp: the wait for the gathered
     // registers (a full vmcnt drain, the compiler not seeing the DMA loads) must not reach the

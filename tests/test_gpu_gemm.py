@@ -265,6 +265,9 @@ TAIL_PADDING = [
     ((333, 517, 263, 5, 3), "128x128"),
     ((100, 300, 37, 3, 3), None),        # one K tile: the prologue publishes the patched tile
     ((333, 520, 264, 3, 0), "256x256"),  # unaligned rows, K and N multiples of 8: nothing to patch
+    ((333, 517, 256, 3, 3), None),       # K a multiple of 64 (last tile full), B's chunk across N
+    ((333, 517, 256, 3, 3), "256x256"),
+    ((300, 1023, 1024, 0, 1), "192x192"),
     ((257, 129, 77, 5, 3), "256x256"),   # B rows narrower than the tile: gathered through VGPRs
     ((333, 517, 8191, 5, 3), None),      # 128x128 tiles split 16 ways: the last split patches
     ((1000, 777, 6151, 1, 1), None),     # a 4-way split of the partial last round
