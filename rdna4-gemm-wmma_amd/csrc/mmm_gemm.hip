@@ -708,7 +708,8 @@ __global__ __launch_bounds__(T::NT, nn_launch_occupancy<T>()) void gemm_nn_kerne
       // Element loads under lane conditions, one memory round trip each: this path serves
       // operands narrower than the tile only, and it runs in the refill peeled off the K loop,
       // where the registers that would keep a chunk's loads in flight together are not free
-      // (they spilled).
+      // (the 256x256 tile spilled; on the 64x64 tile, where they fit, the extra registers cost
+      // its patched-tail launches 0.2-0.3 us per call, more than the gather gained).
 #pragma unroll
       for (int r = 0; r < T::RA; ++r) {
         const int m = m0 + a_row0 + r * RPA, k = k0 + a_kc;

@@ -269,6 +269,8 @@ TAIL_PADDING = [
     ((333, 517, 256, 3, 3), "256x256"),
     ((300, 1023, 1024, 0, 1), "192x192"),
     ((257, 129, 77, 5, 3), "256x256"),   # B rows narrower than the tile: gathered through VGPRs
+    ((300, 40, 77, 5, 3), "64x64"),      # the same on the 64x64 tile (its loads go out together)
+    ((2000, 40, 4097, 1, 1), None),      # ... with the K split of a small grid
     ((333, 517, 8191, 5, 3), None),      # 128x128 tiles split 16 ways: the last split patches
     ((1000, 777, 6151, 1, 1), None),     # a 4-way split of the partial last round
 ]
