@@ -22,6 +22,12 @@ constexpr int kRsrcWord3 = 0x00020000;
 // Byte offset used for masked-off chunks; every descriptor's range is clipped below it.
 constexpr uint32_t kOobOffset = 0x7ffffff0u;
 
+// Eight zero halves in global memory (one copy per source file), never written.  The element
+// gathers load an element past an operand's edge from here instead of masking the loaded value:
+// a value that a later select may discard lets the compiler sink its load into a branch of its
+// own, whose wait then holds back every load after it (one memory round trip per element).
+static __device__ __attribute__((aligned(16))) _Float16 kZeroHalves[8];
+
 // Raw buffer descriptor (base, num_records bytes, word 3) built from uniform values.
 __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t num_records) {
   const uint64_t b = (uint64_t)(uintptr_t)base;

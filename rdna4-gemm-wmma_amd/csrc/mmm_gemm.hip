@@ -46,11 +46,6 @@ namespace mmm {
 // Fragment offsets a wave keeps per K-step (A) or per B fragment: at most kMaxOff of each.
 constexpr int kMaxOff = 8;
 
-// Eight zero halves in global memory, never written.  The element gathers of the register-staged
-// kernels load an element past an operand's edge from here instead of masking the loaded value:
-// a value that a later select may discard lets the compiler sink its load into a branch of its
-// own, whose wait then holds back every load after it (one memory round trip per element).
-__device__ __attribute__((aligned(16))) _Float16 kZeroHalves[8];
 
 // Block tile BM x BN, K step BK (32 or 64), WGM x WGN waves, STAGES-deep LDS ring, OCC
 // workgroups per CU targeted by the launch bounds (OCC > 1 caps registers accordingly), MFMA

@@ -394,35 +394,61 @@ __global__ __launch_bounds__(256, 1) void gemm_stream_wide_kernel(GemmProblem p,
   // globally last K slot of an unaligned problem: gathered element by element (same layout)
   const _Float16* Ah = (const _Float16*)p.A;
   const _Float16* Bh = (const _Float16*)p.B;
-  // Clamped addresses, masked values, a chunk's loads before its store: no load sits under a lane
-  // condition (that would cost a memory round trip per element).  Chunk by chunk, as the widest
-  // instantiations have no registers for more loads in flight.
+  // No load sits under a lane condition (that would cost a memory round trip per element).
+  // Elements past the operands load from kZeroHalves, and every load is issued before the first
+  // store, so the compiler keeps as many in flight as the registers allow.  The 4 x 16-row
+  // instantiations clamp their addresses into the operands instead, mask the values, and store
+  // each chunk after its own eight loads: the 256-column one, already at 512 registers, spilled
+  // with the other form, and the 128-column one's K loop then copied its accumulators between
+  // AGPRs and VGPRs (144 copies per iteration against 20).
   auto gather = [&](int s, int slot) {
     const int k0 = (s_begin + s) * KS;
     char LDS_AS* dst = ring + slot * SLOT + lane * 16;
+    if constexpr (MR == 4) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int row = a_row + i * RPI_A, k = k0 + a_kc[i];
-      const _Float16* src = Ah + (int64_t)(row < M ? row : M - 1) * lda;
-      _Float16 x[8];
+      for (int i = 0; i < NA; ++i) {
+        const int row = a_row + i * RPI_A, k = k0 + a_kc[i];
+        const _Float16* src = Ah + (int64_t)(row < M ? row : M - 1) * lda;
+        _Float16 x[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = src[k + e < K ? k + e : K - 1];
-      half8 v;
+        for (int e = 0; e < 8; ++e) x[e] = src[k + e < K ? k + e : K - 1];
+        half8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (row < M && k + e < K) ? x[e] : (_Float16)0;
-      *(half8 LDS_AS*)(dst + i * 1024) = v;
-    }
+        for (int e = 0; e < 8; ++e) v[e] = (row < M && k + e < K) ? x[e] : (_Float16)0;
+        *(half8 LDS_AS*)(dst + i * 1024) = v;
+      }
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const int k = k0 + i * RPI + b_row, n = n0 + b_nc[W::phase(i)];
-      const _Float16* src = Bh + (int64_t)(k < K ? k : K - 1) * ldb;
-      _Float16 x[8];
+      for (int i = 0; i < NB; ++i) {
+        const int k = k0 + i * RPI + b_row, n = n0 + b_nc[W::phase(i)];
+        const _Float16* src = Bh + (int64_t)(k < K ? k : K - 1) * ldb;
+        _Float16 x[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = src[n + e < N ? n + e : N - 1];
-      half8 v;
+        for (int e = 0; e < 8; ++e) x[e] = src[n + e < N ? n + e : N - 1];
+        half8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (k < K && n + e < N) ? x[e] : (_Float16)0;
-      *(half8 LDS_AS*)(dst + ABYTES + i * 1024) = v;
+        for (int e = 0; e < 8; ++e) v[e] = (k < K && n + e < N) ? x[e] : (_Float16)0;
+        *(half8 LDS_AS*)(dst + ABYTES + i * 1024) = v;
+      }
+    } else {
+      half8 va[NA], vb[NB];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int row = a_row + i * RPI_A, k = k0 + a_kc[i];
+        const _Float16* src = Ah + (int64_t)row * lda + k;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) va[i][e] = *(row < M && k + e < K ? src + e : kZeroHalves);
+      }
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int k = k0 + i * RPI + b_row, n = n0 + b_nc[W::phase(i)];
+        const _Float16* src = Bh + (int64_t)k * ldb + n;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vb[i][e] = *(k < K && n + e < N ? src + e : kZeroHalves);
+      }
+#pragma unroll
+      for (int i = 0; i < NA; ++i) *(half8 LDS_AS*)(dst + i * 1024) = va[i];
+#pragma unroll
+      for (int i = 0; i < NB; ++i) *(half8 LDS_AS*)(dst + ABYTES + i * 1024) = vb[i];
     }
   };
   const bool gather_last = p.tail_regs && s_end == nst_all && nst > 0;
